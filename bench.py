@@ -1,0 +1,251 @@
+"""Benchmark of the fused 2D FNO spectral block on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload c2]
+
+Workload (default): the 256^2 Navier-Stokes-like block
+    y = GELU(SpectralConv(x) + Ws x),  x [32, 64, 256, 256] fp32 Gaussian random
+    field, n_modes (64, 64) -> 64 rows x 33 rfft columns, dense complex weight
+    W [64, 64, 64, 33] (re/im ~ N(0, 1/4096)), 1x1 skip Ws [64, 64] ~ N(0, 1/64),
+    bias 0, exact erf GELU.
+One step = one call of the block on one batch already resident in HBM.
+
+Prints ONE JSON line: value = achieved algorithmic HBM bandwidth (read x once,
+write y once, read W/Ws/bias once) over the timed steps, in GB/s; plus
+us_per_call, the roofline of the block, the torch.fft + einsum ROCm path
+timed on the same GPU, and the CPU baseline (the oracle restatement on the
+host cores, bounded sample).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import torch
+import torch.nn.functional as F
+
+HBM_PEAK_GBS = 8000.0
+
+WORKLOADS = {
+    # name: (B, C, H, W, n_modes)
+    "c2": (32, 64, 256, 256, (64, 64)),
+    "c2_32": (32, 64, 256, 256, (32, 32)),
+    "c1": (32, 64, 128, 128, (32, 32)),
+}
+
+
+def algorithmic_bytes(B, C, H, W, m1, m2h):
+    x = B * C * H * W * 4
+    w = C * C * m1 * m2h * 8
+    return 2 * x + w + C * C * 4 + C * 4
+
+
+def make_inputs(B, C, H, W, nm, device):
+    from neuraloperator_amd.synthetic import gaussian_random_field
+    m1, m2h = nm[0], nm[1] // 2 + 1
+    x = gaussian_random_field((B, C, H, W), seed=2024, device=device)
+    g = torch.Generator().manual_seed(7)
+    w = torch.complex(torch.randn(C, C, m1, m2h, generator=g),
+                      torch.randn(C, C, m1, m2h, generator=g)) / 64.0
+    ws = torch.randn(C, C, generator=g) / 8.0
+    bias = torch.zeros(C)
+    return x, w.to(device), ws.to(device), bias.to(device), (m1, m2h)
+
+
+def torch_rocm_block(x, w, bias, ws, m1, m2h):
+    """The reference op sequence (rfftn, fftshift, window, einsum, ifftshift,
+    ifftn, Hermitian fix-up, irfft, bias) + skip + GELU in torch on the GPU."""
+    B, C, H, W = x.shape
+    X = torch.fft.fftshift(torch.fft.rfftn(x, norm="forward", dim=(-2, -1)), dim=(-2,))
+    out = torch.zeros(B, w.shape[1], H, W // 2 + 1, dtype=torch.complex64, device=x.device)
+    r0 = H // 2 - m1 // 2
+    out[:, :, r0:r0 + m1, :m2h] = torch.einsum("bixy,ioxy->boxy", X[:, :, r0:r0 + m1, :m2h], w)
+    out = torch.fft.ifftn(torch.fft.ifftshift(out, dim=(-2,)), s=(H,), dim=(-2,), norm="forward")
+    out[..., 0].imag.zero_()
+    out[..., -1].imag.zero_()
+    y = torch.fft.irfft(out, n=W, dim=-1, norm="forward") + bias.view(1, -1, 1, 1)
+    y = y + torch.einsum("oi,bihw->bohw", ws, x)
+    return F.gelu(y)
+
+
+def event_times(fn, iters, stream, flush=None):
+    """Per-call durations (ms) with HIP events on ``stream``; optional cache
+    flush between calls, outside the timed interval."""
+    out = []
+    for _ in range(iters):
+        if flush is not None:
+            flush()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        fn()
+        e1.record(stream)
+        e1.synchronize()
+        out.append(e0.elapsed_time(e1))
+    return out
+
+
+def cpu_baseline(B, C, H, W, nm, total_bytes, budget_s=20.0):
+    """The oracle (plain-torch restatement of the reference forward) on the
+    host cores, on a bounded sample of the batch."""
+    from oracle import spectral_ref as R
+    torch.set_num_threads(os.cpu_count() or 1)
+    from neuraloperator_amd.synthetic import gaussian_random_field
+    m1, m2h = nm[0], nm[1] // 2 + 1
+    bs = 1
+    x = gaussian_random_field((bs, C, H, W), seed=5)
+    g = torch.Generator().manual_seed(6)
+    w = torch.complex(torch.randn(C, C, m1, m2h, generator=g), torch.randn(C, C, m1, m2h, generator=g)) / 64
+    ws = torch.randn(C, C, generator=g) / 8
+    bias = torch.zeros(C, 1, 1)
+
+    def run():
+        y = R.spectral_conv_forward(x, w, bias, [m1, m2h], [m1, m2h])
+        return R.gelu(y + R.linear_skip(x, ws))
+
+    for _ in range(2):
+        run()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 5 or (time.perf_counter() - t_start < budget_s and len(times) < 50):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > 3 * budget_s:
+            break
+    per_sample = statistics.median(times)
+    per_call = per_sample * B / bs
+    return {
+        "value": round(total_bytes / per_call / 1e9, 3),
+        "unit": "GB/s",
+        "us_per_call": round(per_call * 1e6, 1),
+        "cores": torch.get_num_threads(),
+        "os_cpu_count": os.cpu_count(),
+        "kind": "port",
+        "sample": f"{bs} of {B} samples, median of {len(times)} runs after 2 warm-ups, "
+                  f"scaled x{B // bs} to one call",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-torch", action="store_true", help="skip the torch ROCm baseline")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; multi-GPU runs are not part of it "
+                                   "(the block shards by batch with no communication)",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    import neuraloperator_amd  # noqa: F401  (loads the library early)
+    from neuraloperator_amd import _native as nat
+    from neuraloperator_amd import functional as Fh
+
+    dev = torch.device("cuda:0")
+    B, C, H, W, nm = WORKLOADS[args.workload]
+    x, w, ws, bias, (m1, m2h) = make_inputs(B, C, H, W, nm, dev)
+    y = torch.empty_like(x)
+    stream = torch.cuda.current_stream(dev)
+    fused = Fh.spectral_block_is_fused(B, C, C, [H, W], [m1, m2h], nat.SKIP_LINEAR)
+    total_bytes = algorithmic_bytes(B, C, H, W, m1, m2h)
+
+    # preallocate the workspace once so the timed calls do not allocate
+    lib = nat.load()
+    sz, md = nat.i32_array([H, W]), nat.i32_array([m1, m2h])
+    wsb = lib.fno_spectral_block_workspace_bytes(B, C, C, 2, sz, md)
+    wsbuf = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    import ctypes
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+
+    def step():
+        rc = lib.fno_spectral_block_f32(P(x), P(w), P(bias), P(ws), P(y), B, C, C, 2, sz, md, 1,
+                                        nat.SKIP_LINEAR, nat.ACT_GELU, P(wsbuf), wsb,
+                                        ctypes.c_void_p(stream.cuda_stream))
+        if rc:
+            raise RuntimeError(nat.last_error())
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms_per_step = (t1 - t0) * 1e3 / args.steps
+
+    # per-call event timing over the same calls (warm) and with a 1 GiB scratch
+    # write between calls to evict the 256 MB Infinity Cache (cold)
+    warm = event_times(step, max(args.steps, 20), stream)
+    scratch = torch.empty(1 << 28, dtype=torch.float32, device=dev)
+    cold = event_times(step, max(args.steps, 20), stream, flush=lambda: scratch.fill_(1.0))
+    del scratch
+    us_warm = statistics.median(warm) * 1e3
+    us_cold = statistics.median(cold) * 1e3
+    us_mean = statistics.mean(warm) * 1e3
+
+    # device copy bandwidth as a calibration of what HBM delivers
+    src = torch.empty(1 << 28, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    ct = event_times(lambda: dst.copy_(src), 10, stream)
+    copy_gbs = 2 * src.numel() * 4 / (statistics.median(ct) * 1e-3) / 1e9
+    del src, dst
+
+    rocm = None
+    if not args.no_torch:
+        with torch.no_grad():
+            fn = lambda: torch_rocm_block(x, w, bias, ws, m1, m2h)
+            for _ in range(2):
+                fn()
+            tt = event_times(fn, 5, stream)
+        rocm = {"us_per_call": round(statistics.median(tt) * 1e3, 1),
+                "gbs": round(total_bytes / (statistics.median(tt) * 1e-3) / 1e9, 1),
+                "what": "torch.fft (rocFFT) + einsum + irfft + conv + gelu, same GPU"}
+
+    value = total_bytes / (ms_per_step * 1e-3) / 1e9
+    achieved_block = total_bytes / (us_mean * 1e-6) / 1e9
+    line = {
+        "metric": "µs/call + achieved HBM GB/s, fused 2D spectral block B32 C64 256² fp32",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "us_per_call": round(ms_per_step * 1e3, 1),
+        "us_per_call_median_warm": round(us_warm, 1),
+        "us_per_call_median_cold": round(us_cold, 1),
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded Gaussian random field, seeded N(0, s^2) weights)",
+        "config": {"workload": f"fused 2D spectral block x[{B},{C},{H},{W}] n_modes{tuple(nm)} "
+                               f"-> {m1}x{m2h} modes, linear skip, bias, erf GELU",
+                   "batch": B, "channels": C, "H": H, "W": W, "modes": [m1, m2h],
+                   "fused_path": bool(fused), "algorithmic_bytes": total_bytes},
+        "roofline": {"bound": "hbm", "achieved": round(achieved_block, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved_block / HBM_PEAK_GBS, 4),
+                     "traffic": None,
+                     "kernel": "whole block call (k_fwd_plane, contraction, k_inv_cols, "
+                               "k_row_epilogue), HIP events on the launch stream"},
+        "copy_bandwidth_gbs": round(copy_gbs, 1),
+        "torch_rocm_baseline": rocm,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(B, C, H, W, nm, total_bytes)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,160 @@
+/*
+ * fno_hip.h -- C ABI of the MI355X (gfx950) FNO spectral-block library
+ * (libfnohip.so).
+ *
+ * Conventions
+ *   - Every pointer is a device pointer to contiguous memory allocated by the
+ *     caller (in practice torch's caching allocator).  Real fields are float32
+ *     N C D1..Dn; complex spectra are complex64 (interleaved float pairs).
+ *   - Returns 0 (FNO_OK) on success, otherwise an FNO_ERR_* code; the message
+ *     is available from fno_last_error() (thread-local).
+ *   - Shapes are validated on the host before any launch.  Work is enqueued on
+ *     `stream` (a hipStream_t passed as void*); nothing synchronizes.
+ *   - The library allocates no device memory: scratch space is the caller's
+ *     `workspace` of at least the size the matching *_workspace_bytes() call
+ *     reports.
+ *   - Spectrum window layout ("window order"): along every axis but the last,
+ *     window index j holds frequency j - m/2 (integer division), which is the
+ *     fftshift-ed order the reference's weights use; along the last (rfft)
+ *     axis index j holds frequency j.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository):
+ *   neuralop/layers/spectral_convolution.py  SpectralConv.forward :417-570
+ *   neuralop/layers/fno_block.py             FNOBlocks.forward_with_postactivation :327-381
+ *   neuralop/layers/skip_connections.py      Flattened1dConv.forward :122-130,
+ *                                            SoftGating.forward :88-93
+ */
+#ifndef FNO_HIP_H
+#define FNO_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FNO_OK 0
+#define FNO_ERR_INVALID 1     /* bad argument or shape */
+#define FNO_ERR_UNSUPPORTED 2 /* valid request the kernels do not cover */
+#define FNO_ERR_HIP 3         /* HIP runtime error */
+#define FNO_ERR_WORKSPACE 4   /* workspace smaller than required */
+
+/* torch.fft norm= values */
+#define FNO_NORM_BACKWARD 0
+#define FNO_NORM_FORWARD 1
+#define FNO_NORM_ORTHO 2
+
+/* skip connection applied by the block entry points */
+#define FNO_SKIP_NONE 0
+#define FNO_SKIP_LINEAR 1      /* 1x1 conv, weight [Co, Ci], no bias */
+#define FNO_SKIP_SOFT_GATING 2 /* per-channel scale, weight [C] (Ci == Co) */
+#define FNO_SKIP_IDENTITY 3    /* Ci == Co */
+
+/* activation applied by the block entry points */
+#define FNO_ACT_NONE 0
+#define FNO_ACT_GELU 1 /* exact erf GELU, torch.nn.functional.gelu default */
+
+/* Library version string. */
+const char* fno_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* fno_last_error(void);
+
+/*
+ * Forward truncated real FFT.  Replaces torch.fft.rfftn(norm=...) + fftshift
+ * + window slice, spectral_convolution.py:443-449 and :500-521.
+ *   x     float32 [planes, N_1..N_ndim]
+ *   xhat  complex64 [planes, m_1..m_ndim] in window order
+ *   modes m_d = kept count per axis (m_last <= N_last/2+1, m_d <= N_d)
+ */
+int fno_rfft_window_f32(const float* x, void* xhat, int64_t planes, int32_t ndim,
+                        const int32_t* sizes, const int32_t* modes, int32_t norm,
+                        void* workspace, size_t workspace_bytes, void* stream);
+size_t fno_rfft_window_workspace_bytes(int64_t planes, int32_t ndim, const int32_t* sizes,
+                                       const int32_t* modes);
+
+/*
+ * Dense mode-wise complex contraction.  Replaces _contract_dense and
+ * _contract_dense_separable, spectral_convolution.py:21-52.
+ *   separable == 0: y[b,o,k] = sum_i x[b,i,k] w[i,o,k]   (w [Ci,Co,M])
+ *   separable != 0: y[b,i,k] = x[b,i,k] w[i,k]           (w [Ci,M], Co == Ci)
+ * M = prod(m_d) modes, all complex64.
+ */
+int fno_contract_dense_c64(const void* xhat, const void* w, void* yhat, int32_t batch,
+                           int32_t in_channels, int32_t out_channels, int64_t n_modes,
+                           int32_t separable, void* stream);
+
+/*
+ * Tucker-factorized contraction with the factors, never forming the dense
+ * weight.  Replaces _contract_tucker (non-separable),
+ * spectral_convolution.py:76-103.
+ *   core     complex64 [r_in, r_out, r_1..r_ndim]
+ *   factors  ndim+2 complex64 matrices: U_in [Ci, r_in], U_out [Co, r_out],
+ *            U_d [m_d, r_d] (already cut to the window rows)
+ *   y[b,o,k] = sum x[b,i,k] core[g,h,a..] U_in[i,g] U_out[o,h] prod_d U_d[k_d,a_d]
+ */
+int fno_contract_tucker_c64(const void* xhat, const void* core, const void* const* factors,
+                            const int32_t* ranks, void* yhat, int32_t batch,
+                            int32_t in_channels, int32_t out_channels, int32_t ndim,
+                            const int32_t* modes, void* workspace, size_t workspace_bytes,
+                            void* stream);
+size_t fno_contract_tucker_workspace_bytes(int32_t batch, int32_t ndim, const int32_t* modes,
+                                           const int32_t* ranks);
+
+/*
+ * Inverse of the window transform plus bias.  Replaces ifftshift + ifftn
+ * (s = out sizes) + Hermitian fix-up + irfft + bias,
+ * spectral_convolution.py:524-568 (enforce_hermitian_symmetry selects the
+ * :547-559 or the :564 branch; out sizes differ from in sizes under
+ * output_shape / resolution_scaling_factor).
+ *   yhat  complex64 [batch*channels, m_1..m_ndim] window order
+ *   bias  float32 [channels] or NULL
+ *   y     float32 [batch*channels, N'_1..N'_ndim]
+ */
+int fno_irfft_window_f32(const void* yhat, const float* bias, float* y, int64_t batch,
+                         int32_t channels, int32_t ndim, const int32_t* in_sizes,
+                         const int32_t* out_sizes, const int32_t* modes, int32_t norm,
+                         int32_t enforce_hermitian, void* workspace, size_t workspace_bytes,
+                         void* stream);
+size_t fno_irfft_window_workspace_bytes(int64_t planes, int32_t ndim, const int32_t* out_sizes,
+                                        const int32_t* modes);
+
+/*
+ * Block epilogue: y = act(spec + skip(x)).  Replaces the skip, add and first
+ * activation of FNOBlocks.forward_with_postactivation, fno_block.py:331-361,
+ * with the skips of skip_connections.py:88-130.  spec may alias y.
+ *   spec, y  float32 [B, Co, P];  x float32 [B, Ci, P]
+ */
+int fno_block_epilogue_f32(const float* spec, const float* x, const float* skip_weight,
+                           float* y, int32_t batch, int32_t in_channels, int32_t out_channels,
+                           int64_t points, int32_t skip_kind, int32_t act, void* stream);
+
+/*
+ * One call for the whole spectral block
+ *     y = act(SpectralConv(x) + skip(x))
+ * with a dense weight (w [Ci, Co, m_1..m_ndim] window, complex64) and bias
+ * [Co] (or NULL).  Output size equals input size.  Picks the fused 2D path
+ * (LDS FFTs + MFMA skip epilogue) when the shape allows it and composes the
+ * generic kernels otherwise.
+ */
+int fno_spectral_block_f32(const float* x, const void* w, const float* bias,
+                           const float* skip_weight, float* y, int32_t batch,
+                           int32_t in_channels, int32_t out_channels, int32_t ndim,
+                           const int32_t* sizes, const int32_t* modes, int32_t norm,
+                           int32_t skip_kind, int32_t act, void* workspace,
+                           size_t workspace_bytes, void* stream);
+size_t fno_spectral_block_workspace_bytes(int32_t batch, int32_t in_channels,
+                                          int32_t out_channels, int32_t ndim,
+                                          const int32_t* sizes, const int32_t* modes);
+
+/* 1 if fno_spectral_block_f32 takes the fused 2D path for this shape. */
+int fno_spectral_block_is_fused(int32_t batch, int32_t in_channels, int32_t out_channels,
+                                int32_t ndim, const int32_t* sizes, const int32_t* modes,
+                                int32_t skip_kind);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FNO_HIP_H */

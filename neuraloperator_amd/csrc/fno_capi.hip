@@ -1,0 +1,283 @@
+// extern "C" entry points of libfnohip.so: host-side validation, workspace
+// accounting and dispatch to the generic and fused kernels.  Declarations and
+// the reference interfaces each entry point replaces are in include/fno_hip.h.
+#include "fno_common.h"
+
+namespace fno {
+const char* last_error_cstr();
+void clear_error();
+int validate_window(int32_t ndim, const int32_t* sizes, const int32_t* modes);
+size_t rfft_window_ws(int64_t planes, int32_t ndim, const int32_t* sizes, const int32_t* modes);
+size_t irfft_window_ws(int64_t planes, int32_t ndim, const int32_t* out_sizes,
+                       const int32_t* modes);
+int rfft_window(const float* x, float2* xhat, int64_t planes, int32_t ndim, const int32_t* sizes,
+                const int32_t* modes, int32_t norm, void* ws, size_t ws_bytes, hipStream_t st);
+int irfft_window(const float2* yhat, const float* bias, float* y, int64_t batch, int32_t channels,
+                 int32_t ndim, const int32_t* in_sizes, const int32_t* out_sizes,
+                 const int32_t* modes, int32_t norm, int32_t enforce, void* ws, size_t ws_bytes,
+                 hipStream_t st);
+int contract_dense(const float2* X, const float2* W, float2* Y, int B, int Ci, int Co, int64_t M,
+                   int64_t sWi, int64_t sWo, int64_t sWk, hipStream_t st);
+int contract_separable(const float2* X, const float2* W, float2* Y, int B, int C, int64_t M,
+                       hipStream_t st);
+int axis_matmul(const float2* in, const float2* mat, float2* out, int64_t outer, int A, int J,
+                int64_t inner, hipStream_t st);
+int block_epilogue(const float* spec, const float* x, const float* ws, float* y, int B, int Ci,
+                   int Co, int64_t P, int skip_kind, int act, hipStream_t st);
+bool fast2d_supported(int B, int Ci, int Co, int ndim, const int32_t* sizes, const int32_t* modes,
+                      int skip_kind);
+size_t fast2d_workspace(int B, int Ci, int Co, const int32_t* sizes, const int32_t* modes);
+int fast2d_block(const float* x, const float2* w, const float* bias, const float* skip_w, float* y,
+                 int B, int Ci, int Co, const int32_t* sizes, const int32_t* modes, int norm,
+                 int skip_kind, int act, void* ws, size_t ws_bytes, hipStream_t st);
+}  // namespace fno
+
+using namespace fno;
+
+static int64_t mode_count(int32_t ndim, const int32_t* modes) {
+  int64_t m = 1;
+  for (int d = 0; d < ndim; ++d) m *= modes[d];
+  return m;
+}
+
+static int check_norm(int32_t norm) {
+  FNO_CHECK_ARG(norm == FNO_NORM_BACKWARD || norm == FNO_NORM_FORWARD || norm == FNO_NORM_ORTHO,
+                "norm must be FNO_NORM_BACKWARD/FORWARD/ORTHO (got %d)", norm);
+  return FNO_OK;
+}
+
+static int check_skip(int32_t skip_kind, int32_t act, int32_t ci, int32_t co, const void* skip_w) {
+  FNO_CHECK_ARG(skip_kind >= FNO_SKIP_NONE && skip_kind <= FNO_SKIP_IDENTITY,
+                "unknown skip kind %d", skip_kind);
+  FNO_CHECK_ARG(act == FNO_ACT_NONE || act == FNO_ACT_GELU, "unknown activation %d", act);
+  FNO_CHECK_ARG(!(skip_kind == FNO_SKIP_LINEAR || skip_kind == FNO_SKIP_SOFT_GATING) || skip_w,
+                "skip kind %d needs a skip weight", skip_kind);
+  FNO_CHECK_ARG(!(skip_kind == FNO_SKIP_SOFT_GATING || skip_kind == FNO_SKIP_IDENTITY) || ci == co,
+                "soft-gating / identity skips need in_channels == out_channels (%d vs %d)", ci,
+                co);
+  return FNO_OK;
+}
+
+extern "C" {
+
+const char* fno_version(void) { return "fnohip 0.1 gfx950"; }
+
+const char* fno_last_error(void) { return last_error_cstr(); }
+
+size_t fno_rfft_window_workspace_bytes(int64_t planes, int32_t ndim, const int32_t* sizes,
+                                       const int32_t* modes) {
+  if (!sizes || !modes || ndim < 1 || ndim > 3) return 0;
+  return rfft_window_ws(planes, ndim, sizes, modes);
+}
+
+int fno_rfft_window_f32(const float* x, void* xhat, int64_t planes, int32_t ndim,
+                        const int32_t* sizes, const int32_t* modes, int32_t norm, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  clear_error();
+  FNO_CHECK_ARG(x && xhat, "x/xhat must not be NULL");
+  FNO_CHECK_ARG(planes >= 1, "planes must be positive");
+  int rc = validate_window(ndim, sizes, modes);
+  if (rc) return rc;
+  rc = check_norm(norm);
+  if (rc) return rc;
+  return rfft_window(x, reinterpret_cast<float2*>(xhat), planes, ndim, sizes, modes, norm, workspace,
+                     workspace_bytes, reinterpret_cast<hipStream_t>(stream));
+}
+
+int fno_contract_dense_c64(const void* xhat, const void* w, void* yhat, int32_t batch,
+                           int32_t in_channels, int32_t out_channels, int64_t n_modes,
+                           int32_t separable, void* stream) {
+  clear_error();
+  FNO_CHECK_ARG(xhat && w && yhat, "xhat/w/yhat must not be NULL");
+  FNO_CHECK_ARG(batch >= 1 && in_channels >= 1 && out_channels >= 1 && n_modes >= 1,
+                "batch/channels/modes must be positive");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const float2* X = reinterpret_cast<const float2*>(xhat);
+  const float2* W = reinterpret_cast<const float2*>(w);
+  float2* Y = reinterpret_cast<float2*>(yhat);
+  if (separable) {
+    FNO_CHECK_ARG(in_channels == out_channels, "separable contraction needs Ci == Co");
+    return contract_separable(X, W, Y, batch, in_channels, n_modes, st);
+  }
+  return contract_dense(X, W, Y, batch, in_channels, out_channels, n_modes,
+                        (int64_t)out_channels * n_modes, n_modes, 1, st);
+}
+
+size_t fno_contract_tucker_workspace_bytes(int32_t batch, int32_t ndim, const int32_t* modes,
+                                           const int32_t* ranks) {
+  if (!modes || !ranks || ndim < 1 || ndim > 3) return 0;
+  const int64_t M = mode_count(ndim, modes);
+  int64_t big = (int64_t)ranks[0] * ranks[1];
+  for (int d = 0; d < ndim; ++d) big *= (modes[d] > ranks[2 + d] ? modes[d] : ranks[2 + d]);
+  const int64_t K = (int64_t)ranks[0] * ranks[1] * M;
+  const int64_t e = K + 2 * big + (int64_t)batch * ranks[0] * M + (int64_t)batch * ranks[1] * M;
+  return (size_t)e * sizeof(float2);
+}
+
+int fno_contract_tucker_c64(const void* xhat, const void* core, const void* const* factors,
+                            const int32_t* ranks, void* yhat, int32_t batch, int32_t in_channels,
+                            int32_t out_channels, int32_t ndim, const int32_t* modes,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  FNO_CHECK_ARG(xhat && core && factors && ranks && yhat && modes, "NULL argument");
+  FNO_CHECK_ARG(ndim >= 1 && ndim <= 3, "ndim must be 1..3");
+  for (int d = 0; d < ndim + 2; ++d) {
+    FNO_CHECK_ARG(factors[d], "factor %d is NULL", d);
+    FNO_CHECK_ARG(ranks[d] >= 1, "rank %d must be positive", d);
+  }
+  FNO_CHECK_ARG(batch >= 1 && in_channels >= 1 && out_channels >= 1, "bad batch/channels");
+  const size_t need = fno_contract_tucker_workspace_bytes(batch, ndim, modes, ranks);
+  if (workspace_bytes < need || !workspace) {
+    set_error("tucker contraction: workspace %zu < %zu bytes", workspace_bytes, need);
+    return FNO_ERR_WORKSPACE;
+  }
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int64_t M = mode_count(ndim, modes);
+  const int rin = ranks[0], rout = ranks[1];
+  int64_t big = (int64_t)rin * rout;
+  for (int d = 0; d < ndim; ++d) big *= (modes[d] > ranks[2 + d] ? modes[d] : ranks[2 + d]);
+  float2* Kt = reinterpret_cast<float2*>(workspace);
+  float2* e1 = Kt + (int64_t)rin * rout * M;
+  float2* e2 = e1 + big;
+  float2* t1 = e2 + big;
+  float2* t2 = t1 + (int64_t)batch * rin * M;
+  // K[g,h,k] = core x_d U_d over the mode axes
+  const float2* src = reinterpret_cast<const float2*>(core);
+  for (int a = 0; a < ndim; ++a) {
+    int64_t outer = (int64_t)rin * rout;
+    for (int b = 0; b < a; ++b) outer *= modes[b];
+    int64_t inner = 1;
+    for (int b = a + 1; b < ndim; ++b) inner *= ranks[2 + b];
+    float2* dst = (a == ndim - 1) ? Kt : ((a % 2 == 0) ? e1 : e2);
+    int rc = axis_matmul(src, reinterpret_cast<const float2*>(factors[2 + a]), dst, outer,
+                         ranks[2 + a], modes[a], inner, st);
+    if (rc) return rc;
+    src = dst;
+  }
+  const float2* X = reinterpret_cast<const float2*>(xhat);
+  const float2* Uin = reinterpret_cast<const float2*>(factors[0]);
+  const float2* Uout = reinterpret_cast<const float2*>(factors[1]);
+  // t1[b,g,k] = sum_i x[b,i,k] U_in[i,g]
+  int rc = contract_dense(X, Uin, t1, batch, in_channels, rin, M, rin, 1, 0, st);
+  if (rc) return rc;
+  // t2[b,h,k] = sum_g t1[b,g,k] K[g,h,k]
+  rc = contract_dense(t1, Kt, t2, batch, rin, rout, M, (int64_t)rout * M, M, 1, st);
+  if (rc) return rc;
+  // y[b,o,k] = sum_h t2[b,h,k] U_out[o,h]
+  return contract_dense(t2, Uout, reinterpret_cast<float2*>(yhat), batch, rout, out_channels, M, 1,
+                        rout, 0, st);
+}
+
+size_t fno_irfft_window_workspace_bytes(int64_t planes, int32_t ndim, const int32_t* out_sizes,
+                                        const int32_t* modes) {
+  if (!out_sizes || !modes || ndim < 1 || ndim > 3) return 0;
+  return irfft_window_ws(planes, ndim, out_sizes, modes);
+}
+
+int fno_irfft_window_f32(const void* yhat, const float* bias, float* y, int64_t batch,
+                         int32_t channels, int32_t ndim, const int32_t* in_sizes,
+                         const int32_t* out_sizes, const int32_t* modes, int32_t norm,
+                         int32_t enforce_hermitian, void* workspace, size_t workspace_bytes,
+                         void* stream) {
+  clear_error();
+  FNO_CHECK_ARG(yhat && y, "yhat/y must not be NULL");
+  FNO_CHECK_ARG(batch >= 1 && channels >= 1, "batch/channels must be positive");
+  int rc = validate_window(ndim, in_sizes, modes);
+  if (rc) return rc;
+  FNO_CHECK_ARG(out_sizes, "out_sizes must not be NULL");
+  for (int d = 0; d < ndim; ++d) {
+    FNO_CHECK_ARG(out_sizes[d] >= 1 && out_sizes[d] <= 4096, "out size %d outside [1, 4096]",
+                  out_sizes[d]);
+  }
+  rc = check_norm(norm);
+  if (rc) return rc;
+  return irfft_window(reinterpret_cast<const float2*>(yhat), bias, y, batch, channels, ndim,
+                      in_sizes, out_sizes, modes, norm, enforce_hermitian, workspace,
+                      workspace_bytes, reinterpret_cast<hipStream_t>(stream));
+}
+
+int fno_block_epilogue_f32(const float* spec, const float* x, const float* skip_weight, float* y,
+                           int32_t batch, int32_t in_channels, int32_t out_channels,
+                           int64_t points, int32_t skip_kind, int32_t act, void* stream) {
+  clear_error();
+  FNO_CHECK_ARG(spec && y, "spec/y must not be NULL");
+  FNO_CHECK_ARG(skip_kind == FNO_SKIP_NONE || x, "x must not be NULL with a skip");
+  FNO_CHECK_ARG(batch >= 1 && in_channels >= 1 && out_channels >= 1 && points >= 1,
+                "bad batch/channels/points");
+  int rc = check_skip(skip_kind, act, in_channels, out_channels, skip_weight);
+  if (rc) return rc;
+  return block_epilogue(spec, x, skip_weight, y, batch, in_channels, out_channels, points,
+                        skip_kind, act, reinterpret_cast<hipStream_t>(stream));
+}
+
+int fno_spectral_block_is_fused(int32_t batch, int32_t in_channels, int32_t out_channels,
+                                int32_t ndim, const int32_t* sizes, const int32_t* modes,
+                                int32_t skip_kind) {
+  if (!sizes || !modes) return 0;
+  return fast2d_supported(batch, in_channels, out_channels, ndim, sizes, modes, skip_kind) ? 1 : 0;
+}
+
+size_t fno_spectral_block_workspace_bytes(int32_t batch, int32_t in_channels,
+                                          int32_t out_channels, int32_t ndim,
+                                          const int32_t* sizes, const int32_t* modes) {
+  if (!sizes || !modes || ndim < 1 || ndim > 3) return 0;
+  size_t fused = 0;
+  if (ndim == 2) fused = fast2d_workspace(batch, in_channels, out_channels, sizes, modes);
+  const int64_t M = mode_count(ndim, modes);
+  const size_t spectra = (size_t)((int64_t)batch * in_channels * M +
+                                  (int64_t)batch * out_channels * M) * sizeof(float2);
+  size_t a = rfft_window_ws((int64_t)batch * in_channels, ndim, sizes, modes);
+  size_t b = irfft_window_ws((int64_t)batch * out_channels, ndim, sizes, modes);
+  const size_t generic = spectra + (a > b ? a : b);
+  return fused > generic ? fused : generic;
+}
+
+int fno_spectral_block_f32(const float* x, const void* w, const float* bias,
+                           const float* skip_weight, float* y, int32_t batch, int32_t in_channels,
+                           int32_t out_channels, int32_t ndim, const int32_t* sizes,
+                           const int32_t* modes, int32_t norm, int32_t skip_kind, int32_t act,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  FNO_CHECK_ARG(x && w && y, "x/w/y must not be NULL");
+  FNO_CHECK_ARG(batch >= 1 && in_channels >= 1 && out_channels >= 1, "bad batch/channels");
+  int rc = validate_window(ndim, sizes, modes);
+  if (rc) return rc;
+  rc = check_norm(norm);
+  if (rc) return rc;
+  rc = check_skip(skip_kind, act, in_channels, out_channels, skip_weight);
+  if (rc) return rc;
+  const size_t need = fno_spectral_block_workspace_bytes(batch, in_channels, out_channels, ndim,
+                                                         sizes, modes);
+  if (!workspace || workspace_bytes < need) {
+    set_error("spectral block: workspace %zu < %zu bytes", workspace_bytes, need);
+    return FNO_ERR_WORKSPACE;
+  }
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (fast2d_supported(batch, in_channels, out_channels, ndim, sizes, modes, skip_kind))
+    return fast2d_block(x, reinterpret_cast<const float2*>(w), bias, skip_weight, y, batch,
+                        in_channels, out_channels, sizes, modes, norm, skip_kind, act, workspace,
+                        workspace_bytes, st);
+  // generic composition
+  const int64_t M = mode_count(ndim, modes);
+  float2* xhat = reinterpret_cast<float2*>(workspace);
+  float2* yhat = xhat + (int64_t)batch * in_channels * M;
+  void* rest = yhat + (int64_t)batch * out_channels * M;
+  const size_t rest_bytes = workspace_bytes - (size_t)((int64_t)batch * (in_channels + out_channels) *
+                                                       M * sizeof(float2));
+  rc = rfft_window(x, xhat, (int64_t)batch * in_channels, ndim, sizes, modes, norm, rest,
+                   rest_bytes, st);
+  if (rc) return rc;
+  rc = contract_dense(xhat, reinterpret_cast<const float2*>(w), yhat, batch, in_channels,
+                      out_channels, M, (int64_t)out_channels * M, M, 1, st);
+  if (rc) return rc;
+  rc = irfft_window(yhat, bias, y, batch, out_channels, ndim, sizes, sizes, modes, norm, 1, rest,
+                    rest_bytes, st);
+  if (rc) return rc;
+  int64_t P = 1;
+  for (int d = 0; d < ndim; ++d) P *= sizes[d];
+  if (skip_kind == FNO_SKIP_NONE && act == FNO_ACT_NONE) return FNO_OK;
+  return block_epilogue(y, x, skip_weight, y, batch, in_channels, out_channels, P, skip_kind, act,
+                        st);
+}
+
+}  // extern "C"

@@ -1,0 +1,513 @@
+// Generic kernels of the FNO spectral path: any spatial size (up to 4096 per
+// axis), 1-3 spatial dims, any mode window.  Each spatial axis is handled by a
+// direct pruned DFT (only the kept frequencies are computed, O(N*m) per line),
+// which is the right tool when m << N or N is not a power of two; the fused 2D
+// kernels in fno_fast2d.hip take over for large power-of-two planes.
+//
+// Frequency bookkeeping follows SpectralConv.forward
+// (neuralop/layers/spectral_convolution.py:429-568):
+//   forward  window index j on a non-last axis holds frequency j - m/2
+//            (rfftn + fftshift + centred slice, :443-449, :500-519);
+//            on the last axis it holds frequency j (rfft half spectrum)
+//   inverse  ifftshift + ifftn(s = N') puts frequency f at index t = f mod N of
+//            the length-N spectrum and then zero-pads / truncates at the end,
+//            so the entry contributes exp(+2 pi i t n / N') iff t < N' (:531-548)
+//   last     irfft(n = N') with the imaginary parts of bin 0 (and of bin N/2
+//            when N' is even, enforce_hermitian_symmetry) zeroed (:550-559)
+#include "fno_common.h"
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+namespace fno {
+
+static thread_local std::string g_last_error;
+
+void set_error(const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return FNO_OK;
+  set_error("%s: %s", what, hipGetErrorString(e));
+  return FNO_ERR_HIP;
+}
+
+int launch_status(const char* what) { return hip_status(hipGetLastError(), what); }
+
+const char* last_error_cstr() { return g_last_error.c_str(); }
+void clear_error() { g_last_error.clear(); }
+
+static double prod_sizes(const int32_t* s, int n) {
+  double p = 1.0;
+  for (int i = 0; i < n; ++i) p *= (double)s[i];
+  return p;
+}
+
+double forward_scale(int norm, const int32_t* in_sizes, int ndim) {
+  double p = prod_sizes(in_sizes, ndim);
+  if (norm == FNO_NORM_FORWARD) return 1.0 / p;
+  if (norm == FNO_NORM_ORTHO) return 1.0 / std::sqrt(p);
+  return 1.0;
+}
+
+double inverse_scale(int norm, const int32_t* out_sizes, int ndim) {
+  double p = prod_sizes(out_sizes, ndim);
+  if (norm == FNO_NORM_BACKWARD) return 1.0 / p;
+  if (norm == FNO_NORM_ORTHO) return 1.0 / std::sqrt(p);
+  return 1.0;
+}
+
+static constexpr int kMaxAxis = 4096;
+static constexpr int kThreads = 256;
+
+// --------------------------------------------------------------- forward axes
+// Last axis, real -> complex:  out[r, j] = s * sum_n x[r, n] exp(-2 pi i j n / N)
+__global__ void __launch_bounds__(kThreads)
+k_r2c_direct(const float* __restrict__ x, float2* __restrict__ out, int64_t rows, int N, int m,
+             int rows_per_block, float scale) {
+  extern __shared__ float smem[];
+  float2* tw = reinterpret_cast<float2*>(smem);
+  float* xs = reinterpret_cast<float*>(tw + N);
+  for (int t = threadIdx.x; t < N; t += blockDim.x) tw[t] = twiddle_pos(t, N);
+  const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
+  const int nr = (int)min((int64_t)rows_per_block, rows - r0);
+  const float* xg = x + r0 * N;
+  for (int t = threadIdx.x; t < nr * N; t += blockDim.x) xs[t] = xg[t];
+  __syncthreads();
+  for (int task = threadIdx.x; task < nr * m; task += blockDim.x) {
+    const int rr = task / m, j = task - (task / m) * m;
+    const float* xr = xs + rr * N;
+    float re = 0.f, im = 0.f;
+    int idx = 0;
+    for (int n = 0; n < N; ++n) {
+      const float2 w = tw[idx];
+      const float v = xr[n];
+      re = fmaf(v, w.x, re);
+      im = fmaf(-v, w.y, im);
+      idx += j;
+      if (idx >= N) idx -= N;
+    }
+    out[(r0 + rr) * m + j] = make_float2(re * scale, im * scale);
+  }
+}
+
+// Middle axis, complex -> complex, centred window:
+//   out[o, j, q] = s * sum_n in[o, n, q] exp(-2 pi i (j - m/2) n / N)
+__global__ void __launch_bounds__(kThreads)
+k_c2c_fwd_direct(const float2* __restrict__ in, float2* __restrict__ out, int64_t outer, int N,
+                 int64_t inner, int m, float scale) {
+  extern __shared__ float smem[];
+  float2* tw = reinterpret_cast<float2*>(smem);
+  for (int t = threadIdx.x; t < N; t += blockDim.x) tw[t] = twiddle_pos(t, N);
+  __syncthreads();
+  const int64_t total = outer * m * inner;
+  for (int64_t task = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; task < total;
+       task += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t q = task % inner;
+    const int64_t t2 = task / inner;
+    const int j = (int)(t2 % m);
+    const int64_t o = t2 / m;
+    int step = (j - m / 2) % N;
+    if (step < 0) step += N;
+    const float2* src = in + o * (int64_t)N * inner + q;
+    float2 acc = make_float2(0.f, 0.f);
+    int idx = 0;
+    for (int n = 0; n < N; ++n) {
+      const float2 v = src[(int64_t)n * inner];
+      const float2 w = tw[idx];
+      acc.x = fmaf(v.x, w.x, fmaf(v.y, w.y, acc.x));
+      acc.y = fmaf(v.y, w.x, fmaf(-v.x, w.y, acc.y));
+      idx += step;
+      if (idx >= N) idx -= N;
+    }
+    out[task] = cscale(acc, scale);
+  }
+}
+
+// ---------------------------------------------------------------- inverse axes
+// Middle axis, window -> length N' (ifftshift + ifftn(s = N') semantics):
+//   out[o, n, q] = s * sum_{j : t_j < N'} in[o, j, q] exp(+2 pi i t_j n / N'),
+//   t_j = (j - m/2) mod N
+__global__ void __launch_bounds__(kThreads)
+k_c2c_inv_direct(const float2* __restrict__ in, float2* __restrict__ out, int64_t outer, int N,
+                 int Np, int64_t inner, int m, float scale) {
+  extern __shared__ float smem[];
+  float2* tw = reinterpret_cast<float2*>(smem);
+  for (int t = threadIdx.x; t < Np; t += blockDim.x) tw[t] = twiddle_pos(t, Np);
+  __syncthreads();
+  const int64_t total = outer * Np * inner;
+  for (int64_t task = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; task < total;
+       task += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t q = task % inner;
+    const int64_t t2 = task / inner;
+    const int n = (int)(t2 % Np);
+    const int64_t o = t2 / Np;
+    const float2* src = in + o * (int64_t)m * inner + q;
+    float2 acc = make_float2(0.f, 0.f);
+    for (int j = 0; j < m; ++j) {
+      int t = (j - m / 2) % N;
+      if (t < 0) t += N;
+      if (t >= Np) continue;
+      const int idx = (int)(((int64_t)t * n) % Np);
+      cfma(acc, src[(int64_t)j * inner], tw[idx]);
+    }
+    out[task] = cscale(acc, scale);
+  }
+}
+
+// Last axis, window -> real length N' (irfft semantics) + bias:
+//   y[r, n] = s * sum_{j < N'/2+1} c_j Re(Z_j exp(2 pi i j n / N')) + bias[channel(r)]
+__global__ void __launch_bounds__(kThreads)
+k_c2r_direct(const float2* __restrict__ in, float* __restrict__ out, const float* __restrict__ bias,
+             int64_t rows, int64_t rows_per_plane, int channels, int N, int Np, int m, int enforce,
+             int rows_per_block, float scale) {
+  extern __shared__ float smem[];
+  float2* tw = reinterpret_cast<float2*>(smem);
+  float2* zs = tw + Np;
+  for (int t = threadIdx.x; t < Np; t += blockDim.x) tw[t] = twiddle_pos(t, Np);
+  const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
+  const int nr = (int)min((int64_t)rows_per_block, rows - r0);
+  const int K = min(m, Np / 2 + 1);
+  for (int t = threadIdx.x; t < nr * K; t += blockDim.x) {
+    const int rr = t / K, j = t - (t / K) * K;
+    float2 z = in[(r0 + rr) * m + j];
+    float c = 2.f;
+    if (j == 0) {
+      z.y = 0.f;
+      c = 1.f;
+    }
+    if (enforce && (Np % 2 == 0) && j == N / 2) z.y = 0.f;
+    if ((Np % 2 == 0) && j == Np / 2) c = 1.f;
+    zs[rr * K + j] = cscale(z, c);
+  }
+  __syncthreads();
+  for (int task = threadIdx.x; task < nr * Np; task += blockDim.x) {
+    const int rr = task / Np, n = task - (task / Np) * Np;
+    const float2* z = zs + rr * K;
+    float acc = 0.f;
+    int idx = 0;
+    for (int j = 0; j < K; ++j) {
+      const float2 w = tw[idx];
+      acc = fmaf(z[j].x, w.x, fmaf(-z[j].y, w.y, acc));
+      idx += n;
+      if (idx >= Np) idx -= Np;
+    }
+    float v = acc * scale;
+    if (bias) v += bias[((r0 + rr) / rows_per_plane) % channels];
+    out[(r0 + rr) * Np + n] = v;
+  }
+}
+
+// ----------------------------------------------------------------- contraction
+// y[b, o, k] = sum_i x[b, i, k] * w[i*sWi + o*sWo + k*sWk]     (complex)
+// One lane per mode k; each thread owns a TB x TO tile of (b, o).
+template <int TB, int TO>
+__global__ void __launch_bounds__(kThreads)
+k_contract_dense(const float2* __restrict__ X, const float2* __restrict__ W, float2* __restrict__ Y,
+                 int B, int Ci, int Co, int64_t M, int64_t sWi, int64_t sWo, int64_t sWk) {
+  const int64_t k = (int64_t)blockIdx.x * 64 + (threadIdx.x & 63);
+  const int nOt = (Co + TO - 1) / TO;
+  const int nBt = (B + TB - 1) / TB;
+  const int tile = blockIdx.y * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (tile >= nOt * nBt || k >= M) return;
+  const int b0 = (tile / nOt) * TB;
+  const int o0 = (tile % nOt) * TO;
+  float2 acc[TB][TO];
+#pragma unroll
+  for (int a = 0; a < TB; ++a)
+#pragma unroll
+    for (int c = 0; c < TO; ++c) acc[a][c] = make_float2(0.f, 0.f);
+  for (int i = 0; i < Ci; ++i) {
+    float2 xv[TB], wv[TO];
+#pragma unroll
+    for (int a = 0; a < TB; ++a)
+      xv[a] = (b0 + a < B) ? X[((int64_t)(b0 + a) * Ci + i) * M + k] : make_float2(0.f, 0.f);
+#pragma unroll
+    for (int c = 0; c < TO; ++c)
+      wv[c] = (o0 + c < Co) ? W[(int64_t)i * sWi + (int64_t)(o0 + c) * sWo + k * sWk]
+                            : make_float2(0.f, 0.f);
+#pragma unroll
+    for (int a = 0; a < TB; ++a)
+#pragma unroll
+      for (int c = 0; c < TO; ++c) cfma(acc[a][c], xv[a], wv[c]);
+  }
+#pragma unroll
+  for (int a = 0; a < TB; ++a)
+#pragma unroll
+    for (int c = 0; c < TO; ++c)
+      if (b0 + a < B && o0 + c < Co) Y[((int64_t)(b0 + a) * Co + o0 + c) * M + k] = acc[a][c];
+}
+
+// y[b, i, k] = x[b, i, k] * w[i, k]
+__global__ void __launch_bounds__(kThreads)
+k_contract_separable(const float2* __restrict__ X, const float2* __restrict__ W,
+                     float2* __restrict__ Y, int64_t CM, int64_t total) {
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x)
+    Y[t] = cmul(X[t], W[t % CM]);
+}
+
+// out[o, j, q] = sum_a in[o, a, q] * mat[j, a]   (complex matrix along an axis)
+__global__ void __launch_bounds__(kThreads)
+k_axis_matmul(const float2* __restrict__ in, const float2* __restrict__ mat, float2* __restrict__ out,
+              int64_t outer, int A, int J, int64_t inner) {
+  const int64_t total = outer * J * inner;
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t q = t % inner;
+    const int64_t t2 = t / inner;
+    const int j = (int)(t2 % J);
+    const int64_t o = t2 / J;
+    const float2* src = in + o * (int64_t)A * inner + q;
+    float2 acc = make_float2(0.f, 0.f);
+    for (int a = 0; a < A; ++a) cfma(acc, src[(int64_t)a * inner], mat[(int64_t)j * A + a]);
+    out[t] = acc;
+  }
+}
+
+// ------------------------------------------------------------------- epilogue
+// y[b, o, p] = act(spec[b, o, p] + skip(x)[b, o, p]); spec may alias y.
+template <int OT>
+__global__ void __launch_bounds__(kThreads)
+k_epilogue(const float* spec, const float* __restrict__ x, const float* __restrict__ ws, float* y,
+           int B, int Ci, int Co, int64_t P, int skip_kind, int act) {
+  const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int o0 = blockIdx.y * OT;
+  const int b = blockIdx.z;
+  if (p >= P) return;
+  float acc[OT];
+#pragma unroll
+  for (int c = 0; c < OT; ++c) acc[c] = 0.f;
+  if (skip_kind == FNO_SKIP_LINEAR) {
+    const float* xb = x + (int64_t)b * Ci * P + p;
+    for (int i = 0; i < Ci; ++i) {
+      const float v = xb[(int64_t)i * P];
+#pragma unroll
+      for (int c = 0; c < OT; ++c)
+        if (o0 + c < Co) acc[c] = fmaf(ws[(int64_t)(o0 + c) * Ci + i], v, acc[c]);
+    }
+  } else if (skip_kind == FNO_SKIP_SOFT_GATING || skip_kind == FNO_SKIP_IDENTITY) {
+#pragma unroll
+    for (int c = 0; c < OT; ++c)
+      if (o0 + c < Co) {
+        const float v = x[((int64_t)b * Ci + o0 + c) * P + p];
+        acc[c] = (skip_kind == FNO_SKIP_SOFT_GATING) ? ws[o0 + c] * v : v;
+      }
+  }
+#pragma unroll
+  for (int c = 0; c < OT; ++c) {
+    if (o0 + c >= Co) break;
+    const int64_t idx = ((int64_t)b * Co + o0 + c) * P + p;
+    float v = spec[idx] + acc[c];
+    if (act == FNO_ACT_GELU) v = gelu_erf(v);
+    y[idx] = v;
+  }
+}
+
+// ============================================================== host helpers
+static int grid_for(int64_t total) {
+  int64_t g = (total + kThreads - 1) / kThreads;
+  if (g > 65536) g = 65536;
+  if (g < 1) g = 1;
+  return (int)g;
+}
+
+static int validate_axes(int32_t ndim, const int32_t* sizes, const int32_t* modes) {
+  FNO_CHECK_ARG(ndim >= 1 && ndim <= 3, "ndim must be 1..3 (got %d)", ndim);
+  FNO_CHECK_ARG(sizes && modes, "sizes/modes must not be NULL");
+  for (int d = 0; d < ndim; ++d) {
+    FNO_CHECK_ARG(sizes[d] >= 1, "size[%d]=%d must be positive", d, sizes[d]);
+    const int cap = (d == ndim - 1) ? sizes[d] / 2 + 1 : sizes[d];
+    FNO_CHECK_ARG(modes[d] >= 1 && modes[d] <= cap, "modes[%d]=%d outside [1, %d]", d, modes[d],
+                  cap);
+  }
+  for (int d = 0; d < ndim; ++d) {
+    if (sizes[d] > kMaxAxis) {
+      set_error("axis %d has size %d > %d supported by the generic kernels", d, sizes[d], kMaxAxis);
+      return FNO_ERR_UNSUPPORTED;
+    }
+  }
+  return FNO_OK;
+}
+
+// elements of the intermediate after the forward transform of axes d..ndim-1
+// (axes before d still full size)
+static int64_t fwd_stage_elems(int64_t planes, int32_t ndim, const int32_t* sizes,
+                               const int32_t* modes, int first_done) {
+  int64_t e = planes;
+  for (int d = 0; d < ndim; ++d) e *= (d >= first_done) ? modes[d] : sizes[d];
+  return e;
+}
+
+int rfft_window(const float* x, float2* xhat, int64_t planes, int32_t ndim, const int32_t* sizes,
+                const int32_t* modes, int32_t norm, void* ws, size_t ws_bytes, hipStream_t st) {
+  // stage s transforms axis (ndim-1-s); stage outputs go to the workspace
+  // (two alternating buffers), the last one to xhat.
+  const double scale = forward_scale(norm, sizes, ndim);
+  const int64_t e0 = fwd_stage_elems(planes, ndim, sizes, modes, ndim - 1);
+  const int64_t e1 = ndim == 3 ? fwd_stage_elems(planes, ndim, sizes, modes, ndim - 2) : 0;
+  const size_t need = (ndim > 1 ? (size_t)e0 * sizeof(float2) : 0) + (size_t)e1 * sizeof(float2);
+  if (ws_bytes < need) {
+    set_error("rfft_window: workspace %zu < %zu bytes", ws_bytes, need);
+    return FNO_ERR_WORKSPACE;
+  }
+  float2* bufA = reinterpret_cast<float2*>(ws);
+  float2* bufB = bufA + e0;
+  // last axis
+  {
+    const int N = sizes[ndim - 1], m = modes[ndim - 1];
+    int64_t rows = planes;
+    for (int d = 0; d < ndim - 1; ++d) rows *= sizes[d];
+    int rpb = (int)((48 * 1024 - 8 * N) / (4 * N));
+    if (rpb < 1) rpb = 1;
+    if (rpb > 64) rpb = 64;
+    const size_t lds = (size_t)N * 8 + (size_t)rpb * N * 4;
+    float2* dst = ndim == 1 ? xhat : bufA;
+    const int64_t blocks = (rows + rpb - 1) / rpb;
+    // only the last stage of the chain carries the scale
+    const float sc = (ndim == 1) ? (float)scale : 1.f;
+    hipLaunchKernelGGL(k_r2c_direct, dim3((unsigned)blocks), dim3(kThreads), lds, st, x, dst, rows,
+                       N, m, rpb, sc);
+    int rc = launch_status("k_r2c_direct");
+    if (rc) return rc;
+  }
+  // middle axes, innermost first
+  const float2* src = bufA;
+  for (int d = ndim - 2; d >= 0; --d) {
+    int64_t outer = planes;
+    for (int a = 0; a < d; ++a) outer *= sizes[a];
+    int64_t inner = 1;
+    for (int a = d + 1; a < ndim; ++a) inner *= modes[a];
+    const int N = sizes[d], m = modes[d];
+    float2* dst = (d == 0) ? xhat : bufB;
+    const float sc = (d == 0) ? (float)scale : 1.f;
+    hipLaunchKernelGGL(k_c2c_fwd_direct, dim3(grid_for(outer * m * inner)), dim3(kThreads),
+                       (size_t)N * 8, st, src, dst, outer, N, inner, m, sc);
+    int rc = launch_status("k_c2c_fwd_direct");
+    if (rc) return rc;
+    src = dst;
+  }
+  return FNO_OK;
+}
+
+int irfft_window(const float2* yhat, const float* bias, float* y, int64_t batch, int32_t channels,
+                 int32_t ndim, const int32_t* in_sizes, const int32_t* out_sizes,
+                 const int32_t* modes, int32_t norm, int32_t enforce, void* ws, size_t ws_bytes,
+                 hipStream_t st) {
+  const int64_t planes = batch * channels;
+  const double scale = inverse_scale(norm, out_sizes, ndim);
+  // stage d (d < ndim-1) expands axis d to out_sizes[d]
+  int64_t eA = 0, eB = 0;
+  if (ndim >= 2) {
+    eA = planes * out_sizes[0];
+    for (int a = 1; a < ndim; ++a) eA *= modes[a];
+  }
+  if (ndim == 3) eB = planes * out_sizes[0] * out_sizes[1] * modes[2];
+  const size_t need = (size_t)(eA + eB) * sizeof(float2);
+  if (ws_bytes < need) {
+    set_error("irfft_window: workspace %zu < %zu bytes", ws_bytes, need);
+    return FNO_ERR_WORKSPACE;
+  }
+  float2* bufA = reinterpret_cast<float2*>(ws);
+  float2* bufB = bufA + eA;
+  const float2* src = yhat;
+  for (int d = 0; d < ndim - 1; ++d) {
+    int64_t outer = planes;
+    for (int a = 0; a < d; ++a) outer *= out_sizes[a];
+    int64_t inner = 1;
+    for (int a = d + 1; a < ndim; ++a) inner *= modes[a];
+    float2* dst = (d == 0) ? bufA : bufB;
+    const int N = in_sizes[d], Np = out_sizes[d], m = modes[d];
+    hipLaunchKernelGGL(k_c2c_inv_direct, dim3(grid_for(outer * Np * inner)), dim3(kThreads),
+                       (size_t)Np * 8, st, src, dst, outer, N, Np, inner, m, 1.f);
+    int rc = launch_status("k_c2c_inv_direct");
+    if (rc) return rc;
+    src = dst;
+  }
+  {
+    int64_t rows = planes;
+    for (int a = 0; a < ndim - 1; ++a) rows *= out_sizes[a];
+    const int N = in_sizes[ndim - 1], Np = out_sizes[ndim - 1], m = modes[ndim - 1];
+    const int K = m < Np / 2 + 1 ? m : Np / 2 + 1;
+    int rpb = kThreads / (Np < kThreads ? Np : kThreads);
+    if (rpb < 1) rpb = 1;
+    if (rpb > 32) rpb = 32;
+    const size_t lds = (size_t)Np * 8 + (size_t)rpb * K * 8;
+    // rows run over (b, c, outer spatial...): the channel of a row is
+    // (row / rows_per_plane) mod channels
+    const int64_t rows_per_plane = rows / planes;
+    hipLaunchKernelGGL(k_c2r_direct, dim3((unsigned)((rows + rpb - 1) / rpb)), dim3(kThreads), lds,
+                       st, src, y, bias, rows, rows_per_plane, channels, N, Np, m, enforce, rpb,
+                       (float)scale);
+    int rc = launch_status("k_c2r_direct");
+    if (rc) return rc;
+  }
+  return FNO_OK;
+}
+
+int contract_dense(const float2* X, const float2* W, float2* Y, int B, int Ci, int Co, int64_t M,
+                   int64_t sWi, int64_t sWo, int64_t sWk, hipStream_t st) {
+  constexpr int TB = 4, TO = 8;
+  const int nTiles = ((B + TB - 1) / TB) * ((Co + TO - 1) / TO);
+  const int wavesPerBlock = kThreads / 64;
+  dim3 grid((unsigned)((M + 63) / 64), (unsigned)((nTiles + wavesPerBlock - 1) / wavesPerBlock));
+  hipLaunchKernelGGL((k_contract_dense<TB, TO>), grid, dim3(kThreads), 0, st, X, W, Y, B, Ci, Co, M,
+                     sWi, sWo, sWk);
+  return launch_status("k_contract_dense");
+}
+
+int contract_separable(const float2* X, const float2* W, float2* Y, int B, int C, int64_t M,
+                       hipStream_t st) {
+  const int64_t total = (int64_t)B * C * M;
+  hipLaunchKernelGGL(k_contract_separable, dim3(grid_for(total)), dim3(kThreads), 0, st, X, W, Y,
+                     (int64_t)C * M, total);
+  return launch_status("k_contract_separable");
+}
+
+int axis_matmul(const float2* in, const float2* mat, float2* out, int64_t outer, int A, int J,
+                int64_t inner, hipStream_t st) {
+  hipLaunchKernelGGL(k_axis_matmul, dim3(grid_for(outer * J * inner)), dim3(kThreads), 0, st, in,
+                     mat, out, outer, A, J, inner);
+  return launch_status("k_axis_matmul");
+}
+
+int block_epilogue(const float* spec, const float* x, const float* ws, float* y, int B, int Ci,
+                   int Co, int64_t P, int skip_kind, int act, hipStream_t st) {
+  constexpr int OT = 16;
+  dim3 grid((unsigned)((P + kThreads - 1) / kThreads), (unsigned)((Co + OT - 1) / OT), (unsigned)B);
+  hipLaunchKernelGGL((k_epilogue<OT>), grid, dim3(kThreads), 0, st, spec, x, ws, y, B, Ci, Co, P,
+                     skip_kind, act);
+  return launch_status("k_epilogue");
+}
+
+int validate_window(int32_t ndim, const int32_t* sizes, const int32_t* modes) {
+  return validate_axes(ndim, sizes, modes);
+}
+
+size_t rfft_window_ws(int64_t planes, int32_t ndim, const int32_t* sizes, const int32_t* modes) {
+  if (ndim <= 1) return 0;
+  size_t e = (size_t)fwd_stage_elems(planes, ndim, sizes, modes, ndim - 1);
+  if (ndim == 3) e += (size_t)fwd_stage_elems(planes, ndim, sizes, modes, ndim - 2);
+  return e * sizeof(float2);
+}
+
+size_t irfft_window_ws(int64_t planes, int32_t ndim, const int32_t* out_sizes,
+                       const int32_t* modes) {
+  int64_t eA = 0, eB = 0;
+  if (ndim >= 2) {
+    eA = planes * out_sizes[0];
+    for (int a = 1; a < ndim; ++a) eA *= modes[a];
+  }
+  if (ndim == 3) eB = planes * out_sizes[0] * out_sizes[1] * modes[2];
+  return (size_t)(eA + eB) * sizeof(float2);
+}
+
+}  // namespace fno

@@ -1,0 +1,299 @@
+"""FNOBlocks on MI355X (neuralop/layers/fno_block.py:18-481).
+
+Post-activation forward (fno_block.py:327-381).  When the layer is
+  SpectralConv (this package's) + linear / soft-gating (no bias) / identity /
+  no skip, no norm, no stabilizer, GELU non-linearity, output size == input
+the spectral conv, bias, skip, add and first GELU run as ONE library call
+(fno_spectral_block_f32: fused 2D path or generic kernels).  Everything after
+it (channel MLP, its skip, second GELU) and every other configuration runs as
+torch ops around the HIP SpectralConv.
+"""
+from __future__ import annotations
+
+from typing import List, Union
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from . import _native as nat
+from .channel_mlp import ChannelMLP
+from .skip_connections import Flattened1dConv, SoftGating, skip_connection
+from .spectral_convolution import SpectralConv
+from .utils import get_active_profiler, maybe_profile, validate_scaling_factor
+
+Number = Union[int, float]
+
+
+class InstanceNorm(nn.Module):
+    """Instance norm over all spatial dims (neuralop normalization_layers)."""
+
+    def __init__(self, **kwargs):
+        super().__init__()
+        self.kwargs = kwargs
+
+    def forward(self, x):
+        size = x.shape
+        x = F.instance_norm(x, **self.kwargs)
+        assert x.shape == size
+        return x
+
+
+class BatchNorm(nn.Module):
+    def __init__(self, n_dim: int, num_features: int, **kwargs):
+        super().__init__()
+        cls = {1: nn.BatchNorm1d, 2: nn.BatchNorm2d, 3: nn.BatchNorm3d}.get(n_dim)
+        if cls is None:
+            raise NotImplementedError(f"BatchNorm for {n_dim} dims")
+        self.norm = cls(num_features=num_features, **kwargs)
+
+    def forward(self, x):
+        return self.norm(x)
+
+
+class FNOBlocks(nn.Module):
+    def __init__(
+        self,
+        in_channels,
+        out_channels,
+        n_modes,
+        resolution_scaling_factor=None,
+        n_layers=1,
+        max_n_modes=None,
+        fno_block_precision="full",
+        use_channel_mlp=True,
+        channel_mlp_dropout=0,
+        channel_mlp_expansion=0.5,
+        non_linearity=F.gelu,
+        stabilizer=None,
+        norm=None,
+        norm_groups=1,
+        ada_in_features=None,
+        preactivation=False,
+        fno_skip="linear",
+        channel_mlp_skip="soft-gating",
+        complex_data=False,
+        separable=False,
+        factorization=None,
+        rank=1.0,
+        conv_module=SpectralConv,
+        fixed_rank_modes=False,
+        implementation="factorized",
+        decomposition_kwargs=dict(),
+        enforce_hermitian_symmetry=True,
+    ):
+        super().__init__()
+        if isinstance(n_modes, int):
+            n_modes = [n_modes]
+        self._n_modes = n_modes
+        self.n_dim = len(n_modes)
+        self.resolution_scaling_factor = validate_scaling_factor(resolution_scaling_factor, self.n_dim,
+                                                                 n_layers)
+        self.max_n_modes = max_n_modes
+        self.fno_block_precision = fno_block_precision
+        self.in_channels = in_channels
+        self.out_channels = out_channels
+        self.n_layers = n_layers
+        self.stabilizer = stabilizer
+        self.rank = rank
+        self.factorization = factorization
+        self.fixed_rank_modes = fixed_rank_modes
+        self.decomposition_kwargs = decomposition_kwargs
+        self.fno_skip = fno_skip
+        self.channel_mlp_skip = channel_mlp_skip
+        self.complex_data = complex_data
+        self.use_channel_mlp = use_channel_mlp
+        self.channel_mlp_expansion = channel_mlp_expansion
+        self.channel_mlp_dropout = channel_mlp_dropout
+        self.implementation = implementation
+        self.separable = separable
+        self.preactivation = preactivation
+        self.ada_in_features = ada_in_features
+        self.enforce_hermitian_symmetry = enforce_hermitian_symmetry
+        if complex_data:
+            raise NotImplementedError("complex_data=True FNO blocks are not built")
+        self.non_linearity = non_linearity
+
+        self.convs = nn.ModuleList([
+            conv_module(
+                self.in_channels,
+                self.out_channels,
+                self.n_modes,
+                resolution_scaling_factor=(self.resolution_scaling_factor[i]
+                                           if resolution_scaling_factor is not None else None),
+                max_n_modes=max_n_modes,
+                rank=rank,
+                fixed_rank_modes=fixed_rank_modes,
+                implementation=implementation,
+                separable=separable,
+                factorization=factorization,
+                fno_block_precision=fno_block_precision,
+                decomposition_kwargs=decomposition_kwargs,
+                complex_data=complex_data,
+                **({"enforce_hermitian_symmetry": enforce_hermitian_symmetry}
+                   if issubclass(conv_module, SpectralConv) else {}),
+            )
+            for i in range(n_layers)
+        ])
+        for i, conv in enumerate(self.convs):
+            setattr(conv, "profile_prefix", f"fno_blocks/{i}/spectral_conv")
+
+        if fno_skip is not None:
+            self.fno_skips = nn.ModuleList([
+                skip_connection(self.in_channels, self.out_channels, skip_type=fno_skip,
+                                n_dim=self.n_dim) for _ in range(n_layers)])
+        else:
+            self.fno_skips = None
+
+        if self.use_channel_mlp:
+            self.channel_mlp = nn.ModuleList([
+                ChannelMLP(in_channels=self.out_channels,
+                           hidden_channels=round(self.out_channels * channel_mlp_expansion),
+                           dropout=channel_mlp_dropout, n_dim=self.n_dim)
+                for _ in range(n_layers)])
+            if channel_mlp_skip is not None:
+                self.channel_mlp_skips = nn.ModuleList([
+                    skip_connection(self.in_channels, self.out_channels, skip_type=channel_mlp_skip,
+                                    n_dim=self.n_dim) for _ in range(n_layers)])
+            else:
+                self.channel_mlp_skips = None
+
+        self.n_norms = 2
+        if norm is None:
+            self.norm = None
+        elif norm == "instance_norm":
+            self.norm = nn.ModuleList([InstanceNorm() for _ in range(n_layers * self.n_norms)])
+        elif norm == "group_norm":
+            self.norm = nn.ModuleList([nn.GroupNorm(num_groups=norm_groups, num_channels=self.out_channels)
+                                       for _ in range(n_layers * self.n_norms)])
+        elif norm == "batch_norm":
+            self.norm = nn.ModuleList([BatchNorm(n_dim=self.n_dim, num_features=self.out_channels)
+                                       for _ in range(n_layers * self.n_norms)])
+        elif norm == "ada_in":
+            raise NotImplementedError("ada_in norm is not built")
+        else:
+            raise ValueError(f"Got norm={norm} but expected None or one of "
+                             "[instance_norm, group_norm, batch_norm, ada_in]")
+
+    # ------------------------------------------------------------------ fused
+    def _fused_skip(self, index):
+        """(skip_kind, skip_weight) if the fno skip can run inside the kernel."""
+        if self.fno_skips is None:
+            return nat.SKIP_NONE, None
+        s = self.fno_skips[index]
+        if isinstance(s, Flattened1dConv) and s.conv.bias is None:
+            return nat.SKIP_LINEAR, s.conv.weight.reshape(s.conv.out_channels, -1)
+        if isinstance(s, SoftGating) and s.bias is None:
+            return nat.SKIP_SOFT_GATING, s.weight.reshape(-1)
+        if isinstance(s, nn.Identity):
+            return nat.SKIP_IDENTITY, None
+        return None, None
+
+    def _can_fuse(self, x, index, output_shape):
+        conv = self.convs[index]
+        if not isinstance(conv, SpectralConv) or not x.is_cuda:
+            return False
+        if self.norm is not None or self.stabilizer is not None or self.preactivation:
+            return False
+        if self.non_linearity is not F.gelu:
+            return False
+        if output_shape is not None or conv.resolution_scaling_factor is not None:
+            return False
+        kind, _ = self._fused_skip(index)
+        return kind is not None
+
+    def forward(self, x, index=0, output_shape=None):
+        if self.preactivation:
+            return self.forward_with_preactivation(x, index, output_shape)
+        return self.forward_with_postactivation(x, index, output_shape)
+
+    def forward_with_postactivation(self, x, index=0, output_shape=None):
+        profiler = get_active_profiler()
+        prefix = f"fno_blocks/{index}"
+        if self.use_channel_mlp and self.channel_mlp_skips is not None:
+            with maybe_profile(profiler, f"{prefix}/channel_mlp_skip", x.device):
+                x_skip_channel_mlp = self.channel_mlp_skips[index](x)
+                x_skip_channel_mlp = self.convs[index].transform(x_skip_channel_mlp,
+                                                                 output_shape=output_shape)
+        act0 = index < (self.n_layers - 1)
+        if self._can_fuse(x, index, output_shape):
+            kind, sw = self._fused_skip(index)
+            with maybe_profile(profiler, f"{prefix}/spectral_block", x.device):
+                x = self.convs[index]._forward_hip(x, None, kind, sw,
+                                                   nat.ACT_GELU if act0 else nat.ACT_NONE)
+        else:
+            if self.fno_skips is not None:
+                with maybe_profile(profiler, f"{prefix}/fno_skip", x.device):
+                    x_skip_fno = self.fno_skips[index](x)
+                    x_skip_fno = self.convs[index].transform(x_skip_fno, output_shape=output_shape)
+            if self.stabilizer == "tanh":
+                x = torch.tanh(x)
+            x_fno = self.convs[index](x, output_shape=output_shape)
+            if self.norm is not None:
+                x_fno = self.norm[self.n_norms * index](x_fno)
+            x = x_fno + x_skip_fno if self.fno_skips is not None else x_fno
+            if act0:
+                x = self.non_linearity(x)
+        if self.use_channel_mlp:
+            with maybe_profile(profiler, f"{prefix}/channel_mlp", x.device):
+                x = self.channel_mlp[index](x)
+            if self.channel_mlp_skips is not None:
+                x = x + x_skip_channel_mlp
+        if self.norm is not None:
+            x = self.norm[self.n_norms * index + 1](x)
+        if index < (self.n_layers - 1):
+            with maybe_profile(profiler, f"{prefix}/activation_1", x.device):
+                x = self.non_linearity(x)
+        return x
+
+    def forward_with_preactivation(self, x, index=0, output_shape=None):
+        """fno_block.py:383-437 (torch glue around the HIP SpectralConv)."""
+        x = self.non_linearity(x)
+        if self.norm is not None:
+            x = self.norm[self.n_norms * index](x)
+        if self.fno_skips is not None:
+            x_skip_fno = self.convs[index].transform(self.fno_skips[index](x), output_shape=output_shape)
+        if self.use_channel_mlp and self.channel_mlp_skips is not None:
+            x_skip_channel_mlp = self.convs[index].transform(self.channel_mlp_skips[index](x),
+                                                             output_shape=output_shape)
+        if self.stabilizer == "tanh":
+            x = torch.tanh(x)
+        x_fno = self.convs[index](x, output_shape=output_shape)
+        x = x_fno + x_skip_fno if self.fno_skips is not None else x_fno
+        if index < (self.n_layers - 1):
+            x = self.non_linearity(x)
+        if self.norm is not None:
+            x = self.norm[self.n_norms * index + 1](x)
+        if self.use_channel_mlp:
+            x = self.channel_mlp[index](x)
+            if self.channel_mlp_skips is not None:
+                x = x + x_skip_channel_mlp
+        return x
+
+    @property
+    def n_modes(self):
+        return self._n_modes
+
+    @n_modes.setter
+    def n_modes(self, n_modes):
+        for i in range(self.n_layers):
+            self.convs[i].n_modes = n_modes
+        self._n_modes = n_modes
+
+    def get_block(self, indices):
+        if self.n_layers == 1:
+            raise ValueError("A single layer is parametrized, directly use the main class.")
+        return SubModule(self, indices)
+
+    def __getitem__(self, indices):
+        return self.get_block(indices)
+
+
+class SubModule(nn.Module):
+    def __init__(self, main_module, indices):
+        super().__init__()
+        self.main_module = main_module
+        self.indices = indices
+
+    def forward(self, x):
+        return self.main_module.forward(x, self.indices)

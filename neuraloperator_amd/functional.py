@@ -1,0 +1,174 @@
+"""Tensor-level wrappers over the C ABI of libfnohip.so.
+
+Every function takes CUDA (HIP) tensors, enqueues work on torch's current
+stream and returns new tensors allocated by torch.  Inputs are made
+contiguous float32 / complex64 first.  Nothing here computes on the CPU:
+a CPU tensor or a missing library raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Sequence
+
+import torch
+
+from . import _native as nat
+
+
+def _require_gpu(*tensors):
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(
+                "neuraloperator_amd runs the FNO spectral path only on the GPU (HIP); "
+                f"got a tensor on {t.device}")
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def _stream(device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _workspace(nbytes: int, device):
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def _f32(t):
+    return t.contiguous() if t.dtype == torch.float32 else t.float().contiguous()
+
+
+def _c64(t):
+    return t.contiguous() if t.dtype == torch.complex64 else t.to(torch.complex64).contiguous()
+
+
+def rfft_window(x: torch.Tensor, modes: Sequence[int], fft_norm: str = "forward") -> torch.Tensor:
+    """Kept-mode window of rfftn(x) in fftshift-ed window order.
+    x [B, C, *S] -> complex64 [B, C, *modes]."""
+    _require_gpu(x)
+    lib = nat.load()
+    x = _f32(x)
+    B, C, *S = x.shape
+    nd = len(S)
+    planes = B * C
+    out = torch.empty((B, C, *modes), dtype=torch.complex64, device=x.device)
+    sz, md = nat.i32_array(S), nat.i32_array(modes)
+    wsb = lib.fno_rfft_window_workspace_bytes(planes, nd, sz, md)
+    ws = _workspace(wsb, x.device)
+    nat.check(lib.fno_rfft_window_f32(_ptr(x), _ptr(out), planes, nd, sz, md, nat.NORMS[fft_norm],
+                                      _ptr(ws), wsb, _stream(x.device)), "fno_rfft_window_f32")
+    return out
+
+
+def contract_dense(xhat: torch.Tensor, weight: torch.Tensor, separable: bool = False) -> torch.Tensor:
+    """Mode-wise contraction of the window spectrum with a dense weight window."""
+    _require_gpu(xhat, weight)
+    lib = nat.load()
+    xhat, weight = _c64(xhat), _c64(weight)
+    B, Ci, *modes = xhat.shape
+    Co = Ci if separable else weight.shape[1]
+    M = 1
+    for m in modes:
+        M *= m
+    out = torch.empty((B, Co, *modes), dtype=torch.complex64, device=xhat.device)
+    nat.check(lib.fno_contract_dense_c64(_ptr(xhat), _ptr(weight), _ptr(out), B, Ci, Co, M,
+                                         int(bool(separable)), _stream(xhat.device)),
+              "fno_contract_dense_c64")
+    return out
+
+
+def contract_tucker(xhat: torch.Tensor, core: torch.Tensor, factors: Sequence[torch.Tensor]) -> torch.Tensor:
+    """Tucker-factorized contraction; factors = [U_in, U_out, U_1..U_d] with
+    the mode factors already cut to the window rows."""
+    _require_gpu(xhat, core, *factors)
+    lib = nat.load()
+    xhat = _c64(xhat)
+    core = _c64(core)
+    factors = [_c64(f) for f in factors]
+    B, Ci, *modes = xhat.shape
+    nd = len(modes)
+    Co = factors[1].shape[0]
+    ranks = list(core.shape)
+    out = torch.empty((B, Co, *modes), dtype=torch.complex64, device=xhat.device)
+    fp = (ctypes.c_void_p * len(factors))(*[f.data_ptr() for f in factors])
+    md, rk = nat.i32_array(modes), nat.i32_array(ranks)
+    wsb = lib.fno_contract_tucker_workspace_bytes(B, nd, md, rk)
+    ws = _workspace(wsb, xhat.device)
+    nat.check(lib.fno_contract_tucker_c64(_ptr(xhat), _ptr(core), fp, rk, _ptr(out), B, Ci, Co, nd,
+                                          md, _ptr(ws), wsb, _stream(xhat.device)),
+              "fno_contract_tucker_c64")
+    return out
+
+
+def irfft_window(yhat: torch.Tensor, in_sizes: Sequence[int], out_sizes: Sequence[int],
+                 bias: Optional[torch.Tensor] = None, fft_norm: str = "forward",
+                 enforce_hermitian_symmetry: bool = True) -> torch.Tensor:
+    """Real field of size out_sizes from a window spectrum (+ bias)."""
+    _require_gpu(yhat, bias)
+    lib = nat.load()
+    yhat = _c64(yhat)
+    B, C, *modes = yhat.shape
+    nd = len(modes)
+    y = torch.empty((B, C, *out_sizes), dtype=torch.float32, device=yhat.device)
+    b = _f32(bias.reshape(-1)) if bias is not None else None
+    isz, osz, md = nat.i32_array(in_sizes), nat.i32_array(out_sizes), nat.i32_array(modes)
+    wsb = lib.fno_irfft_window_workspace_bytes(B * C, nd, osz, md)
+    ws = _workspace(wsb, yhat.device)
+    nat.check(lib.fno_irfft_window_f32(_ptr(yhat), _ptr(b), _ptr(y), B, C, nd, isz, osz, md,
+                                       nat.NORMS[fft_norm], int(bool(enforce_hermitian_symmetry)),
+                                       _ptr(ws), wsb, _stream(yhat.device)),
+              "fno_irfft_window_f32")
+    return y
+
+
+def block_epilogue(spec: torch.Tensor, x: Optional[torch.Tensor], skip_kind: int,
+                   skip_weight: Optional[torch.Tensor], act: int, out: Optional[torch.Tensor] = None):
+    """act(spec + skip(x)); writes into ``out`` (default: spec itself)."""
+    _require_gpu(spec, x, skip_weight)
+    lib = nat.load()
+    spec = _f32(spec)
+    y = spec if out is None else out
+    B, Co, *S = spec.shape
+    Ci = x.shape[1] if x is not None else Co
+    P = 1
+    for s in S:
+        P *= s
+    xx = _f32(x) if x is not None else None
+    w = _f32(skip_weight.reshape(-1)) if skip_weight is not None else None
+    nat.check(lib.fno_block_epilogue_f32(_ptr(spec), _ptr(xx), _ptr(w), _ptr(y), B, Ci, Co, P,
+                                         skip_kind, act, _stream(spec.device)),
+              "fno_block_epilogue_f32")
+    return y
+
+
+def spectral_block_is_fused(B, Ci, Co, sizes, modes, skip_kind) -> bool:
+    lib = nat.load()
+    return bool(lib.fno_spectral_block_is_fused(B, Ci, Co, len(sizes), nat.i32_array(sizes),
+                                                nat.i32_array(modes), skip_kind))
+
+
+def spectral_block(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor],
+                   modes: Sequence[int], skip_kind: int = nat.SKIP_NONE,
+                   skip_weight: Optional[torch.Tensor] = None, act: int = nat.ACT_NONE,
+                   fft_norm: str = "forward", out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y = act(SpectralConv(x) + skip(x)), output size == input size, dense
+    weight window [Ci, Co, *modes]."""
+    _require_gpu(x, weight, bias, skip_weight)
+    lib = nat.load()
+    x = _f32(x)
+    weight = _c64(weight)
+    B, Ci, *S = x.shape
+    Co = weight.shape[1]
+    nd = len(S)
+    y = out if out is not None else torch.empty((B, Co, *S), dtype=torch.float32, device=x.device)
+    b = _f32(bias.reshape(-1)) if bias is not None else None
+    w = _f32(skip_weight.reshape(-1)) if skip_weight is not None else None
+    sz, md = nat.i32_array(S), nat.i32_array(modes)
+    wsb = lib.fno_spectral_block_workspace_bytes(B, Ci, Co, nd, sz, md)
+    ws = _workspace(wsb, x.device)
+    nat.check(lib.fno_spectral_block_f32(_ptr(x), _ptr(weight), _ptr(b), _ptr(w), _ptr(y), B, Ci, Co,
+                                         nd, sz, md, nat.NORMS[fft_norm], skip_kind, act, _ptr(ws),
+                                         wsb, _stream(x.device)),
+              "fno_spectral_block_f32")
+    return y

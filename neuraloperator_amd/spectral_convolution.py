@@ -1,0 +1,269 @@
+"""SpectralConv on MI355X: same module API as neuralop's SpectralConv
+(neuralop/layers/spectral_convolution.py:183-570), forward computed by the
+HIP kernels of libfnohip.so.
+
+Forward dispatch (all on the GPU, nothing in torch.fft):
+  * dense / reconstructed weight, output size == input size
+        -> fno_spectral_block_f32 (fused 2D FFT path when the plane allows it,
+           generic window transforms otherwise)
+  * output_shape / resolution_scaling_factor, separable, or a Tucker weight
+    contracted through its factors ('factorized')
+        -> fno_rfft_window_f32 -> contraction -> fno_irfft_window_f32
+CP / TT weights are reconstructed (torch ops on the weight only) and then
+contracted densely; the result is the same mathematics as the reference's
+factor-wise einsums (spectral_convolution.py:55-73, :106-132).
+
+Autograd: the HIP path is forward-only.  Calling backward through it raises.
+"""
+from __future__ import annotations
+
+from typing import List, Optional, Tuple, Union
+
+import torch
+from torch import nn
+
+from . import _native as nat
+from . import functional as Fh
+from .factorized_tensors import FactorizedTensor, TuckerTensor, _TuckerView
+from .resample import resample
+from .utils import get_active_profiler, maybe_profile, validate_scaling_factor
+
+Number = Union[int, float]
+
+
+class BaseSpectralConv(nn.Module):
+    """Abstract base (neuralop/layers/base_spectral_conv.py:4-27)."""
+
+    def __init__(self, device=None, dtype=None):
+        super().__init__()
+        self.dtype = dtype
+        self.device = device
+
+    def transform(self, x):
+        return x
+
+
+def get_contract_fun(weight, implementation="reconstructed", separable=False):
+    """Validates the implementation / factorization pair the way
+    spectral_convolution.py:135-177 does and names the contraction used."""
+    if implementation == "reconstructed":
+        return "dense_separable" if separable else "dense"
+    if implementation == "factorized":
+        if torch.is_tensor(weight):
+            return "dense"
+        if isinstance(weight, FactorizedTensor):
+            name = weight.name.lower()
+            if name.endswith("dense"):
+                return "dense"
+            if name.endswith("tucker"):
+                return "tucker"
+            if name.endswith("tt"):
+                return "tt"
+            if name.endswith("cp"):
+                return "cp"
+            raise ValueError(f"Got unexpected factorized weight type {weight.name}")
+        raise ValueError(f"Got unexpected weight type of class {weight.__class__.__name__}")
+    raise ValueError(
+        f'Got implementation={implementation}, expected "reconstructed" or "factorized"')
+
+
+class _NoGradThroughHip(torch.autograd.Function):
+    """Attaches the HIP forward result to the graph with a backward that
+    raises: the backward kernels of the spectral path are not built."""
+
+    @staticmethod
+    def forward(ctx, y, *inputs):
+        return y
+
+    @staticmethod
+    def backward(ctx, *grads):
+        raise NotImplementedError(
+            "backward of the HIP spectral path is not implemented (forward-only build)")
+
+
+def _attach(y, *params):
+    if torch.is_grad_enabled() and any(p is not None and p.requires_grad for p in params):
+        return _NoGradThroughHip.apply(y, *[p for p in params if p is not None])
+    return y
+
+
+class SpectralConv(BaseSpectralConv):
+    """Spectral convolution of an FNO layer; constructor and attributes as in
+    neuralop/layers/spectral_convolution.py:285-381."""
+
+    def __init__(
+        self,
+        in_channels,
+        out_channels,
+        n_modes,
+        complex_data=False,
+        max_n_modes=None,
+        bias=True,
+        separable=False,
+        resolution_scaling_factor: Optional[Union[Number, List[Number]]] = None,
+        fno_block_precision="full",
+        rank=1.0,
+        factorization=None,
+        implementation="reconstructed",
+        enforce_hermitian_symmetry=True,
+        fixed_rank_modes=False,
+        decomposition_kwargs: Optional[dict] = None,
+        init_std="auto",
+        fft_norm="forward",
+        device=None,
+    ):
+        super().__init__(device=device)
+        self.in_channels = in_channels
+        self.out_channels = out_channels
+        self.complex_data = complex_data
+        self.n_modes = n_modes
+        self.order = len(self.n_modes)
+        if max_n_modes is None:
+            max_n_modes = self.n_modes
+        elif isinstance(max_n_modes, int):
+            max_n_modes = [max_n_modes]
+        self.max_n_modes = max_n_modes
+        self.fno_block_precision = fno_block_precision
+        self.rank = rank
+        self.factorization = factorization
+        self.implementation = implementation
+        self.enforce_hermitian_symmetry = enforce_hermitian_symmetry
+        self.resolution_scaling_factor = validate_scaling_factor(resolution_scaling_factor, self.order)
+        if init_std == "auto":
+            init_std = (2 / (in_channels + out_channels)) ** 0.5
+        if isinstance(fixed_rank_modes, bool):
+            fixed_rank_modes = [0] if fixed_rank_modes else None
+        if fft_norm not in nat.NORMS:
+            raise ValueError(f"fft_norm must be one of {sorted(nat.NORMS)}, got {fft_norm}")
+        self.fft_norm = fft_norm
+        if factorization is None:
+            factorization = "Dense"
+        if separable:
+            if in_channels != out_channels:
+                raise ValueError(
+                    "To use separable Fourier Conv, in_channels must be equal "
+                    f"to out_channels, but got in_channels={in_channels} and "
+                    f"out_channels={out_channels}")
+            weight_shape = (in_channels, *max_n_modes)
+        else:
+            weight_shape = (in_channels, out_channels, *max_n_modes)
+        self.separable = separable
+        tensor_kwargs = decomposition_kwargs if decomposition_kwargs is not None else {}
+        self.weight = FactorizedTensor.new(weight_shape, rank=self.rank, factorization=factorization,
+                                           fixed_rank_modes=fixed_rank_modes, dtype=torch.cfloat,
+                                           **tensor_kwargs)
+        self.weight.normal_(0, init_std)
+        self._contract = get_contract_fun(self.weight, implementation=implementation,
+                                          separable=separable)
+        if bias:
+            self.bias = nn.Parameter(init_std * torch.randn(*((self.out_channels,) + (1,) * self.order)))
+        else:
+            self.bias = None
+        if device is not None:
+            self.to(device)
+
+    # ---------------------------------------------------------------- API
+    def transform(self, x, output_shape=None):
+        """Resample the skip input to the output resolution (:383-398)."""
+        in_shape = list(x.shape[2:])
+        if self.resolution_scaling_factor is not None and output_shape is None:
+            out_shape = [round(s * r) for s, r in zip(in_shape, self.resolution_scaling_factor)]
+        elif output_shape is not None:
+            out_shape = list(output_shape)
+        else:
+            out_shape = in_shape
+        if in_shape == out_shape:
+            return x
+        return resample(x, 1.0, list(range(2, x.ndim)), output_shape=out_shape)
+
+    @property
+    def n_modes(self):
+        return self._n_modes
+
+    @n_modes.setter
+    def n_modes(self, n_modes):
+        """Last entry becomes n//2+1 for real data (:404-415)."""
+        if isinstance(n_modes, int):
+            n_modes = [n_modes]
+        else:
+            n_modes = list(n_modes)
+        if not self.complex_data:
+            n_modes[-1] = n_modes[-1] // 2 + 1
+        self._n_modes = n_modes
+
+    # ------------------------------------------------------ window bookkeeping
+    def window(self, spatial_sizes) -> Tuple[List[int], tuple]:
+        """Kept mode counts and the weight slice for an input of the given
+        spatial size (:464-489): kept_d = min(fft_size_d, n_modes_d); on every
+        axis but the last the weight window starts (max_d - kept_d) // 2 in."""
+        fft_size = list(spatial_sizes)
+        if not self.complex_data:
+            fft_size[-1] = fft_size[-1] // 2 + 1
+        starts = [mx - min(s, n) for s, n, mx in zip(fft_size, self.n_modes, self.max_n_modes)]
+        sl = [slice(None)] if self.separable else [slice(None), slice(None)]
+        sl += [slice(s // 2, -s // 2) if s else slice(s, None) for s in starts[:-1]]
+        sl += [slice(None, -starts[-1]) if starts[-1] else slice(None)]
+        kept = [mx - s for mx, s in zip(self.max_n_modes, starts)]
+        return kept, tuple(sl)
+
+    def output_sizes(self, spatial_sizes, output_shape=None) -> List[int]:
+        sizes = list(spatial_sizes)
+        if self.resolution_scaling_factor is not None and output_shape is None:
+            sizes = [round(s * r) for s, r in zip(sizes, self.resolution_scaling_factor)]
+        if output_shape is not None:
+            sizes = list(output_shape)
+        return [int(s) for s in sizes]
+
+    def dense_window_weight(self, sl) -> torch.Tensor:
+        """The weight window as a dense complex tensor (reconstructing a
+        factorized weight when needed)."""
+        w = self.weight[sl] if isinstance(self.weight, FactorizedTensor) else self.weight[sl]
+        w = w.to_tensor() if isinstance(w, FactorizedTensor) else w
+        return w
+
+    # ---------------------------------------------------------------- forward
+    def forward(self, x: torch.Tensor, output_shape: Optional[Tuple[int]] = None):
+        if not x.is_cuda:
+            raise RuntimeError(
+                "SpectralConv (neuraloperator_amd) runs on the GPU only; move the module and "
+                "input to a HIP device")
+        if self.complex_data:
+            raise NotImplementedError("complex_data=True spectral path is not built")
+        profiler = get_active_profiler()
+        name = getattr(self, "profile_prefix", "spectral_conv")
+        with maybe_profile(profiler, name, x.device):
+            return self._forward_hip(x, output_shape)
+
+    def _forward_hip(self, x, output_shape=None, skip_kind=nat.SKIP_NONE, skip_weight=None,
+                     act=nat.ACT_NONE):
+        sizes = list(x.shape[2:])
+        kept, sl = self.window(sizes)
+        out_sizes = self.output_sizes(sizes, output_shape)
+        bias = self.bias.reshape(-1) if self.bias is not None else None
+        same_size = out_sizes == sizes
+        kind = self._contract
+        params = [self.bias] + list(self.weight.parameters()) + [skip_weight]
+        if kind in ("dense", "cp", "tt") and same_size and not self.separable:
+            w = self.dense_window_weight(sl).detach()
+            y = Fh.spectral_block(x.detach(), w, None if bias is None else bias.detach(), kept,
+                                  skip_kind, None if skip_weight is None else skip_weight.detach(),
+                                  act, self.fft_norm)
+            return _attach(y, x, *params)
+        # composed path: window transform, contraction, inverse window transform
+        xhat = Fh.rfft_window(x.detach(), kept, self.fft_norm)
+        if kind == "tucker" and not self.separable:
+            wv = self.weight[sl]
+            core = wv.core.detach()
+            factors = [f.detach() for f in wv.factors]
+            yhat = Fh.contract_tucker(xhat, core, factors)
+        else:
+            w = self.dense_window_weight(sl).detach()
+            yhat = Fh.contract_dense(xhat, w, separable=self.separable)
+        y = Fh.irfft_window(yhat, sizes, out_sizes, None if bias is None else bias.detach(),
+                            self.fft_norm, self.enforce_hermitian_symmetry)
+        if skip_kind != nat.SKIP_NONE or act != nat.ACT_NONE:
+            if not same_size:
+                raise RuntimeError("fused skip requires output size == input size")
+            y = Fh.block_epilogue(y, x.detach(), skip_kind,
+                                  None if skip_weight is None else skip_weight.detach(), act)
+        return _attach(y, x, *params)

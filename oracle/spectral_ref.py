@@ -1,0 +1,476 @@
+"""Plain-torch CPU restatement of the reference FNO spectral path.
+
+TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).  Every function follows
+the reference op sequence one step at a time, citing the file:line it
+restates (paths relative to the reference repository root).
+"""
+from __future__ import annotations
+
+import math
+from typing import List, Optional, Sequence
+
+import torch
+import torch.nn.functional as F
+
+EINSUM_SYMBOLS = "abcdefghijklmnopqrstuvwxyzABCDEFGHIJKLMNOPQRSTUVWXYZ"
+
+
+# ---------------------------------------------------------------------------
+# n_modes bookkeeping
+# ---------------------------------------------------------------------------
+def stored_n_modes(n_modes, complex_data: bool = False) -> List[int]:
+    """n_modes as stored by the setter (spectral_convolution.py:404-415):
+    the last entry becomes n//2+1 for real data."""
+    if isinstance(n_modes, int):
+        n_modes = [n_modes]
+    else:
+        n_modes = list(n_modes)
+    if not complex_data:
+        n_modes[-1] = n_modes[-1] // 2 + 1
+    return n_modes
+
+
+def weight_slices(fft_size, n_modes, max_n_modes, separable=False, complex_data=False):
+    """Weight window (spectral_convolution.py:465-489)."""
+    starts = [
+        (max_modes - min(size, n_mode))
+        for (size, n_mode, max_modes) in zip(fft_size, n_modes, max_n_modes)
+    ]
+    sl = [slice(None)] if separable else [slice(None), slice(None)]
+    if complex_data:
+        sl += [slice(s // 2, -s // 2) if s else slice(s, None) for s in starts]
+    else:
+        sl += [slice(s // 2, -s // 2) if s else slice(s, None) for s in starts[:-1]]
+        sl += [slice(None, -starts[-1]) if starts[-1] else slice(None)]
+    return tuple(sl)
+
+
+def x_slices(fft_size, kept_modes):
+    """Input-spectrum window (spectral_convolution.py:500-519)."""
+    sl = [slice(None), slice(None)]
+    for all_modes, kept in zip(fft_size, kept_modes):
+        center = all_modes // 2
+        neg = kept // 2
+        pos = kept // 2 + kept % 2
+        sl.append(slice(center - neg, center + pos))
+    if kept_modes[-1] < fft_size[-1]:
+        sl[-1] = slice(None, kept_modes[-1])
+    else:
+        sl[-1] = slice(None)
+    return tuple(sl)
+
+
+# ---------------------------------------------------------------------------
+# contractions
+# ---------------------------------------------------------------------------
+def contract_dense(x, weight, separable=False):
+    """spectral_convolution.py:21-46 (tl.einsum -> opt_einsum -> torch)."""
+    order = x.ndim
+    x_syms = list(EINSUM_SYMBOLS[:order])
+    weight_syms = list(x_syms[1:])
+    if separable:
+        out_syms = [x_syms[0]] + list(weight_syms)
+    else:
+        weight_syms.insert(1, EINSUM_SYMBOLS[order])
+        out_syms = list(weight_syms)
+        out_syms[0] = x_syms[0]
+    eq = f'{"".join(x_syms)},{"".join(weight_syms)}->{"".join(out_syms)}'
+    return torch.einsum(eq, x, weight)
+
+
+def contract_dense_separable(x, weight, separable=True):
+    """spectral_convolution.py:49-52."""
+    return x * weight
+
+
+def contract_tucker(x, core, factors, separable=False):
+    """spectral_convolution.py:76-103 (einsum with core and all factors)."""
+    order = x.ndim
+    x_syms = str(EINSUM_SYMBOLS[:order])
+    out_sym = EINSUM_SYMBOLS[order]
+    out_syms = list(x_syms)
+    if separable:
+        core_syms = EINSUM_SYMBOLS[order + 1: 2 * order]
+        factor_syms = [xs + rs for (xs, rs) in zip(x_syms[1:], core_syms)]
+    else:
+        core_syms = EINSUM_SYMBOLS[order + 1: 2 * order + 1]
+        out_syms[1] = out_sym
+        factor_syms = [EINSUM_SYMBOLS[1] + core_syms[0], out_sym + core_syms[1]]
+        factor_syms += [xs + rs for (xs, rs) in zip(x_syms[2:], core_syms[2:])]
+    eq = f'{x_syms},{core_syms},{",".join(factor_syms)}->{"".join(out_syms)}'
+    return torch.einsum(eq, x, core, *factors)
+
+
+def contract_cp(x, weights, factors, separable=False):
+    """spectral_convolution.py:55-73."""
+    order = x.ndim
+    x_syms = str(EINSUM_SYMBOLS[:order])
+    rank_sym = EINSUM_SYMBOLS[order]
+    out_sym = EINSUM_SYMBOLS[order + 1]
+    out_syms = list(x_syms)
+    if separable:
+        factor_syms = [EINSUM_SYMBOLS[1] + rank_sym]
+    else:
+        out_syms[1] = out_sym
+        factor_syms = [EINSUM_SYMBOLS[1] + rank_sym, out_sym + rank_sym]
+    factor_syms += [xs + rank_sym for xs in x_syms[2:]]
+    eq = f'{x_syms},{rank_sym},{",".join(factor_syms)}->{"".join(out_syms)}'
+    return torch.einsum(eq, x, weights, *factors)
+
+
+def contract_tt(x, factors, separable=False):
+    """spectral_convolution.py:106-132."""
+    order = x.ndim
+    x_syms = list(EINSUM_SYMBOLS[:order])
+    weight_syms = list(x_syms[1:])
+    if not separable:
+        weight_syms.insert(1, EINSUM_SYMBOLS[order])
+        out_syms = list(weight_syms)
+        out_syms[0] = x_syms[0]
+    else:
+        out_syms = list(x_syms)
+    rank_syms = list(EINSUM_SYMBOLS[order + 1:])
+    tt_syms = [[rank_syms[i], s, rank_syms[i + 1]] for i, s in enumerate(weight_syms)]
+    eq = "".join(x_syms) + "," + ",".join("".join(f) for f in tt_syms) + "->" + "".join(out_syms)
+    return torch.einsum(eq, x, *factors)
+
+
+# ---------------------------------------------------------------------------
+# factorized weight reconstruction (tltorch semantics, restated)
+# ---------------------------------------------------------------------------
+def tucker_to_tensor(core, factors):
+    """Full tensor of a Tucker decomposition: core x_0 U_0 x_1 U_1 ..."""
+    t = core
+    for mode, U in enumerate(factors):
+        t = torch.movedim(torch.tensordot(t, U, dims=([mode], [1])), -1, mode)
+    return t
+
+
+def cp_to_tensor(weights, factors):
+    """Full tensor of a CP decomposition sum_r w_r u_0r o u_1r o ..."""
+    order = len(factors)
+    syms = EINSUM_SYMBOLS[:order]
+    eq = "z," + ",".join(s + "z" for s in syms) + "->" + syms
+    return torch.einsum(eq, weights, *factors)
+
+
+def tt_to_tensor(factors):
+    """Full tensor of a tensor train (cores r_k x n_k x r_{k+1})."""
+    full = factors[0]
+    for f in factors[1:]:
+        full = torch.tensordot(full, f, dims=([-1], [0]))
+    return full.squeeze(0).squeeze(-1)
+
+
+def tucker_rank_from_fraction(shape: Sequence[int], rank: float, fixed_modes=None):
+    """Restatement of tensorly 0.9.0 ``validate_tucker_rank`` for a float rank
+    (used by tltorch 0.5.0 TuckerTensor.new).  Parity unpinned: tensorly is
+    not importable here and no reference fixture holds the tuple.
+
+    Solves n_param * x**n_compressed + (sum s_i**2 + fixed) * x = rank * n_param
+    for the fraction x, then rank_i = max(round(s_i * x), 1).
+    """
+    shape = list(shape)
+    n_param = float(math.prod(shape))
+    fixed = []
+    if fixed_modes is not None:
+        fixed = [(m, shape.pop(m)) for m in sorted(fixed_modes, reverse=True)][::-1]
+    n_fixed = float(sum(s * s for _, s in fixed))
+    n_comp = len(shape)
+    sq = float(sum(s * s for s in shape))
+
+    def fun(x):
+        return n_param * x ** n_comp + sq * x + n_fixed * x - rank * n_param
+
+    lo, hi = 0.0, max(rank, 1.0)
+    for _ in range(200):
+        mid = 0.5 * (lo + hi)
+        if fun(lo) * fun(mid) <= 0:
+            hi = mid
+        else:
+            lo = mid
+    frac = 0.5 * (lo + hi)
+    out = [max(int(round(s * frac)), 1) for s in shape]
+    for mode, size in fixed:
+        out.insert(mode, size)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# SpectralConv.forward restated (spectral_convolution.py:417-570)
+# ---------------------------------------------------------------------------
+def spectral_conv_forward(
+    x: torch.Tensor,
+    weight,
+    bias: Optional[torch.Tensor],
+    n_modes,
+    max_n_modes=None,
+    *,
+    fft_norm: str = "forward",
+    separable: bool = False,
+    complex_data: bool = False,
+    enforce_hermitian_symmetry: bool = True,
+    output_shape=None,
+    resolution_scaling_factor=None,
+    factorization: Optional[str] = None,
+    implementation: str = "reconstructed",
+):
+    """Forward of a SpectralConv, op for op.
+
+    ``n_modes`` / ``max_n_modes`` are the *stored* lists (last entry already
+    n//2+1 for real data).  ``weight`` is either a dense complex tensor of the
+    max_n_modes window, or a dict describing a factorized weight:
+    {"tucker": (core, factors)}, {"cp": (weights, factors)}, {"tt": factors}.
+    """
+    if max_n_modes is None:
+        max_n_modes = list(n_modes)
+    order = len(n_modes)
+    batchsize, channels, *mode_sizes = x.shape
+    fft_size = list(mode_sizes)
+    if not complex_data:
+        fft_size[-1] = fft_size[-1] // 2 + 1          # :431-433
+    fft_dims = list(range(-order, 0))                  # :434
+
+    if complex_data:                                   # :439-446
+        xf = torch.fft.fftn(x, norm=fft_norm, dim=fft_dims)
+        dims_to_fft_shift = fft_dims
+    else:
+        xf = torch.fft.rfftn(x, norm=fft_norm, dim=fft_dims)
+        dims_to_fft_shift = fft_dims[:-1]
+    if order > 1:                                      # :448-449
+        xf = torch.fft.fftshift(xf, dim=dims_to_fft_shift)
+
+    cdtype = xf.dtype
+    if isinstance(weight, dict):
+        out_channels = _factorized_out_channels(weight, separable, channels)
+    else:
+        out_channels = weight.shape[0] if separable else weight.shape[1]
+    out_fft = torch.zeros([batchsize, out_channels, *fft_size], dtype=cdtype)  # :460-462
+
+    sl_w = weight_slices(fft_size, n_modes, max_n_modes, separable, complex_data)
+    w_start = 1 if separable else 2
+    if isinstance(weight, dict):
+        kept = _factorized_window_shape(weight, sl_w, w_start)
+    else:
+        w = weight[sl_w]                               # :489
+        kept = list(w.shape[w_start:])
+    sl_x = x_slices(fft_size, kept)                    # :500-519
+    xs = xf[sl_x]
+
+    if isinstance(weight, dict):
+        y = _contract_factorized(xs, weight, sl_w, w_start, separable, implementation, cdtype)
+    elif separable:
+        y = contract_dense_separable(xs, w.to(cdtype))
+    else:
+        y = contract_dense(xs, w.to(cdtype))
+    out_fft[sl_x] = y                                  # :520-522
+
+    if resolution_scaling_factor is not None and output_shape is None:   # :524-525
+        mode_sizes = tuple(round(s * r) for (s, r) in zip(mode_sizes, resolution_scaling_factor))
+    if output_shape is not None:                       # :527-528
+        mode_sizes = output_shape
+    mode_sizes = list(mode_sizes)
+
+    if order > 1:                                      # :531-532
+        out_fft = torch.fft.ifftshift(out_fft, dim=fft_dims[:-1])
+
+    if complex_data:                                   # :536-538
+        out = torch.fft.ifftn(out_fft, s=mode_sizes, dim=fft_dims, norm=fft_norm)
+    elif enforce_hermitian_symmetry:                   # :547-559
+        if order > 1:
+            out_fft = torch.fft.ifftn(out_fft, s=mode_sizes[:-1], dim=fft_dims[:-1], norm=fft_norm)
+        else:
+            # ifftn over zero dims is the identity, but torch still returns a copy
+            out_fft = out_fft.clone()
+        out_fft[..., 0].imag.zero_()
+        if mode_sizes[-1] % 2 == 0:
+            out_fft[..., -1].imag.zero_()
+        out = torch.fft.irfft(out_fft, n=mode_sizes[-1], dim=fft_dims[-1], norm=fft_norm)
+    else:                                              # :564
+        out = torch.fft.irfftn(out_fft, s=mode_sizes, dim=fft_dims, norm=fft_norm)
+
+    if bias is not None:                               # :567-568
+        out = out + bias
+    return out
+
+
+def _factorized_out_channels(weight, separable, channels):
+    if separable:
+        return channels
+    if "tucker" in weight:
+        return weight["tucker"][1][1].shape[0]
+    if "cp" in weight:
+        return weight["cp"][1][1].shape[0]
+    return weight["tt"][1].shape[1]
+
+
+def _slice_factor_list(factors, sl_w):
+    return [U[s] for U, s in zip(factors, sl_w)]
+
+
+def _factorized_window_shape(weight, sl_w, w_start):
+    if "tucker" in weight:
+        core, factors = weight["tucker"]
+        return [U[s].shape[0] for U, s in zip(factors[w_start:], sl_w[w_start:])]
+    if "cp" in weight:
+        _, factors = weight["cp"]
+        return [U[s].shape[0] for U, s in zip(factors[w_start:], sl_w[w_start:])]
+    factors = weight["tt"]
+    return [G[:, s, :].shape[1] for G, s in zip(factors[w_start:], sl_w[w_start:])]
+
+
+def _contract_factorized(xs, weight, sl_w, w_start, separable, implementation, cdtype):
+    """Slicing a factorized tensor slices the mode factors (tltorch
+    FactorizedTensor.__getitem__), then either contracts the factors directly
+    ('factorized', spectral_convolution.py:156-169) or reconstructs
+    ('reconstructed', :151-155)."""
+    if "tucker" in weight:
+        core, factors = weight["tucker"]
+        fs = [U[s].to(cdtype) for U, s in zip(factors, sl_w)]
+        core = core.to(cdtype)
+        if implementation == "factorized":
+            return contract_tucker(xs, core, fs, separable)
+        full = tucker_to_tensor(core, fs)
+    elif "cp" in weight:
+        w, factors = weight["cp"]
+        fs = [U[s].to(cdtype) for U, s in zip(factors, sl_w)]
+        w = w.to(cdtype)
+        if implementation == "factorized":
+            return contract_cp(xs, w, fs, separable)
+        full = cp_to_tensor(w, fs)
+    else:
+        factors = weight["tt"]
+        fs = [G[:, s, :].to(cdtype) for G, s in zip(factors, sl_w)]
+        if implementation == "factorized":
+            return contract_tt(xs, fs, separable)
+        full = tt_to_tensor(fs)
+    if separable:
+        return contract_dense_separable(xs, full)
+    return contract_dense(xs, full)
+
+
+# ---------------------------------------------------------------------------
+# skip connections, channel MLP, grid embedding (torch modules restated)
+# ---------------------------------------------------------------------------
+def gelu(x):
+    """Exact erf GELU, torch.nn.functional.gelu default (fno_block.py:118)."""
+    return F.gelu(x)
+
+
+def linear_skip(x, ws):
+    """Flattened1dConv with kernel 1, no bias (skip_connections.py:96-130):
+    s[b,o,p] = sum_i ws[o,i] x[b,i,p]."""
+    size = list(x.shape)
+    xf = x.reshape(size[0], size[1], -1)
+    out = F.conv1d(xf, ws.reshape(ws.shape[0], ws.shape[1], 1))
+    return out.reshape(size[0], ws.shape[0], *size[2:])
+
+
+def soft_gating(x, w, b=None):
+    """SoftGating (skip_connections.py:88-93)."""
+    return w * x + b if b is not None else w * x
+
+
+def channel_mlp(x, weights, biases, non_linearity=gelu):
+    """ChannelMLP.forward (channel_mlp.py:212-249) with 1x1 Conv1d layers."""
+    size = list(x.shape)
+    h = x.reshape(size[0], size[1], -1)
+    n = len(weights)
+    for i, (w, b) in enumerate(zip(weights, biases)):
+        h = F.conv1d(h, w.reshape(w.shape[0], w.shape[1], 1), b)
+        if i < n - 1:
+            h = non_linearity(h)
+    return h.reshape(size[0], h.shape[1], *size[2:])
+
+
+def regular_grid_nd(resolutions, grid_boundaries):
+    """embeddings.py:351-383: linspace(start, stop, res+1)[:-1] per dim."""
+    inputs = [torch.linspace(a, b, r + 1)[:-1] for r, (a, b) in zip(resolutions, grid_boundaries)]
+    return tuple(torch.meshgrid(*inputs, indexing="ij"))
+
+
+def grid_embedding_nd(x, grid_boundaries=None):
+    """GridEmbeddingND.forward (embeddings.py:147-164)."""
+    dim = x.ndim - 2
+    if grid_boundaries is None:
+        grid_boundaries = [[0.0, 1.0]] * dim
+    grids = regular_grid_nd(list(x.shape[2:]), grid_boundaries)
+    grids = [g.to(x.dtype).unsqueeze(0).unsqueeze(0).repeat(x.shape[0], *[1] * (dim + 1)) for g in grids]
+    return torch.cat((x, *grids), dim=1)
+
+
+# ---------------------------------------------------------------------------
+# FNO block and FNO forward (fno_block.py:327-381, fno.py:342-408)
+# ---------------------------------------------------------------------------
+def spectral_block_forward(x, conv: dict, ws, activation=True):
+    """The fused block measured by the benchmark: GELU(SpectralConv(x) + Ws x).
+
+    Composed explicitly (not via FNOBlocks(use_channel_mlp=False), which
+    applies GELU twice for non-last layers, fno_block.py:359-361,377-379)."""
+    y = spectral_conv_forward(x, **conv)
+    y = y + linear_skip(x, ws)
+    return gelu(y) if activation else y
+
+
+def fno_block_forward(x, index, n_layers, conv: dict, fno_skip: Optional[dict], mlp: Optional[dict],
+                      mlp_skip: Optional[dict], non_linearity=gelu, output_shape=None):
+    """FNOBlocks.forward_with_postactivation (fno_block.py:327-381) without
+    norms/stabilizer.  ``fno_skip``/``mlp_skip`` are {"type": "linear", "w": ..}
+    or {"type": "soft-gating", "w": .., "b": ..} or {"type": "identity"} or None."""
+    def apply_skip(s, inp):
+        if s["type"] == "linear":
+            return linear_skip(inp, s["w"])
+        if s["type"] == "soft-gating":
+            return soft_gating(inp, s["w"], s.get("b"))
+        return inp
+
+    def transform(t):
+        # SpectralConv.transform (spectral_convolution.py:383-398)
+        in_shape = list(t.shape[2:])
+        rsf = conv.get("resolution_scaling_factor")
+        if rsf is not None and output_shape is None:
+            out_shape = [round(s * r) for s, r in zip(in_shape, rsf)]
+        elif output_shape is not None:
+            out_shape = list(output_shape)
+        else:
+            out_shape = in_shape
+        if in_shape == out_shape:
+            return t
+        if len(in_shape) == 1:
+            return F.interpolate(t, size=out_shape[0], mode="linear", align_corners=True)
+        if len(in_shape) == 2:
+            return F.interpolate(t, size=out_shape, mode="bicubic", align_corners=True)
+        raise NotImplementedError("3D spectral resample is not restated")
+
+    x_skip_fno = transform(apply_skip(fno_skip, x)) if fno_skip is not None else None
+    x_skip_mlp = None
+    if mlp is not None and mlp_skip is not None:
+        x_skip_mlp = transform(apply_skip(mlp_skip, x))
+    x_fno = spectral_conv_forward(x, output_shape=output_shape, **conv)
+    x = x_fno + x_skip_fno if x_skip_fno is not None else x_fno
+    if index < n_layers - 1:
+        x = non_linearity(x)
+    if mlp is not None:
+        x = channel_mlp(x, mlp["weights"], mlp["biases"], non_linearity)
+        if x_skip_mlp is not None:
+            x = x + x_skip_mlp
+    if index < n_layers - 1:
+        x = non_linearity(x)
+    return x
+
+
+def fno_forward(x, params: dict):
+    """FNO.forward (fno.py:342-408): grid embedding, lifting, blocks, projection.
+
+    ``params`` = {"lifting": {"weights", "biases"}, "projection": {...},
+    "layers": [ {conv, fno_skip, mlp, mlp_skip}, ...], "positional_embedding": bool}
+    """
+    if params.get("positional_embedding", True):
+        x = grid_embedding_nd(x)
+    x = channel_mlp(x, params["lifting"]["weights"], params["lifting"]["biases"])
+    n_layers = len(params["layers"])
+    for i, layer in enumerate(params["layers"]):
+        x = fno_block_forward(x, i, n_layers, layer["conv"], layer.get("fno_skip"),
+                              layer.get("mlp"), layer.get("mlp_skip"))
+    x = channel_mlp(x, params["projection"]["weights"], params["projection"]["biases"])
+    return x

@@ -1,0 +1,313 @@
+"""GPU parity: the HIP path (through the module API and the C ABI) against
+the oracle on the same seeded inputs and weights.
+
+Tolerance (fp32 path): max |y - ref| / max |ref| <= 1e-4, ref in float64.
+"""
+import glob
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import neuraloperator_amd as na
+from neuraloperator_amd import _native as nat
+from neuraloperator_amd import functional as Fh
+from oracle import spectral_ref as R
+from neuraloperator_amd.synthetic import gaussian_random_field
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def rel_err(y, ref):
+    y = y.detach().double().cpu()
+    ref = ref.detach().double().cpu()
+    return ((y - ref).abs().max() / ref.abs().max()).item()
+
+
+def _case_id(p):
+    return os.path.basename(p)[:-4]
+
+
+@pytest.mark.parametrize("path", sorted(glob.glob(os.path.join(GOLDEN, "*.npz"))), ids=_case_id)
+def test_golden_fixtures(path, cuda_device):
+    d = np.load(path)
+    x = torch.from_numpy(d["x"])
+    w = torch.from_numpy(d["w"])
+    nm = d["n_modes"].tolist()
+    mx_stored = d["max_n_modes"].tolist()
+    sizes = list(x.shape[2:])
+    outs = d["out_sizes"].tolist()
+    norm = str(d["norm"])
+    Ci, Co = w.shape[0], w.shape[1]
+    print(f"golden {_case_id(path)} x{tuple(x.shape)} modes={nm} out={outs} norm={norm}", flush=True)
+    conv = na.SpectralConv(Ci, Co, nm, fft_norm=norm)
+    # max_n_modes as stored: rebuild the weight container at that window
+    conv.max_n_modes = mx_stored
+    conv.weight = na.FactorizedTensor.new((Ci, Co, *mx_stored), factorization="Dense")
+    with torch.no_grad():
+        conv.weight.tensor.copy_(w)
+        conv.bias.copy_(torch.from_numpy(d["bias"]))
+    conv = conv.to(cuda_device)
+    xg = x.to(cuda_device)
+    with torch.no_grad():
+        if "skip_w" in d:
+            ws = torch.from_numpy(d["skip_w"]).to(cuda_device)
+            y = conv._forward_hip(xg, None, nat.SKIP_LINEAR, ws, nat.ACT_GELU)
+        else:
+            y = conv(xg, output_shape=tuple(outs) if outs != sizes else None)
+    torch.cuda.synchronize()
+    err = rel_err(y, torch.from_numpy(d["expected"]))
+    assert err <= TOL, err
+
+
+FUSED_CASES = [
+    # B, Ci, Co, H, W, n_modes (constructor)
+    (2, 32, 32, 64, 128, (16, 16)),
+    (2, 64, 64, 128, 128, (32, 32)),
+    (1, 64, 64, 256, 256, (64, 64)),
+    (1, 64, 64, 256, 256, (32, 32)),
+    (2, 32, 64, 256, 128, (33, 30)),
+    (1, 64, 32, 128, 256, (20, 64)),
+    (1, 32, 32, 64, 128, (64, 128)),    # every row and the Nyquist column kept
+]
+
+
+def _dense_conv(Ci, Co, nm, device, seed=0):
+    torch.manual_seed(seed)
+    conv = na.SpectralConv(Ci, Co, nm).to(device)
+    return conv
+
+
+@pytest.mark.parametrize("B,Ci,Co,H,W,nm", FUSED_CASES)
+@pytest.mark.parametrize("skip", ["linear", "soft-gating", "identity", "none"])
+def test_fused_block_matches_oracle(B, Ci, Co, H, W, nm, skip, cuda_device):
+    if skip in ("soft-gating", "identity") and Ci != Co:
+        pytest.skip("gating/identity skips need Ci == Co")
+    print(f"fused B{B} Ci{Ci} Co{Co} {H}x{W} modes={nm} skip={skip}", flush=True)
+    conv = _dense_conv(Ci, Co, nm, cuda_device)
+    kept, sl = conv.window([H, W])
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(B, Ci, H, W, generator=g)
+    kind = {"linear": nat.SKIP_LINEAR, "soft-gating": nat.SKIP_SOFT_GATING,
+            "identity": nat.SKIP_IDENTITY, "none": nat.SKIP_NONE}[skip]
+    ws = None
+    if skip == "linear":
+        ws = torch.randn(Co, Ci, generator=g) / Ci ** 0.5
+    elif skip == "soft-gating":
+        ws = torch.rand(Co, generator=g) + 0.5
+    assert Fh.spectral_block_is_fused(B, Ci, Co, [H, W], kept, kind)
+    with torch.no_grad():
+        y = conv._forward_hip(x.to(cuda_device), None, kind,
+                              None if ws is None else ws.to(cuda_device), nat.ACT_GELU)
+    torch.cuda.synchronize()
+    w = conv.weight.to_tensor().detach().cpu().to(torch.complex128)
+    ref = R.spectral_conv_forward(x.double(), w, conv.bias.detach().cpu().double(), conv.n_modes,
+                                  conv.max_n_modes)
+    if skip == "linear":
+        ref = ref + R.linear_skip(x.double(), ws.double())
+    elif skip == "soft-gating":
+        ref = ref + ws.double().view(1, -1, 1, 1) * x.double()
+    elif skip == "identity":
+        ref = ref + x.double()
+    ref = R.gelu(ref)
+    err = rel_err(y, ref)
+    assert err <= TOL, err
+
+
+def test_headline_block_per_sample_slice(cuda_device):
+    """Two samples of the 256^2 headline block (C=64, n_modes (64,64), GRF
+    input, N(0,1/4096) complex weights, N(0,1/64) skip, bias 0) against the
+    float64 oracle."""
+    print("headline slice B2 C64 256x256 modes 64x64", flush=True)
+    B, C, H, W = 2, 64, 256, 256
+    x = gaussian_random_field((B, C, H, W), seed=11)
+    g = torch.Generator().manual_seed(12)
+    w = torch.complex(torch.randn(C, C, 64, 33, generator=g), torch.randn(C, C, 64, 33, generator=g)) / 64
+    ws = torch.randn(C, C, generator=g) / 8
+    bias = torch.zeros(C)
+    with torch.no_grad():
+        y = Fh.spectral_block(x.to(cuda_device), w.to(cuda_device), bias.to(cuda_device), [64, 33],
+                              nat.SKIP_LINEAR, ws.to(cuda_device), nat.ACT_GELU)
+    torch.cuda.synchronize()
+    ref = R.spectral_conv_forward(x.double(), w.to(torch.complex128), bias.double().view(-1, 1, 1),
+                                  [64, 33], [64, 33])
+    ref = R.gelu(ref + R.linear_skip(x.double(), ws.double()))
+    err = rel_err(y, ref)
+    assert err <= TOL, err
+
+
+@pytest.mark.parametrize("dim,sizes,nm", [
+    (1, (1024,), (30,)),
+    (1, (37,), (12,)),
+    (2, (12, 12), (6, 8)),
+    (2, (9, 10), (4, 5)),
+    (3, (16, 16, 16), (8, 8, 8)),
+    (3, (8, 9, 10), (4, 4, 4)),
+])
+@pytest.mark.parametrize("norm", ["forward", "backward", "ortho"])
+def test_generic_spectral_conv(dim, sizes, nm, norm, cuda_device):
+    print(f"generic dim{dim} {sizes} {nm} {norm}", flush=True)
+    torch.manual_seed(3)
+    conv = na.SpectralConv(3, 4, nm, fft_norm=norm).to(cuda_device)
+    x = torch.randn(2, 3, *sizes)
+    with torch.no_grad():
+        y = conv(x.to(cuda_device))
+    ref = R.spectral_conv_forward(x.double(), conv.weight.to_tensor().detach().cpu().to(torch.complex128),
+                                  conv.bias.detach().cpu().double(), conv.n_modes, conv.max_n_modes,
+                                  fft_norm=norm)
+    assert rel_err(y, ref) <= TOL
+
+
+@pytest.mark.parametrize("scale", [0.5, 2])
+@pytest.mark.parametrize("dim", [1, 2, 3])
+@pytest.mark.parametrize("size", [8, 9])
+def test_resolution_scaling(scale, dim, size, cuda_device):
+    """Reference test_spectral_convolution.py:89-116 shapes, plus numbers."""
+    torch.manual_seed(4)
+    modes = (4, 5, 7)[:dim]
+    conv = na.SpectralConv(3, 4, modes, resolution_scaling_factor=scale).to(cuda_device)
+    x = torch.randn(2, 3, *([size] * dim))
+    with torch.no_grad():
+        y = conv(x.to(cuda_device))
+    out = [round(size * scale)] * dim
+    assert list(y.shape) == [2, 4, *out] and y.dtype == torch.float32
+    ref = R.spectral_conv_forward(x.double(), conv.weight.to_tensor().detach().cpu().to(torch.complex128),
+                                  conv.bias.detach().cpu().double(), conv.n_modes, conv.max_n_modes,
+                                  resolution_scaling_factor=[scale] * dim)
+    assert rel_err(y, ref) <= TOL
+
+
+@pytest.mark.parametrize("enforce", [True, False])
+def test_output_shape_with_nyquist(enforce, cuda_device):
+    torch.manual_seed(5)
+    conv = na.SpectralConv(3, 4, (8, 8), enforce_hermitian_symmetry=enforce).to(cuda_device)
+    x = torch.randn(2, 3, 8, 8)
+    with torch.no_grad():
+        y = conv(x.to(cuda_device), output_shape=(16, 16))
+    ref = R.spectral_conv_forward(x.double(), conv.weight.to_tensor().detach().cpu().to(torch.complex128),
+                                  conv.bias.detach().cpu().double(), conv.n_modes, conv.max_n_modes,
+                                  output_shape=(16, 16), enforce_hermitian_symmetry=enforce)
+    assert rel_err(y, ref) <= TOL
+
+
+def test_incremental_modes_window(cuda_device):
+    torch.manual_seed(6)
+    conv = na.SpectralConv(3, 3, (10, 8), max_n_modes=(10, 8)).to(cuda_device)
+    conv.n_modes = (6, 4)
+    x = torch.randn(2, 3, 12, 12)
+    with torch.no_grad():
+        y = conv(x.to(cuda_device))
+    ref = R.spectral_conv_forward(x.double(), conv.weight.to_tensor().detach().cpu().to(torch.complex128),
+                                  conv.bias.detach().cpu().double(), conv.n_modes, conv.max_n_modes)
+    assert rel_err(y, ref) <= TOL
+
+
+@pytest.mark.parametrize("factorization", ["Tucker", "CP", "TT"])
+@pytest.mark.parametrize("implementation", ["factorized", "reconstructed"])
+@pytest.mark.parametrize("dim", [2, 3])
+def test_factorized_weights(factorization, implementation, dim, cuda_device):
+    torch.manual_seed(7)
+    nm = (8, 8, 8)[:dim]
+    conv = na.SpectralConv(4, 5, nm, factorization=factorization, rank=0.5,
+                           implementation=implementation).to(cuda_device)
+    x = torch.randn(2, 4, *([12] * dim))
+    with torch.no_grad():
+        y = conv(x.to(cuda_device))
+    full = conv.weight.to_tensor().detach().cpu().to(torch.complex128)
+    ref = R.spectral_conv_forward(x.double(), full, conv.bias.detach().cpu().double(), conv.n_modes,
+                                  conv.max_n_modes)
+    assert rel_err(y, ref) <= TOL
+
+
+def test_separable(cuda_device):
+    torch.manual_seed(8)
+    conv = na.SpectralConv(4, 4, (6, 6), separable=True).to(cuda_device)
+    x = torch.randn(2, 4, 10, 12)
+    with torch.no_grad():
+        y = conv(x.to(cuda_device))
+    ref = R.spectral_conv_forward(x.double(), conv.weight.to_tensor().detach().cpu().to(torch.complex128),
+                                  conv.bias.detach().cpu().double(), conv.n_modes, conv.max_n_modes,
+                                  separable=True)
+    assert rel_err(y, ref) <= TOL
+
+
+def test_tfno3d_tucker_block(cuda_device):
+    """3D Tucker-factorized block (reduced C4 shape) through the factors."""
+    torch.manual_seed(9)
+    B, C = 2, 32
+    conv = na.SpectralConv(C, C, (16, 16, 16), factorization="Tucker", rank=0.1,
+                           implementation="factorized").to(cuda_device)
+    x = gaussian_random_field((B, C, 32, 32, 32), seed=13)
+    with torch.no_grad():
+        y = conv(x.to(cuda_device))
+    core = conv.weight.core.detach().cpu().to(torch.complex128)
+    factors = [f.detach().cpu().to(torch.complex128) for f in conv.weight.factors]
+    ref = R.spectral_conv_forward(x.double(), {"tucker": (core, factors)},
+                                  conv.bias.detach().cpu().double(), conv.n_modes, conv.max_n_modes,
+                                  implementation="factorized")
+    assert rel_err(y, ref) <= TOL
+
+
+def _layer_params(blocks, i):
+    conv = blocks.convs[i]
+    layer = {"conv": dict(weight=conv.weight.to_tensor().detach().cpu().to(torch.complex128),
+                          bias=conv.bias.detach().cpu().double(), n_modes=conv.n_modes,
+                          max_n_modes=conv.max_n_modes)}
+    s = blocks.fno_skips[i]
+    layer["fno_skip"] = {"type": "linear", "w": s.conv.weight.detach().cpu().double()[:, :, 0]}
+    if blocks.use_channel_mlp:
+        m = blocks.channel_mlp[i]
+        layer["mlp"] = {"weights": [f.weight.detach().cpu().double() for f in m.fcs],
+                        "biases": [f.bias.detach().cpu().double() for f in m.fcs]}
+        sk = blocks.channel_mlp_skips[i]
+        layer["mlp_skip"] = {"type": "soft-gating", "w": sk.weight.detach().cpu().double()}
+    return layer
+
+
+def _mlp(m):
+    return {"weights": [f.weight.detach().cpu().double() for f in m.fcs],
+            "biases": [f.bias.detach().cpu().double() for f in m.fcs]}
+
+
+@pytest.mark.parametrize("hidden,H,W,nm", [(32, 64, 128, (16, 16)), (64, 128, 128, (32, 32))])
+def test_fno_forward_matches_oracle(hidden, H, W, nm, cuda_device):
+    print(f"fno hidden{hidden} {H}x{W} {nm}", flush=True)
+    torch.manual_seed(10)
+    model = na.FNO(nm, in_channels=1, out_channels=1, hidden_channels=hidden, n_layers=4).to(cuda_device)
+    with torch.no_grad():
+        for sk in model.fno_blocks.channel_mlp_skips:
+            sk.weight.uniform_(0.5, 1.5)
+    x = gaussian_random_field((2, 1, H, W), seed=14)
+    with torch.no_grad():
+        y = model(x.to(cuda_device))
+    params = {"lifting": _mlp(model.lifting), "projection": _mlp(model.projection),
+              "layers": [_layer_params(model.fno_blocks, i) for i in range(4)]}
+    ref = R.fno_forward(x.double(), params)
+    assert rel_err(y, ref) <= TOL
+
+
+def test_deterministic(cuda_device):
+    torch.manual_seed(11)
+    conv = na.SpectralConv(64, 64, (64, 64)).to(cuda_device)
+    x = torch.randn(2, 64, 256, 256, device=cuda_device)
+    ws = torch.randn(64, 64, device=cuda_device) / 8
+    with torch.no_grad():
+        a = conv._forward_hip(x, None, nat.SKIP_LINEAR, ws, nat.ACT_GELU)
+        b = conv._forward_hip(x, None, nat.SKIP_LINEAR, ws, nat.ACT_GELU)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
+def test_errors_raise(cuda_device):
+    conv = na.SpectralConv(3, 4, (4, 4)).to(cuda_device)
+    with pytest.raises(RuntimeError):
+        conv(torch.randn(1, 3, 8, 8))            # CPU input
+    with pytest.raises(RuntimeError, match="4096"):
+        conv(torch.randn(1, 3, 8, 8200, device=cuda_device))
+    with pytest.raises(NotImplementedError):
+        x = torch.randn(1, 3, 8, 8, device=cuda_device, requires_grad=True)
+        conv(x).sum().backward()

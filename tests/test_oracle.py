@@ -1,0 +1,225 @@
+"""Pins the oracle (oracle/spectral_ref.py) before it is trusted as the checker.
+
+Each check is chosen so that a plausible mistake fails it:
+  * closed-form float64 DFT (oracle/dft64.py)  -> sign, index, shift, window,
+    scaling, Hermitian and output-size bookkeeping
+  * plane-wave known answers                   -> amplitude / phase / row order
+  * circular-shift equivariance, linearity     -> transposed operands, dropped terms
+  * factorized == dense on the reconstructed weight (reference invariant,
+    neuralop/layers/tests/test_spectral_convolution.py:53-65)
+  * committed golden fixtures
+"""
+import glob
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import dft64, spectral_ref as R
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+CASES = [
+    ((12,), (10,), None, None, "forward"),
+    ((16,), (8,), (12,), None, "forward"),
+    ((9, 10), (4, 5), None, None, "forward"),
+    ((8, 8), (4, 4), (8, 8), None, "backward"),
+    ((12, 12), (4, 6), None, (24, 24), "forward"),
+    ((9, 9), (4, 7), None, (4, 4), "ortho"),
+    ((8, 9, 10), (4, 4, 4), None, None, "forward"),
+    ((9, 8), (4, 4), None, (18, 16), "forward"),
+    ((8, 8), (8, 8), None, (16, 16), "forward"),
+    ((6, 10), (6, 10), None, (12, 10), "forward"),
+]
+
+
+@pytest.mark.parametrize("sizes,nm,mx,outs,norm", CASES)
+@pytest.mark.parametrize("enforce", [True, False])
+def test_restatement_matches_closed_form(sizes, nm, mx, outs, norm, enforce):
+    torch.manual_seed(0)
+    nms = R.stored_n_modes(nm)
+    mxs = R.stored_n_modes(mx) if mx else nms
+    x = torch.randn(2, 3, *sizes, dtype=torch.float64)
+    w = torch.randn(3, 4, *mxs, dtype=torch.complex128)
+    b = torch.randn(4, *([1] * len(sizes)), dtype=torch.float64)
+    y = R.spectral_conv_forward(x, w, b, nms, mxs, fft_norm=norm, output_shape=outs,
+                                enforce_hermitian_symmetry=enforce)
+    yd = dft64.spectral_conv(x.numpy(), w.numpy(), b.numpy(), nms, mxs, norm=norm, out_sizes=outs,
+                             enforce_hermitian_symmetry=enforce)
+    assert y.shape == yd.shape
+    assert np.abs(y.numpy() - yd).max() <= 1e-12 * np.abs(yd).max()
+
+
+def test_hermitian_flag_matters_only_for_kept_nyquist_with_resize():
+    torch.manual_seed(1)
+    nms = R.stored_n_modes((8, 8))
+    x = torch.randn(1, 2, 8, 8, dtype=torch.float64)
+    w = torch.randn(2, 2, *nms, dtype=torch.complex128)
+    a = R.spectral_conv_forward(x, w, None, nms, nms, output_shape=(16, 16), enforce_hermitian_symmetry=True)
+    b = R.spectral_conv_forward(x, w, None, nms, nms, output_shape=(16, 16), enforce_hermitian_symmetry=False)
+    assert (a - b).abs().max() > 1e-3
+    a = R.spectral_conv_forward(x, w, None, nms, nms, enforce_hermitian_symmetry=True)
+    b = R.spectral_conv_forward(x, w, None, nms, nms, enforce_hermitian_symmetry=False)
+    assert (a - b).abs().max() == 0
+
+
+@pytest.mark.parametrize("kh,kw", [(0, 0), (3, 2), (-4, 5), (-2, 0), (5, 0)])
+def test_plane_wave_known_answer(kh, kw):
+    """x = cos(2 pi (kh h/H + kw w/W)); weight nonzero (= c) only at window
+    index of (kh, kw) -> y = |c| cos(theta + arg c) for kw > 0, and half that
+    amplitude per conjugate partner when kw == 0."""
+    H, W, m1, m2 = 16, 16, 12, 8
+    nms = R.stored_n_modes((m1, 2 * (m2 - 1)))
+    assert nms == [m1, m2]
+    h = torch.arange(H, dtype=torch.float64)[:, None]
+    ww = torch.arange(W, dtype=torch.float64)[None, :]
+    theta = 2 * math.pi * (kh * h / H + kw * ww / W)
+    x = torch.cos(theta)[None, None]
+    c = complex(0.7, -0.4)
+    wt = torch.zeros(1, 1, m1, m2, dtype=torch.complex128)
+    wt[0, 0, kh + m1 // 2, kw] = c
+    y = R.spectral_conv_forward(x, wt, None, nms, nms)[0, 0]
+    amp, ph = abs(c), math.atan2(c.imag, c.real)
+    if kw > 0:
+        expected = amp * torch.cos(theta + ph)
+    else:
+        # X[kh,0] = X[-kh,0] = 1/2; only the (kh,0) weight is nonzero: the
+        # output is Re(c/2 e^{i theta}) from the DC column (c_0 = 1)
+        expected = 0.5 * amp * torch.cos(theta + ph) if kh != 0 else amp * math.cos(ph) * torch.ones_like(theta)
+    assert torch.allclose(y, expected, atol=1e-12)
+
+
+def test_circular_shift_equivariance():
+    torch.manual_seed(2)
+    nms = R.stored_n_modes((6, 6))
+    x = torch.randn(2, 3, 12, 10, dtype=torch.float64)
+    w = torch.randn(3, 4, *nms, dtype=torch.complex128)
+    y = R.spectral_conv_forward(x, w, None, nms, nms)
+    ys = R.spectral_conv_forward(torch.roll(x, shifts=(3, -2), dims=(2, 3)), w, None, nms, nms)
+    assert torch.allclose(torch.roll(y, shifts=(3, -2), dims=(2, 3)), ys, atol=1e-12)
+
+
+def test_linearity():
+    torch.manual_seed(3)
+    nms = R.stored_n_modes((4, 6))
+    x1 = torch.randn(2, 3, 8, 12, dtype=torch.float64)
+    x2 = torch.randn(2, 3, 8, 12, dtype=torch.float64)
+    w = torch.randn(3, 2, *nms, dtype=torch.complex128)
+    f = lambda x: R.spectral_conv_forward(x, w, None, nms, nms)
+    assert torch.allclose(f(2.5 * x1 - x2), 2.5 * f(x1) - f(x2), atol=1e-12)
+
+
+@pytest.mark.parametrize("implementation", ["factorized", "reconstructed"])
+@pytest.mark.parametrize("dim", [1, 2, 3])
+def test_tucker_equals_dense(implementation, dim):
+    torch.manual_seed(4)
+    sizes = (10,) * dim
+    nms = R.stored_n_modes((6,) * dim)
+    shape = (3, 4, *nms)
+    ranks = [2, 3] + [3] * dim
+    core = torch.randn(*ranks, dtype=torch.complex128)
+    factors = [torch.randn(s, r, dtype=torch.complex128) for s, r in zip(shape, ranks)]
+    x = torch.randn(2, 3, *sizes, dtype=torch.float64)
+    full = R.tucker_to_tensor(core, factors)
+    yf = R.spectral_conv_forward(x, {"tucker": (core, factors)}, None, nms, nms,
+                                 implementation=implementation)
+    yd = R.spectral_conv_forward(x, full, None, nms, nms)
+    assert torch.allclose(yf, yd, atol=1e-10)
+
+
+def test_tucker_window_slices_mode_factors():
+    torch.manual_seed(5)
+    nms = R.stored_n_modes((4, 6))
+    mxs = R.stored_n_modes((8, 8))
+    shape = (3, 2, *mxs)
+    ranks = [2, 2, 3, 3]
+    core = torch.randn(*ranks, dtype=torch.complex128)
+    factors = [torch.randn(s, r, dtype=torch.complex128) for s, r in zip(shape, ranks)]
+    x = torch.randn(1, 3, 12, 12, dtype=torch.float64)
+    yf = R.spectral_conv_forward(x, {"tucker": (core, factors)}, None, nms, mxs,
+                                 implementation="factorized")
+    yd = R.spectral_conv_forward(x, R.tucker_to_tensor(core, factors), None, nms, mxs)
+    assert torch.allclose(yf, yd, atol=1e-10)
+
+
+def test_cp_and_tt_equal_dense():
+    torch.manual_seed(6)
+    nms = R.stored_n_modes((4, 6))
+    shape = (3, 2, *nms)
+    x = torch.randn(2, 3, 9, 10, dtype=torch.float64)
+    wts = torch.randn(5, dtype=torch.complex128)
+    cf = [torch.randn(s, 5, dtype=torch.complex128) for s in shape]
+    y1 = R.spectral_conv_forward(x, {"cp": (wts, cf)}, None, nms, nms, implementation="factorized")
+    y2 = R.spectral_conv_forward(x, R.cp_to_tensor(wts, cf), None, nms, nms)
+    assert torch.allclose(y1, y2, atol=1e-10)
+    ranks = [1, 2, 3, 2, 1]
+    tf = [torch.randn(ranks[k], s, ranks[k + 1], dtype=torch.complex128) for k, s in enumerate(shape)]
+    y1 = R.spectral_conv_forward(x, {"tt": tf}, None, nms, nms, implementation="factorized")
+    y2 = R.spectral_conv_forward(x, R.tt_to_tensor(tf), None, nms, nms)
+    assert torch.allclose(y1, y2, atol=1e-10)
+
+
+def test_separable_matches_closed_form():
+    torch.manual_seed(7)
+    nms = R.stored_n_modes((4, 6))
+    x = torch.randn(2, 3, 9, 12, dtype=torch.float64)
+    w = torch.randn(3, *nms, dtype=torch.complex128)
+    y = R.spectral_conv_forward(x, w, None, nms, nms, separable=True)
+    yd = dft64.spectral_conv(x.numpy(), w.numpy(), None, nms, nms, separable=True)
+    assert np.abs(y.numpy() - yd).max() < 1e-12
+
+
+def test_gelu_is_exact_erf():
+    xs = torch.tensor([-3.0, -1.0, 0.0, 0.5, 1.0, 2.0], dtype=torch.float64)
+    ref = torch.tensor([0.5 * v * (1 + math.erf(v / math.sqrt(2))) for v in xs.tolist()], dtype=torch.float64)
+    assert torch.allclose(R.gelu(xs), ref, atol=1e-15)
+    # gelu(1) = Phi(1) = 0.8413447460685429 (standard normal CDF)
+    assert abs(R.gelu(torch.tensor(1.0, dtype=torch.float64)).item() - 0.8413447460685429) < 1e-15
+    # the tanh approximation differs by more than the 1e-4 tolerance somewhere
+    t = torch.linspace(-5, 5, 2001, dtype=torch.float64)
+    tanh_gelu = torch.nn.functional.gelu(t, approximate="tanh")
+    assert (tanh_gelu - R.gelu(t)).abs().max() > 1e-4
+
+
+def test_grid_embedding_coordinates():
+    x = torch.zeros(2, 1, 4, 8)
+    e = R.grid_embedding_nd(x)
+    assert e.shape == (2, 3, 4, 8)
+    assert torch.allclose(e[0, 1, :, 0], torch.tensor([0.0, 0.25, 0.5, 0.75]))
+    assert torch.allclose(e[0, 2, 0, :], torch.arange(8) / 8.0)
+
+
+def test_linear_skip_is_channel_matmul():
+    torch.manual_seed(8)
+    x = torch.randn(2, 3, 5, 6)
+    ws = torch.randn(4, 3)
+    assert torch.allclose(R.linear_skip(x, ws), torch.einsum("oi,bihw->bohw", ws, x), atol=1e-6)
+
+
+@pytest.mark.parametrize("path", sorted(glob.glob(os.path.join(GOLDEN, "*.npz"))),
+                         ids=lambda p: os.path.basename(p)[:-4])
+def test_oracle_reproduces_golden(path):
+    d = np.load(path)
+    x = torch.from_numpy(d["x"]).double()
+    w = torch.from_numpy(d["w"]).to(torch.complex128)
+    b = torch.from_numpy(d["bias"]).double()
+    nms = d["stored_n_modes"].tolist()
+    mxs = d["max_n_modes"].tolist()
+    outs = tuple(d["out_sizes"].tolist())
+    norm = str(d["norm"])
+    y = R.spectral_conv_forward(x, w, b, nms, mxs, fft_norm=norm, output_shape=outs)
+    if "skip_w" in d:
+        y = R.gelu(y + R.linear_skip(x, torch.from_numpy(d["skip_w"]).double()))
+    exp = d["expected"]
+    assert np.abs(y.numpy() - exp).max() <= 1e-6 * np.abs(exp).max()
+
+
+def test_tucker_rank_rule_for_tfno_default():
+    # rank fraction 0.1 of the 3D TFNO weight (32,32,16,16,9): the solved
+    # ranks must reproduce ~10% of the dense parameter count
+    shape = (32, 32, 16, 16, 9)
+    ranks = R.tucker_rank_from_fraction(shape, 0.1)
+    n = math.prod(ranks) + sum(s * r for s, r in zip(shape, ranks))
+    assert abs(n / math.prod(shape) - 0.1) < 0.03
