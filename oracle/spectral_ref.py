@@ -63,6 +63,36 @@ def x_slices(fft_size, kept_modes):
 # ---------------------------------------------------------------------------
 # contractions
 # ---------------------------------------------------------------------------
+def einsum_pairwise(eq: str, *operands):
+    """Multi-operand einsum evaluated as a sequence of two-operand einsums,
+    each step contracting the pair whose result is smallest (a greedy
+    contraction path).  The reference's tl.einsum goes through opt_einsum's
+    path search (spectral_convolution.py:16-17); torch.einsum without
+    opt_einsum contracts left to right, which for the Tucker equations builds
+    intermediates of hundreds of GB.  The path only changes rounding."""
+    lhs, out = eq.split("->")
+    terms = lhs.split(",")
+    ops = list(operands)
+    sizes = {}
+    for t, op in zip(terms, ops):
+        for s, n in zip(t, op.shape):
+            sizes[s] = n
+    while len(ops) > 2:
+        best = None
+        for a in range(len(ops)):
+            for b in range(a + 1, len(ops)):
+                others = set(out).union(*[set(t) for k, t in enumerate(terms) if k not in (a, b)])
+                keep = "".join(s for s in dict.fromkeys(terms[a] + terms[b]) if s in others)
+                cost = math.prod(sizes[s] for s in keep)
+                if best is None or cost < best[0]:
+                    best = (cost, a, b, keep)
+        _, a, b, keep = best
+        r = torch.einsum(f"{terms[a]},{terms[b]}->{keep}", ops[a], ops[b])
+        terms = [t for k, t in enumerate(terms) if k not in (a, b)] + [keep]
+        ops = [o for k, o in enumerate(ops) if k not in (a, b)] + [r]
+    return torch.einsum(f"{','.join(terms)}->{out}", *ops)
+
+
 def contract_dense(x, weight, separable=False):
     """spectral_convolution.py:21-46 (tl.einsum -> opt_einsum -> torch)."""
     order = x.ndim
@@ -98,7 +128,7 @@ def contract_tucker(x, core, factors, separable=False):
         factor_syms = [EINSUM_SYMBOLS[1] + core_syms[0], out_sym + core_syms[1]]
         factor_syms += [xs + rs for (xs, rs) in zip(x_syms[2:], core_syms[2:])]
     eq = f'{x_syms},{core_syms},{",".join(factor_syms)}->{"".join(out_syms)}'
-    return torch.einsum(eq, x, core, *factors)
+    return einsum_pairwise(eq, x, core, *factors)
 
 
 def contract_cp(x, weights, factors, separable=False):
@@ -115,7 +145,7 @@ def contract_cp(x, weights, factors, separable=False):
         factor_syms = [EINSUM_SYMBOLS[1] + rank_sym, out_sym + rank_sym]
     factor_syms += [xs + rank_sym for xs in x_syms[2:]]
     eq = f'{x_syms},{rank_sym},{",".join(factor_syms)}->{"".join(out_syms)}'
-    return torch.einsum(eq, x, weights, *factors)
+    return einsum_pairwise(eq, x, weights, *factors)
 
 
 def contract_tt(x, factors, separable=False):
@@ -132,7 +162,7 @@ def contract_tt(x, factors, separable=False):
     rank_syms = list(EINSUM_SYMBOLS[order + 1:])
     tt_syms = [[rank_syms[i], s, rank_syms[i + 1]] for i, s in enumerate(weight_syms)]
     eq = "".join(x_syms) + "," + ",".join("".join(f) for f in tt_syms) + "->" + "".join(out_syms)
-    return torch.einsum(eq, x, *factors)
+    return einsum_pairwise(eq, x, *factors)
 
 
 # ---------------------------------------------------------------------------
