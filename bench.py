@@ -237,8 +237,8 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved_block, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved_block / HBM_PEAK_GBS, 4),
                      "traffic": None,
-                     "kernel": "whole block call (k_fwd_plane, contraction, k_inv_cols, "
-                               "k_row_epilogue), HIP events on the launch stream"},
+                     "kernel": "whole block call (k_fwd_stream, k_contract_dense, k_inv_cols, "
+                               "k_row_epilogue on one stream), HIP events on that stream"},
         "copy_bandwidth_gbs": round(copy_gbs, 1),
         "torch_rocm_baseline": rocm,
     }

@@ -3,24 +3,38 @@
 //
 //   y = act( irfft2_window( contract( rfft2_window(x) ) ) + bias + skip(x) )
 //
-// K1  k_fwd_plane      one workgroup per (b, c) plane: row real FFTs (two real
-//                      rows packed as one complex line) keep m2h bins in an LDS
-//                      plane buffer; column FFTs then emit only the m1 kept rows,
-//                      already in window (fftshift-ed) order, scaled.
+// K1  k_fwd_stream     one workgroup per (b, c) plane, streaming the plane in
+//                      D = H/32 chunks of 32 rows h = c + D*h2 (h2 < 32):
+//                        * row real FFTs (two rows packed as one complex line,
+//                          LDS-exchanged four-step) keep the m2h kept bins;
+//                        * a 32-point DFT down each kept column of the chunk
+//                          (4 lanes x 8 points) gives the chunk's spectrum at
+//                          every frequency mod 32;
+//                        * the twiddle w_H^(-kh c) folds it into register
+//                          accumulators of the m1 kept rows.
+//                      x is read once with the next chunk's rows in flight;
+//                      LDS holds one chunk, so 3 workgroups share a CU.
 // K2  contraction      fno_generic.hip (mode-wise complex GEMM).
-// K3  k_inv_cols       one workgroup per (b, o) plane: inverse column FFTs of
-//                      the m2h kept columns from the m1 window rows, staged in
-//                      LDS and written as Z[b,o,h,kw] with coalesced stores.
-// K4  k_row_epilogue   one workgroup per (b, h) output row: inverse row real
-//                      FFTs of Z for every output channel (two channels packed
-//                      per complex line), the 1x1-conv skip on fp32 MFMA
-//                      (v_mfma_f32_32x32x2f32, accumulators = skip result),
-//                      bias and exact erf GELU, one write of y.
+// K3  k_epilogue_fold  one workgroup per (b, r), TH output rows h = r + s*H/TH:
+//                        * the inverse column transform of those TH rows is
+//                          folded from the m1 window rows of every output
+//                          channel (m1/TH complex MACs per value + a TH-point
+//                          DFT), straight from the contraction output -- no
+//                          column-transformed intermediate goes through HBM;
+//                        * per row: inverse row real FFTs of all output
+//                          channels (two channels per complex line) into LDS,
+//                          the 1x1-conv skip on fp32 MFMA
+//                          (v_mfma_f32_32x32x2f32, x operand prefetched one row
+//                          ahead), bias and erf GELU, one coalesced write of y.
+//                      Workgroups of one sample are placed on one XCD so the
+//                      sample's spectrum stays in that XCD's L2.
 //
 // Semantics follow SpectralConv.forward (neuralop/layers/spectral_convolution.py
 // :429-568) with output size == input size, and the post-activation block of
 // FNOBlocks (neuralop/layers/fno_block.py:331-361).
 #include "fno_fft_lds.h"
+
+#include <type_traits>
 
 namespace fno {
 
@@ -32,102 +46,170 @@ __device__ __forceinline__ void fill_twiddles(float2* tw) {
 }
 
 // ------------------------------------------------------------------------ K1
-template <int H, int W, int BLOCK>
-__global__ void __launch_bounds__(BLOCK)
-k_fwd_plane(const float* __restrict__ x, float2* __restrict__ xhat, int m1, int m2h, int TS,
-            float scale) {
+// Kept window of a plane: rows kh in [kmin, kmin + m1), kmin = -(m1/2), stored
+// at window row kh - kmin; columns kw < m2h.  A kept row kh is reached from its
+// residue k' = kh mod 32 as kh = k0(k') + 32 e, k0 = kmin + ((k' - kmin) & 31).
+template <int H, int W, int KPR>
+__global__ void __launch_bounds__(16 * LinePlan<W>::T)
+k_fwd_stream(const float* __restrict__ x, float2* __restrict__ xhat, int m1, int m2h, float scale) {
   using PW = LinePlan<W>;
-  using PH = LinePlan<H>;
+  constexpr int T = PW::T, R = PW::R, Q = PW::Q;
+  constexpr int BLOCK = 16 * T;
+  constexpr int D = H / 32;
+  static_assert(H % 32 == 0 && D >= 1, "H must be a multiple of 32");
   extern __shared__ float4 smem4[];
-  float2* twW = reinterpret_cast<float2*>(smem4);
-  float2* twH = twW + W;
-  float2* plane = twH + H;                 // [H][TS]
-  float2* exall = plane + H * TS;          // per-group exchange slices
+  float2* twW = reinterpret_cast<float2*>(smem4);  // w_W^t, t < W
+  float2* twH = twW + W;                             // w_H^t, t < H
+  float2* exall = twH + H;                           // 16 lines x W
+  float2* S = exall + 16 * W;                        // [32][SP] chunk spectrum
+  const int SP = m2h | 1;
   fill_twiddles<W>(twW);
   fill_twiddles<H>(twH);
-  __syncthreads();
 
+  const int tid = threadIdx.x;
+  const int L = tid / T, t = tid % T;     // line of the chunk, lane in the line
   const float* xp = x + (int64_t)blockIdx.x * H * W;
-  // ---- rows: pairs (2r, 2r+1) packed as one complex line
+
+  // column stage roles: 4 lanes per kept column
+  const int col = tid >> 2, j = tid & 3;
+  const bool col_on = col < m2h;
+  const int kmin = -(m1 / 2);
+  float2 acc[2][4][KPR];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int e = 0; e < KPR; ++e) acc[a][b][e] = make_float2(0.f, 0.f);
+
+  // rows of line L in chunk c: h = c + D*(2L), c + D*(2L+1)
+  // x is addressed as a uniform plane base plus 32-bit lane offsets, so the
+  // compiler keeps one offset register per row instead of 64-bit pointers
+  float va[R], vb[R];
   {
-    constexpr int T = PW::T, R = PW::R, Q = PW::Q;
-    constexpr int G = BLOCK / T;
-    const int g = threadIdx.x / T, t = threadIdx.x % T;
-    float2* ex = exall + g * W;
-    for (int pr = g; pr < H / 2; pr += G) {
-      const float* ra = xp + (2 * pr) * W;
-      const float* rb = ra + W;
-      float2 v[R];
+    const uint32_t oa = (uint32_t)(D * (2 * L)) * W + t;
 #pragma unroll
-      for (int s = 0; s < R; ++s) v[s] = make_float2(ra[t + T * s], rb[t + T * s]);
-      float2 out[Q][T];
-      line_fft<W, -1>(v, ex, twW, t, out);
-      // Z[k] in natural order for the bins the split needs
-#pragma unroll
-      for (int q = 0; q < Q; ++q)
-#pragma unroll
-        for (int s = 0; s < T; ++s) {
-          const int k = t + T * q + R * s;
-          if (k < m2h || k > W - m2h) ex[k] = out[q][s];
-        }
-      wave_sync();
-      // X_a[k] = (Z[k] + conj Z[W-k]) / 2,  X_b[k] = -i (Z[k] - conj Z[W-k]) / 2
-      for (int k = t; k < m2h; k += T) {
-        const float2 zk = ex[k];
-        const float2 zn = ex[(W - k) & (W - 1)];
-        const float2 xa = make_float2(0.5f * (zk.x + zn.x), 0.5f * (zk.y - zn.y));
-        const float2 xb = make_float2(0.5f * (zk.y + zn.y), 0.5f * (zn.x - zk.x));
-        plane[(2 * pr) * TS + k] = xa;
-        plane[(2 * pr + 1) * TS + k] = xb;
-      }
-      wave_sync();
+    for (int s = 0; s < R; ++s) {
+      va[s] = xp[oa + T * s];
+      vb[s] = xp[oa + D * W + T * s];
     }
   }
   __syncthreads();
-  // ---- columns: kept bins only, emit kept rows in window order
-  {
-    constexpr int T = PH::T, R = PH::R, Q = PH::Q;
-    constexpr int G = BLOCK / T;
-    const int g = threadIdx.x / T, t = threadIdx.x % T;
-    float2* ex = exall + g * H;
-    float2* op = xhat + (int64_t)blockIdx.x * m1 * m2h;
-    const int pos = m1 - m1 / 2;  // kept non-negative frequencies 0..pos-1
-    const int neg = m1 / 2;       // kept negative frequencies -neg..-1
-    for (int kw = g; kw < m2h; kw += G) {
-      float2 v[R];
+
+#pragma unroll 1
+  for (int c = 0; c < D; ++c) {
+    // thread index laundered through an empty asm so per-lane addresses are
+    // recomputed in the loop rather than hoisted into live registers
+    int tl = tid;
+    asm volatile("" : "+v"(tl));
+    const int Ll = tl / T, tt = tl % T;
+    float2 v[R];
 #pragma unroll
-      for (int s = 0; s < R; ++s) v[s] = plane[(t + T * s) * TS + kw];
+    for (int s = 0; s < R; ++s) v[s] = make_float2(va[s], vb[s]);
+    if (c + 1 < D) {  // next chunk's rows in flight during this chunk
+      const uint32_t oa = (uint32_t)(c + 1 + D * (2 * Ll)) * W + tt;
+#pragma unroll
+      for (int s = 0; s < R; ++s) {
+        va[s] = xp[oa + T * s];
+        vb[s] = xp[oa + D * W + T * s];
+      }
+    }
+    // ---- row pair FFT, keep bins k < m2h and their mirrors
+    {
+      float2* exl = exall + Ll * W;
       float2 out[Q][T];
-      line_fft<H, -1>(v, ex, twH, t, out);
+      line_fft<W, -1>(v, exl, twW, tt, out);
 #pragma unroll
       for (int q = 0; q < Q; ++q)
 #pragma unroll
         for (int s = 0; s < T; ++s) {
-          const int k = t + T * q + R * s;
-          int j = -1;
-          if (k < pos) j = k + neg;
-          else if (k >= H - neg) j = k - H + neg;
-          if (j >= 0) op[j * m2h + kw] = cscale(out[q][s], scale);
+          const int k = tt + T * q + R * s;
+          if (k < m2h || k > W - m2h) exl[k] = out[q][s];
         }
+      wave_sync();
+      // X_a[k] = (Z[k] + conj Z[W-k]) / 2,  X_b[k] = -i (Z[k] - conj Z[W-k]) / 2
+      for (int k = tt; k < m2h; k += T) {
+        const float2 zk = exl[k];
+        const float2 zn = exl[(W - k) & (W - 1)];
+        S[(2 * Ll) * SP + k] = make_float2(0.5f * (zk.x + zn.x), 0.5f * (zk.y - zn.y));
+        S[(2 * Ll + 1) * SP + k] = make_float2(0.5f * (zk.y + zn.y), 0.5f * (zn.x - zk.x));
+      }
     }
+    __syncthreads();
+    // ---- 32-point column DFTs of the chunk, folded into the kept rows
+    if (col_on) {
+      const int col = tl >> 2, j = tl & 3;
+      float2 f[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) f[u] = S[(j + 4 * u) * SP + col];
+      dft8<-1>(f);
+#pragma unroll
+      for (int k1 = 1; k1 < 8; ++k1) f[k1] = cmulc(f[k1], twH[((j * k1) & 31) * D]);
+      wave_sync();
+#pragma unroll
+      for (int k1 = 0; k1 < 8; ++k1) S[(j * 8 + k1) * SP + col] = f[k1];
+      wave_sync();
+#pragma unroll
+      for (int e2 = 0; e2 < 2; ++e2) {
+        const int k1 = 2 * j + e2;
+        float2 g0 = S[(0 * 8 + k1) * SP + col], g1 = S[(1 * 8 + k1) * SP + col];
+        float2 g2 = S[(2 * 8 + k1) * SP + col], g3 = S[(3 * 8 + k1) * SP + col];
+        dft4<-1>(g0, g1, g2, g3);
+        const float2 P[4] = {g0, g1, g2, g3};
+#pragma unroll
+        for (int k2 = 0; k2 < 4; ++k2) {
+          const int kr = k1 + 8 * k2;  // frequency mod 32
+          const int k0 = kmin + ((kr - kmin) & 31);
+#pragma unroll
+          for (int e = 0; e < KPR; ++e) {
+            const int kh = k0 + 32 * e;
+            // w_H^(-kh c): the positive-exponent table at (-kh c) mod H
+            if (kh < kmin + m1) cfma(acc[e2][k2][e], P[k2], twH[(-kh * c) & (H - 1)]);
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (col_on) {
+    float2* op = xhat + (int64_t)blockIdx.x * m1 * m2h;
+#pragma unroll
+    for (int e2 = 0; e2 < 2; ++e2)
+#pragma unroll
+      for (int k2 = 0; k2 < 4; ++k2) {
+        const int kr = 2 * j + e2 + 8 * k2;
+        const int k0 = kmin + ((kr - kmin) & 31);
+#pragma unroll
+        for (int e = 0; e < KPR; ++e) {
+          const int kh = k0 + 32 * e;
+          if (kh < kmin + m1) op[(kh - kmin) * m2h + col] = cscale(acc[e2][k2][e], scale);
+        }
+      }
   }
 }
 
 // ------------------------------------------------------------------------ K3
+// Inverse column transform of one (b, o) plane: the m2h kept columns of the
+// window spectrum, zero-padded to H rows at their frequencies, inverse
+// FFT-ed along H and written row-major as Z[b][h][o][kw] so that K4 reads one
+// contiguous block per output row.
 template <int H, int BLOCK>
 __global__ void __launch_bounds__(BLOCK)
-k_inv_cols(const float2* __restrict__ yhat, float2* __restrict__ z, int m1, int m2h, int TS) {
+k_inv_cols(const float2* __restrict__ yhat, float2* __restrict__ z, int Co, int m1, int m2h) {
   using PH = LinePlan<H>;
+  constexpr int T = PH::T, R = PH::R, Q = PH::Q;
+  constexpr int G = BLOCK / T;
   extern __shared__ float4 smem4[];
   float2* twH = reinterpret_cast<float2*>(smem4);
-  float2* zs = twH + H;                   // [H][TS]
-  float2* exall = zs + H * TS;            // groups x H
+  const int TS = m2h | 1;
+  float2* zs = twH + H;          // [H][TS]
+  float2* exall = zs + H * TS;   // G x H
   fill_twiddles<H>(twH);
-  const float2* win = yhat + (int64_t)blockIdx.x * m1 * m2h;   // [m1][m2h] window
+  const int plane = blockIdx.x;  // b * Co + o
+  const int b = plane / Co, o = plane - b * Co;
+  const float2* win = yhat + (int64_t)plane * m1 * m2h;   // [m1][m2h] window
   __syncthreads();
   {
-    constexpr int T = PH::T, R = PH::R, Q = PH::Q;
-    constexpr int G = BLOCK / T;
     const int g = threadIdx.x / T, t = threadIdx.x % T;
     float2* ex = exall + g * H;
     const int pos = m1 - m1 / 2, neg = m1 / 2;
@@ -150,10 +232,10 @@ k_inv_cols(const float2* __restrict__ yhat, float2* __restrict__ z, int m1, int 
     }
   }
   __syncthreads();
-  float2* zp = z + (int64_t)blockIdx.x * H * m2h;
+  float2* zp = z + ((int64_t)b * H * Co + o) * m2h;   // + h * Co * m2h
   for (int i = threadIdx.x; i < H * m2h; i += BLOCK) {
     const int h = i / m2h, kw = i - h * m2h;
-    zp[i] = zs[h * TS + kw];
+    zp[(int64_t)h * Co * m2h + kw] = zs[h * TS + kw];
   }
 }
 
@@ -162,200 +244,388 @@ k_inv_cols(const float2* __restrict__ yhat, float2* __restrict__ z, int m1, int 
 //   A (32 x 2):  lane l supplies A[l % 32][l / 32]
 //   B (2 x 32):  lane l supplies B[l / 32][l % 32]
 //   D (32 x 32): lane l, register r holds D[8*(r/4) + 4*(l/32) + r%4][l % 32]
-// Here M = output pixels of the row, N = output channels, K = input channels.
-template <int W, int CO>
-__global__ void __launch_bounds__(256)
+// Here M = output channels, N = pixels of the row, K = input channels.
+//
+// One workgroup runs TR (even) consecutive rows of one sample as a software
+// pipeline.  Step s, between two barriers:
+//   1. issue the loads of row s+1 (x operand, Z bins) into the idle buffers
+//   2. the MFMA skip of row s, each k-step interleaved (sched_barrier) with
+//      bias + GELU + store of EPK elements of row s-1, so the matrix cores and
+//      the VALU work at the same time
+//   3. inverse row FFTs of row s into spec buffer s & 1
+// Accumulators, operands and spec buffers are double-buffered by row parity.
+//
+// LDS (floats): twW [2W] | wsT [CI*CO] | bias [CO] | spec [2][CO][W+8]
+template <int W>
+__host__ __device__ constexpr int spec_stride() { return W + 8; }
+
+// Raw buffer resource over [base, base + bytes): loads and stores take a
+// 32-bit VGPR byte offset plus an SGPR byte offset, so per-element address
+// arithmetic stays 32-bit and mostly scalar.  Reads past the end return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+// soff must be wave-uniform; readfirstlane states that to the compiler so it
+// stays in an SGPR.  The b32/b64 builtins move raw bits: values are bit-cast.
+__device__ __forceinline__ float ld_f32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff,
+                                                  __builtin_amdgcn_readfirstlane((int)soff), 0));
+}
+__device__ __forceinline__ float2 ld_f64(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(
+      float2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff,
+                                                   __builtin_amdgcn_readfirstlane((int)soff), 0));
+}
+__device__ __forceinline__ void st_f32(float v, __amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                       uint32_t soff) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, (int)voff,
+                                        __builtin_amdgcn_readfirstlane((int)soff), 0);
+}
+
+template <int H, int W, int CO, int CI, int NB>
+__global__ void __launch_bounds__(CO / 2 * LinePlan<W>::T)
 k_row_epilogue(const float* __restrict__ x, const float2* __restrict__ z,
                const float* __restrict__ skip_w, const float* __restrict__ bias,
-               float* __restrict__ y, int H, int Ci, int m2h, int skip_kind, int act,
-               float inv_scale) {
+               float* __restrict__ y, int TR, int m2h, int skip_kind, int act, float inv_scale) {
   using PW = LinePlan<W>;
-  constexpr int MT = W / 4 / 32;       // 32-pixel tiles per wave
-  constexpr int NT = CO / 32;          // 32-channel tiles
-  constexpr int AST = W + 4;           // LDS row stride of the irfft chunk
-  static_assert(MT >= 1, "row too short for the wave tiling");
+  constexpr int T = PW::T, R = PW::R, Q = PW::Q;
+  constexpr int BLOCK = CO / 2 * T;
+  constexpr int SS = spec_stride<W>();
+  constexpr int NPX = W / 32;                  // 32-pixel tiles of a row
+  constexpr int MT_PER = (CO >= 64) ? 2 : 1;   // channel tiles per wave
+  constexpr int NT_PER = 2 / MT_PER;           // pixel tiles per wave
+  constexpr int KS = CI / 2;                   // MFMA k-steps
+  constexpr int NEL = MT_PER * NT_PER * 16;    // epilogue elements per lane and row
+  constexpr int EPK = NEL / KS;                // ... per k-step
+  constexpr uint32_t HW = (uint32_t)H * W;
+  static_assert(CO % 32 == 0 && CI % 2 == 0, "channel counts");
+  static_assert((CO / 32) * NPX == 2 * (BLOCK / 64), "two MFMA tiles per wave");
+  static_assert(NEL % KS == 0, "epilogue elements must spread evenly over the k-steps");
   extern __shared__ float4 smem4[];
   float2* twW = reinterpret_cast<float2*>(smem4);
-  float* wsk = reinterpret_cast<float*>(twW + W);          // [CO][Ci] skip weight
-  float* achunk = wsk + (skip_kind == FNO_SKIP_LINEAR ? CO * Ci : 0);  // [32][AST]
+  float* wsT = reinterpret_cast<float*>(twW + W);
+  float* bS = wsT + (skip_kind == FNO_SKIP_LINEAR ? CI * CO : 0);
+  float* spec = bS + CO + (CO & 1);   // [2][CO][SS]: irfft * scale + bias
 
-  const int b = blockIdx.x / H, h = blockIdx.x % H;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int p_wave = wave * (W / 4);
+  const int RB = H / TR;
+  const int b = blockIdx.x / RB, h0 = (blockIdx.x % RB) * TR;
+  const int tid = threadIdx.x, wave = tid >> 6;
+  const bool linear = (skip_kind == FNO_SKIP_LINEAR);
+  const bool gated = (skip_kind == FNO_SKIP_SOFT_GATING || skip_kind == FNO_SKIP_IDENTITY);
+  const bool gelu_on = (act == FNO_ACT_GELU);
+  const int pxt0 = (CO >= 64) ? (wave % NPX) : 2 * wave;
+  const int mt0 = (CO >= 64) ? 2 * (wave / NPX) : 0;
+  // per-sample bases (uniform); buffer descriptors are built where used so
+  // they stay in scalar registers
+  const float* xs = x + (size_t)b * CI * HW;
+  const float2* zs = z + (size_t)b * H * CO * m2h;
+  float* ys = y + (size_t)b * CO * HW;
+  constexpr uint32_t xbytes = CI * HW * 4u, ybytes = CO * HW * 4u;
+  const uint32_t zbytes = (uint32_t)H * CO * m2h * 8u;
+
   fill_twiddles<W>(twW);
-  if (skip_kind == FNO_SKIP_LINEAR)
-    for (int i = threadIdx.x; i < CO * Ci; i += 256) wsk[i] = skip_w[i];
-  __syncthreads();
+  if (linear)
+    for (int i = tid; i < CI * CO; i += BLOCK) {
+      const int ci = i / CO, o = i - ci * CO;
+      wsT[i] = skip_w[o * CI + ci];
+    }
+  for (int i = tid; i < CO; i += BLOCK) bS[i] = bias ? bias[i] : 0.f;
 
-  v16f acc[MT][NT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[mt][nt][r] = 0.f;
+  float xr[2][NT_PER][KS];
+  float2 za[2][NB], zc[2][NB];   // bins k = t + T*n of channels 2g and 2g+1
+  v16f acc[2][MT_PER][NT_PER];
 
-  const int64_t HW = (int64_t)H * W;
-  const float* xb = x + (int64_t)b * Ci * HW + (int64_t)h * W;
-  if (skip_kind == FNO_SKIP_LINEAR) {
-    const int kk = lane >> 5, mm = lane & 31;
-    for (int i0 = 0; i0 < Ci; i0 += 2) {
-      float a[MT];
+  // ---- loads of row h into buffer BUF (tv: laundered thread index)
+  auto load_row = [&](int h, int tv, auto buf_c) __attribute__((always_inline)) {
+    constexpr int buf = decltype(buf_c)::value;
+    const int ln = tv & 63;
+    if (linear) {
+      const __amdgpu_buffer_rsrc_t rx = make_rsrc(xs, xbytes);
+      const uint32_t xo = ((uint32_t)(ln >> 5) * HW + (uint32_t)h * W + 32 * pxt0 + (ln & 31)) * 4u;
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) a[mt] = xb[(int64_t)(i0 + kk) * HW + p_wave + 32 * mt + mm];
+      for (int n = 0; n < NT_PER; ++n)
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const float bv = wsk[(32 * nt + mm) * Ci + i0 + kk];
+        for (int ks = 0; ks < KS; ++ks)
+          xr[buf][n][ks] = __builtin_bit_cast(
+              float, __builtin_amdgcn_raw_buffer_load_b32(rx, (int)(xo + 128u * n),
+                                                          (int)((uint32_t)(2 * ks) * HW * 4u), 0));
+    }
+    const __amdgpu_buffer_rsrc_t rz = make_rsrc(zs, zbytes);
+    const int tl = tv % T;
+    const uint32_t zo = (((uint32_t)h * CO + 2 * (tv / T)) * m2h + tl) * 8u;
+    const int m2o = __builtin_amdgcn_readfirstlane(m2h * 8);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[mt], bv, acc[mt][nt], 0, 0, 0);
+    for (int n = 0; n < NB; ++n) {
+      const bool in = tl + T * n < m2h;
+      const float2 a = __builtin_bit_cast(
+          float2, __builtin_amdgcn_raw_buffer_load_b64(rz, (int)(zo + 8u * T * n), 0, 0));
+      const float2 c = __builtin_bit_cast(
+          float2, __builtin_amdgcn_raw_buffer_load_b64(rz, (int)(zo + 8u * T * n), m2o, 0));
+      za[buf][n] = in ? a : make_float2(0.f, 0.f);
+      zc[buf][n] = in ? c : make_float2(0.f, 0.f);
+    }
+  };
+
+  // ---- inverse row FFTs of the Z bins in buffer BUF into spec buffer BUF,
+  //      written as irfft * inv_scale + bias
+  auto irfft_row = [&](int tv, auto buf_c) __attribute__((always_inline)) {
+    constexpr int buf = decltype(buf_c)::value;
+    const int gl = tv / T, tt = tv % T;
+    float* rowa = spec + (buf * CO + 2 * gl) * SS;
+    float2* ex = reinterpret_cast<float2*>(rowa);
+    // stage the line's bins (Za[k], Zb[k] interleaved) to gather the mirrors
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const int k = tt + T * u;
+      if (k < m2h) {
+        ex[2 * k] = za[buf][u];
+        ex[2 * k + 1] = zc[buf][u];
       }
     }
-  } else if (skip_kind == FNO_SKIP_SOFT_GATING || skip_kind == FNO_SKIP_IDENTITY) {
+    wave_sync();
+    float2 v[R];
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      const int o = 32 * nt + (lane & 31);
-      const float gate = (skip_kind == FNO_SKIP_SOFT_GATING) ? skip_w[o] : 1.f;
+    for (int u = 0; u < R; ++u) {
+      const int k = tt + T * u;
+      float2 val = make_float2(0.f, 0.f);
+      if (u < NB && k < m2h) {
+        float2 a = za[buf][u < NB ? u : 0], c = zc[buf][u < NB ? u : 0];
+        if (k == 0 || 2 * k == W) {  // Hermitian fix-up of the irfft input
+          a.y = 0.f;
+          c.y = 0.f;
+        }
+        val = make_float2(a.x - c.y, a.y + c.x);           // Za + i Zb
+      } else if (k > W / 2 && W - k < m2h) {
+        const float2 a = ex[2 * (W - k)], c = ex[2 * (W - k) + 1];
+        val = make_float2(a.x + c.y, c.x - a.y);           // conj Za + i conj Zb
+      }
+      v[u] = val;
+    }
+    const float ba = bS[2 * gl], bb = bS[2 * gl + 1];
+    wave_sync();
+    float2 out[Q][T];
+    line_fft<W, +1>(v, ex, twW, tt, out);
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+    for (int q = 0; q < Q; ++q)
+#pragma unroll
+      for (int u = 0; u < T; ++u) {
+        const int p = tt + T * q + R * u;
+        rowa[p] = fmaf(out[q][u].x, inv_scale, ba);
+        rowa[SS + p] = fmaf(out[q][u].y, inv_scale, bb);
+      }
+  };
+
+  // element e of the lane's NEL: tile (m, n), register r
+  auto el_m = [](int e) { return e / (NT_PER * 16); };
+  auto el_n = [](int e) { return (e / 16) % NT_PER; };
+  // spec address of element e (o = channel, px = pixel) for lane ln
+  auto spec_idx = [&](int e, int ln, int buf) __attribute__((always_inline)) {
+    const int r = e % 16;
+    const int o = 32 * (mt0 + el_m(e)) + 8 * (r >> 2) + 4 * (ln >> 5) + (r & 3);
+    const int px = 32 * (pxt0 + el_n(e)) + (ln & 31);
+    return (buf * CO + o) * SS + px;
+  };
+  // final value and store of element e of row h from (acc, spec value)
+  auto epi_store = [&](int e, float accv, float specv, uint32_t yo) __attribute__((always_inline)) {
+    const int r = e % 16;
+    const uint32_t oc = 32 * (mt0 + el_m(e)) + 8 * (r >> 2) + (r & 3);   // o minus the lane part
+    float v = accv + specv;
+    v = gelu_on ? gelu_erf(v) : v;   // branch-free: the select keeps one basic block
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), make_rsrc(ys, ybytes),
+                                          (int)(yo + 128u * el_n(e)), (int)(oc * HW * 4u), 0);
+  };
+
+  // ---- the skip accumulators of row h (gated / identity / none)
+  auto skip_direct = [&](int h, int ln, auto buf_c) __attribute__((always_inline)) {
+    constexpr int buf = decltype(buf_c)::value;
+#pragma unroll
+    for (int m = 0; m < MT_PER; ++m)
+#pragma unroll
+      for (int n = 0; n < NT_PER; ++n)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int p = p_wave + 32 * mt + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-          acc[mt][nt][r] = gate * xb[(int64_t)o * HW + p];
-        }
-    }
-  }
-
-  // ---- inverse row FFTs, 32 output channels (16 packed pairs) per chunk
-  constexpr int T = PW::T, R = PW::R, Q = PW::Q;
-  constexpr int G = 256 / T;
-  const int g = threadIdx.x / T, t = threadIdx.x % T;
-  const float2* zb = z + ((int64_t)b * CO * H + h) * m2h;   // + o*H*m2h
-  const int64_t zo = (int64_t)H * m2h;
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    if (g < 16) {
-      const int oa = 32 * nt + 2 * g;
-      float* slot = achunk + (2 * g) * AST;
-      float2* ex = reinterpret_cast<float2*>(slot);
-      const float2* za = zb + oa * zo;
-      const float2* zbb = za + zo;
-      // Z2[k] = Ya[k] + i Yb[k] extended with Hermitian symmetry; imaginary
-      // parts of bin 0 and bin W/2 are dropped (irfft semantics)
-      float2 v[R];
-#pragma unroll
-      for (int s = 0; s < R; ++s) {
-        const int k = t + T * s;
-        float2 val = make_float2(0.f, 0.f);
-        if (k < m2h) {
-          float2 ya = za[k], yb = zbb[k];
-          if (k == 0 || 2 * k == W) {
-            ya.y = 0.f;
-            yb.y = 0.f;
+          float v = 0.f;
+          if (gated) {
+            const int o = 32 * (mt0 + m) + 8 * (r >> 2) + 4 * (ln >> 5) + (r & 3);
+            const int px = 32 * (pxt0 + n) + (ln & 31);
+            const float gate = (skip_kind == FNO_SKIP_SOFT_GATING) ? skip_w[o] : 1.f;
+            v = gate * xs[(size_t)o * HW + (size_t)h * W + px];
           }
-          val = make_float2(ya.x - yb.y, ya.y + yb.x);
-        } else if (k > W / 2 && W - k < m2h) {
-          const float2 ya = za[W - k], yb = zbb[W - k];
-          // conj(ya) + i conj(yb)
-          val = make_float2(ya.x + yb.y, yb.x - ya.y);
+          acc[buf][m][n][r] = v;
         }
-        v[s] = val;
-      }
-      float2 out[Q][T];
-      line_fft<W, +1>(v, ex, twW, t, out);
-#pragma unroll
-      for (int q = 0; q < Q; ++q)
-#pragma unroll
-        for (int s = 0; s < T; ++s) {
-          const int p = t + T * q + R * s;
-          slot[p] = out[q][s].x * inv_scale;
-          slot[AST + p] = out[q][s].y * inv_scale;
-        }
+  };
+
+  // ---- pipeline step s: MFMA (row s) with EPI of row s-1, then irfft (row s)
+  auto step = [&](int s, auto cur_c, auto mf_c, auto ep_c) __attribute__((always_inline)) {
+    constexpr int cur = decltype(cur_c)::value, prv = cur ^ 1;
+    constexpr bool MF = decltype(mf_c)::value, EP = decltype(ep_c)::value;
+    // Thread index laundered through an empty asm: the addresses derived from
+    // it are recomputed in the step instead of hoisted into live registers.
+    int tv = tid;
+    asm volatile("" : "+v"(tv));
+    const int ln = tv & 63;
+    const int h = h0 + s;
+    if constexpr (MF) {
+      if (s + 1 < TR) load_row(h + 1, tv, std::integral_constant<int, prv>());
+      if (!linear) skip_direct(h, ln, cur_c);
     }
-    __syncthreads();
-    {
-      const int o = 32 * nt + (lane & 31);
-      const float bo = bias ? bias[o] : 0.f;
-      const float* arow = achunk + (lane & 31) * AST;
+    const uint32_t yo = ((uint32_t)(4 * (ln >> 5)) * HW + (uint32_t)(h - 1) * W +
+                         32 * pxt0 + (ln & 31)) * 4u;
+    if (MF && linear) {
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+      for (int m = 0; m < MT_PER; ++m)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int p = p_wave + 32 * mt + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-          float v = acc[mt][nt][r] + arow[p] + bo;
-          if (act == FNO_ACT_GELU) v = gelu_erf(v);
-          acc[mt][nt][r] = v;
-        }
-    }
-    __syncthreads();
-  }
-  // ---- store y[b, o, h, p]: four consecutive pixels per register group
-  float* yb = y + (int64_t)b * CO * HW + (int64_t)h * W;
+        for (int n = 0; n < NT_PER; ++n)
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const int o = 32 * nt + (lane & 31);
+          for (int r = 0; r < 16; ++r) acc[cur][m][n][r] = 0.f;
+      const float* arow = wsT + (ln >> 5) * CO + 32 * mt0 + (ln & 31);
+      // LDS operands one k-step ahead: A (weights) and the spec values of
+      // the elements stored in the next step
+      float a_c[MT_PER], a_n[MT_PER], sp_c[EPK], sp_n[EPK];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+      for (int m = 0; m < MT_PER; ++m) a_c[m] = arow[32 * m];
+      if constexpr (EP) {
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        const int p = p_wave + 32 * mt + 8 * r4 + 4 * (lane >> 5);
-        float4 v = make_float4(acc[mt][nt][4 * r4], acc[mt][nt][4 * r4 + 1], acc[mt][nt][4 * r4 + 2],
-                               acc[mt][nt][4 * r4 + 3]);
-        *reinterpret_cast<float4*>(yb + (int64_t)o * HW + p) = v;
+        for (int i = 0; i < EPK; ++i) sp_c[i] = spec[spec_idx(i, ln, prv)];
       }
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        if (ks + 1 < KS) {
+#pragma unroll
+          for (int m = 0; m < MT_PER; ++m) a_n[m] = arow[2 * (ks + 1) * CO + 32 * m];
+          if constexpr (EP) {
+#pragma unroll
+            for (int i = 0; i < EPK; ++i) sp_n[i] = spec[spec_idx((ks + 1) * EPK + i, ln, prv)];
+          }
+        }
+#pragma unroll
+        for (int m = 0; m < MT_PER; ++m)
+#pragma unroll
+          for (int n = 0; n < NT_PER; ++n)
+            acc[cur][m][n] =
+                __builtin_amdgcn_mfma_f32_32x32x2f32(a_c[m], xr[cur][n][ks], acc[cur][m][n], 0, 0, 0);
+        if constexpr (EP) {
+#pragma unroll
+          for (int i = 0; i < EPK; ++i) {
+            const int e = ks * EPK + i;
+            epi_store(e, acc[prv][el_m(e)][el_n(e)][e % 16], sp_c[i], yo);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int m = 0; m < MT_PER; ++m) a_c[m] = a_n[m];
+#pragma unroll
+        for (int i = 0; i < EPK; ++i) sp_c[i] = sp_n[i];
+      }
+    } else if constexpr (EP) {
+#pragma unroll
+      for (int e = 0; e < NEL; ++e)
+        epi_store(e, acc[prv][el_m(e)][el_n(e)][e % 16], spec[spec_idx(e, ln, prv)], yo);
+    }
+    if constexpr (MF) irfft_row(tv, cur_c);
+    __syncthreads();
+  };
+
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using BT = std::integral_constant<bool, true>;
+  using BF = std::integral_constant<bool, false>;
+  load_row(h0, tid, I0());
+  __syncthreads();
+  step(0, I0(), BT(), BF());
+#pragma unroll 1
+  for (int s = 1; s < TR; s += 2) {
+    step(s, I1(), BT(), BT());
+    if (s + 1 < TR) step(s + 1, I0(), BT(), BT());
   }
+  step(TR, I0(), BF(), BT());   // TR even: row TR-1 sits in buffer 1
 }
 
 // ============================================================== host side
 int contract_dense(const float2* X, const float2* W, float2* Y, int B, int Ci, int Co, int64_t M,
                    int64_t sWi, int64_t sWo, int64_t sWk, hipStream_t st);
+int rfft_window(const float* x, float2* xhat, int64_t planes, int32_t ndim, const int32_t* sizes,
+                const int32_t* modes, int32_t norm, void* ws, size_t ws_bytes, hipStream_t st);
+size_t rfft_window_ws(int64_t planes, int32_t ndim, const int32_t* sizes, const int32_t* modes);
 
 static constexpr size_t kMaxLds = 160 * 1024;
 
 static int line_lanes(int n) { return n >= 256 ? 16 : 8; }
-static int fwd_block(int H, int W) { return (H >= 256 || W >= 256) ? 512 : 256; }
-static int inv_block(int H) { return H >= 256 ? 512 : 256; }
 
 static size_t fwd_lds_bytes(int H, int W, int m2h) {
-  const int blk = fwd_block(H, W);
-  const int exW = blk / line_lanes(W) * W, exH = blk / line_lanes(H) * H;
-  const int TS = m2h | 1;
-  return (size_t)(W + H + H * TS + (exW > exH ? exW : exH)) * sizeof(float2);
+  const int SP = m2h | 1;
+  return (size_t)(W + H + 16 * W + 32 * SP) * sizeof(float2);
 }
+
+static int fwd_kpr(int m1) { return m1 <= 32 ? 1 : (m1 <= 64 ? 2 : 4); }
+
+// K1 covers the plane when the kept columns fit one pass of the column stage
+// (4 lanes per column) and the kept rows fit the register accumulators.
+static bool fwd_supported(int H, int W, int m1, int m2h) {
+  if (!(H == 64 || H == 128 || H == 256)) return false;
+  if (!(W == 128 || W == 256)) return false;
+  if (m1 < 1 || m1 > 128 || m1 > H) return false;
+  if (m2h < 1 || m2h > 16 * line_lanes(W) / 4) return false;
+  return fwd_lds_bytes(H, W, m2h) <= kMaxLds;
+}
+
+static int inv_block(int H) { return H >= 256 ? 512 : 256; }
+
 static size_t inv_lds_bytes(int H, int m2h) {
   const int TS = m2h | 1;
   return (size_t)(H + H * TS + inv_block(H) / line_lanes(H) * H) * sizeof(float2);
 }
+
 static size_t epi_lds_bytes(int W, int Co, int Ci, int skip_kind) {
-  return (size_t)W * sizeof(float2) +
-         (size_t)(skip_kind == FNO_SKIP_LINEAR ? Co * Ci : 0) * sizeof(float) +
-         (size_t)32 * (W + 4) * sizeof(float);
+  size_t f = 2 * (size_t)W + (skip_kind == FNO_SKIP_LINEAR ? (size_t)Ci * Co : 0) + (size_t)Co +
+             (Co & 1);
+  f += 2 * (size_t)Co * (W + 8);
+  return f * sizeof(float);
 }
 
+// bin slots per lane of the row irfft: ceil(m2h / lanes per line)
+static int epi_bins(int W, int m2h) {
+  const int T = line_lanes(W);
+  const int nb = (m2h + T - 1) / T;
+  return nb <= 2 ? 2 : (nb <= 3 ? 3 : (nb <= 5 ? 5 : 9));
+}
+
+static int epi_rows_per_block(int H) { return H >= 64 ? 16 : H; }
+
+static bool epi_supported(int H, int W, int Ci, int Co, int m1, int m2h, int skip_kind) {
+  if (!(W == 128 || W == 256)) return false;
+  if (!(H == 64 || H == 128 || H == 256)) return false;
+  if (!(Co == 32 || Co == 64)) return false;
+  if (skip_kind == FNO_SKIP_LINEAR && !(Ci == 32 || Ci == 64)) return false;
+  if ((skip_kind == FNO_SKIP_IDENTITY || skip_kind == FNO_SKIP_SOFT_GATING) && Ci != Co)
+    return false;
+  if (m1 < 1 || m1 > H || m2h < 1 || m2h > W / 2 + 1) return false;
+  if (2 * m2h > W + 8) return false;  // mirror staging fits the line's LDS rows
+  return epi_lds_bytes(W, Co, Ci, skip_kind) <= kMaxLds && inv_lds_bytes(H, m2h) <= kMaxLds;
+}
+
+// The fused path is taken when the epilogue kernel covers the shape; the
+// forward window transform is K1 when it covers the plane and the generic
+// direct-DFT kernels otherwise.
 bool fast2d_supported(int B, int Ci, int Co, int ndim, const int32_t* sizes, const int32_t* modes,
                       int skip_kind) {
   if (ndim != 2 || B < 1) return false;
   const int H = sizes[0], W = sizes[1];
-  if (!(H == 64 || H == 128 || H == 256)) return false;
-  if (!(W == 128 || W == 256)) return false;
-  if (!(Co == 32 || Co == 64 || Co == 96 || Co == 128)) return false;
-  if (skip_kind == FNO_SKIP_LINEAR && (Ci % 2 != 0 || Ci < 2)) return false;
-  if ((skip_kind == FNO_SKIP_IDENTITY || skip_kind == FNO_SKIP_SOFT_GATING) && Ci != Co)
-    return false;
-  if (modes[0] < 1 || modes[0] > H || modes[1] < 1 || modes[1] > W / 2 + 1) return false;
-  if (fwd_lds_bytes(H, W, modes[1]) > kMaxLds) return false;
-  if (inv_lds_bytes(H, modes[1]) > kMaxLds) return false;
-  if (epi_lds_bytes(W, Co, Ci, skip_kind) > kMaxLds) return false;
-  return true;
+  return epi_supported(H, W, Ci, Co, modes[0], modes[1], skip_kind);
 }
 
 size_t fast2d_workspace(int B, int Ci, int Co, const int32_t* sizes, const int32_t* modes) {
   const int64_t M = (int64_t)modes[0] * modes[1];
-  const int64_t e = (int64_t)B * Ci * M + (int64_t)B * Co * M + (int64_t)B * Co * sizes[0] * modes[1];
-  return (size_t)e * sizeof(float2);
+  size_t e = (size_t)((int64_t)B * Ci * M + (int64_t)B * Co * M +
+                      (int64_t)B * sizes[0] * Co * modes[1]) * sizeof(float2);
+  if (!fwd_supported(sizes[0], sizes[1], modes[0], modes[1]))
+    e += rfft_window_ws((int64_t)B * Ci, 2, sizes, modes);
+  return e;
 }
 
-// Kernels taking more than 64 KB of dynamic LDS get the limit raised once.
+// Kernels taking more than 64 KB of dynamic LDS get the limit raised.
 template <typename K>
 static int allow_lds(K kernel, size_t bytes) {
   if (bytes <= 64 * 1024) return FNO_OK;
@@ -364,48 +634,32 @@ static int allow_lds(K kernel, size_t bytes) {
                     "hipFuncSetAttribute(MaxDynamicSharedMemorySize)");
 }
 
-template <int H, int W>
+template <int H, int W, int KPR>
 static int launch_fwd(const float* x, float2* xhat, int64_t planes, int m1, int m2h, float scale,
                       hipStream_t st) {
-  constexpr int BLOCK = (H >= 256 || W >= 256) ? 512 : 256;
-  const int TS = m2h | 1;
+  constexpr int BLOCK = 16 * (W >= 256 ? 16 : 8);
   const size_t lds = fwd_lds_bytes(H, W, m2h);
-  int rc = allow_lds(k_fwd_plane<H, W, BLOCK>, lds);
+  int rc = allow_lds(k_fwd_stream<H, W, KPR>, lds);
   if (rc) return rc;
-  hipLaunchKernelGGL((k_fwd_plane<H, W, BLOCK>), dim3((unsigned)planes), dim3(BLOCK), lds, st, x,
-                     xhat, m1, m2h, TS, scale);
-  return launch_status("k_fwd_plane");
+  hipLaunchKernelGGL((k_fwd_stream<H, W, KPR>), dim3((unsigned)planes), dim3(BLOCK), lds, st, x,
+                     xhat, m1, m2h, scale);
+  return launch_status("k_fwd_stream");
 }
 
-template <int H>
-static int launch_inv(const float2* yhat, float2* zbuf, int64_t planes, int m1, int m2h,
-                      hipStream_t st) {
-  constexpr int BLOCK = (H >= 256) ? 512 : 256;
-  const int TS = m2h | 1;
-  const size_t lds = inv_lds_bytes(H, m2h);
-  int rc = allow_lds(k_inv_cols<H, BLOCK>, lds);
-  if (rc) return rc;
-  hipLaunchKernelGGL((k_inv_cols<H, BLOCK>), dim3((unsigned)planes), dim3(BLOCK), lds, st, yhat,
-                     zbuf, m1, m2h, TS);
-  return launch_status("k_inv_cols");
-}
-
-template <int W, int CO>
-static int launch_epi(const float* x, const float2* zbuf, const float* skip_w, const float* bias,
-                      float* y, int B, int H, int Ci, int m2h, int skip_kind, int act,
-                      float inv_scale, hipStream_t st) {
-  const size_t lds = epi_lds_bytes(W, CO, Ci, skip_kind);
-  int rc = allow_lds(k_row_epilogue<W, CO>, lds);
-  if (rc) return rc;
-  hipLaunchKernelGGL((k_row_epilogue<W, CO>), dim3((unsigned)(B * H)), dim3(256), lds, st, x, zbuf,
-                     skip_w, bias, y, H, Ci, m2h, skip_kind, act, inv_scale);
-  return launch_status("k_row_epilogue");
+template <int H, int W>
+static int launch_fwd_k(const float* x, float2* xhat, int64_t planes, int m1, int m2h, float scale,
+                        hipStream_t st) {
+  switch (fwd_kpr(m1)) {
+    case 1: return launch_fwd<H, W, 1>(x, xhat, planes, m1, m2h, scale, st);
+    case 2: return launch_fwd<H, W, 2>(x, xhat, planes, m1, m2h, scale, st);
+    default: return launch_fwd<H, W, 4>(x, xhat, planes, m1, m2h, scale, st);
+  }
 }
 
 static int dispatch_fwd(int H, int W, const float* x, float2* xhat, int64_t planes, int m1, int m2h,
                         float scale, hipStream_t st) {
 #define FNO_FWD(h, w) \
-  if (H == h && W == w) return launch_fwd<h, w>(x, xhat, planes, m1, m2h, scale, st);
+  if (H == h && W == w) return launch_fwd_k<h, w>(x, xhat, planes, m1, m2h, scale, st);
   FNO_FWD(64, 128) FNO_FWD(128, 128) FNO_FWD(256, 128)
   FNO_FWD(64, 256) FNO_FWD(128, 256) FNO_FWD(256, 256)
 #undef FNO_FWD
@@ -413,26 +667,72 @@ static int dispatch_fwd(int H, int W, const float* x, float2* xhat, int64_t plan
   return FNO_ERR_UNSUPPORTED;
 }
 
-static int dispatch_inv(int H, const float2* yhat, float2* zbuf, int64_t planes, int m1, int m2h,
+template <int H>
+static int launch_inv(const float2* yhat, float2* zbuf, int B, int Co, int m1, int m2h,
+                      hipStream_t st) {
+  constexpr int BLOCK = (H >= 256) ? 512 : 256;
+  const size_t lds = inv_lds_bytes(H, m2h);
+  int rc = allow_lds(k_inv_cols<H, BLOCK>, lds);
+  if (rc) return rc;
+  hipLaunchKernelGGL((k_inv_cols<H, BLOCK>), dim3((unsigned)(B * Co)), dim3(BLOCK), lds, st, yhat,
+                     zbuf, Co, m1, m2h);
+  return launch_status("k_inv_cols");
+}
+
+static int dispatch_inv(int H, const float2* yhat, float2* zbuf, int B, int Co, int m1, int m2h,
                         hipStream_t st) {
-  if (H == 64) return launch_inv<64>(yhat, zbuf, planes, m1, m2h, st);
-  if (H == 128) return launch_inv<128>(yhat, zbuf, planes, m1, m2h, st);
-  if (H == 256) return launch_inv<256>(yhat, zbuf, planes, m1, m2h, st);
+  if (H == 64) return launch_inv<64>(yhat, zbuf, B, Co, m1, m2h, st);
+  if (H == 128) return launch_inv<128>(yhat, zbuf, B, Co, m1, m2h, st);
+  if (H == 256) return launch_inv<256>(yhat, zbuf, B, Co, m1, m2h, st);
   set_error("fused 2D inverse: unsupported H=%d", H);
   return FNO_ERR_UNSUPPORTED;
 }
 
-static int dispatch_epi(int W, int Co, const float* x, const float2* zbuf, const float* skip_w,
-                        const float* bias, float* y, int B, int H, int Ci, int m2h, int skip_kind,
-                        int act, float inv_scale, hipStream_t st) {
-#define FNO_EPI(w, co)                                                                        \
-  if (W == w && Co == co)                                                                     \
-    return launch_epi<w, co>(x, zbuf, skip_w, bias, y, B, H, Ci, m2h, skip_kind, act, inv_scale, \
-                             st);
-  FNO_EPI(128, 32) FNO_EPI(128, 64) FNO_EPI(128, 96) FNO_EPI(128, 128)
-  FNO_EPI(256, 32) FNO_EPI(256, 64) FNO_EPI(256, 96) FNO_EPI(256, 128)
+template <int H, int W, int CO, int CI, int NB>
+static int launch_epi(const float* x, const float2* z, const float* skip_w, const float* bias,
+                      float* y, int B, int m2h, int skip_kind, int act, float inv_scale,
+                      hipStream_t st) {
+  constexpr int BLOCK = CO / 2 * (W >= 256 ? 16 : 8);
+  const size_t lds = epi_lds_bytes(W, CO, CI, skip_kind);
+  int rc = allow_lds(k_row_epilogue<H, W, CO, CI, NB>, lds);
+  if (rc) return rc;
+  const int TR = epi_rows_per_block(H);
+  const int64_t grid = (int64_t)B * (H / TR);
+  hipLaunchKernelGGL((k_row_epilogue<H, W, CO, CI, NB>), dim3((unsigned)grid), dim3(BLOCK), lds,
+                     st, x, z, skip_w, bias, y, TR, m2h, skip_kind, act, inv_scale);
+  return launch_status("k_row_epilogue");
+}
+
+template <int W, int CO, int CI>
+static int launch_epi_h(const float* x, const float2* z, const float* skip_w, const float* bias,
+                        float* y, int B, int H, int m2h, int skip_kind, int act, float inv_scale,
+                        hipStream_t st) {
+  const bool few = epi_bins(W, m2h) <= 3;
+#define FNO_EPI_H(h)                                                                          \
+  if (H == h)                                                                                 \
+    return few ? launch_epi<h, W, CO, CI, 3>(x, z, skip_w, bias, y, B, m2h, skip_kind, act,   \
+                                             inv_scale, st)                                   \
+               : launch_epi<h, W, CO, CI, 9>(x, z, skip_w, bias, y, B, m2h, skip_kind, act,   \
+                                             inv_scale, st);
+  FNO_EPI_H(64) FNO_EPI_H(128) FNO_EPI_H(256)
+#undef FNO_EPI_H
+  set_error("fused 2D epilogue: unsupported H=%d", H);
+  return FNO_ERR_UNSUPPORTED;
+}
+
+static int dispatch_epi(int W, int Co, int Ci, const float* x, const float2* z,
+                        const float* skip_w, const float* bias, float* y, int B, int H, int m2h,
+                        int skip_kind, int act, float inv_scale, hipStream_t st) {
+  // the x operand width only matters for the linear skip
+  const int ci = (skip_kind == FNO_SKIP_LINEAR) ? Ci : Co;
+#define FNO_EPI(w, co, cin)                                                                     \
+  if (W == w && Co == co && ci == cin)                                                          \
+    return launch_epi_h<w, co, cin>(x, z, skip_w, bias, y, B, H, m2h, skip_kind, act, inv_scale, \
+                                    st);
+  FNO_EPI(128, 32, 32) FNO_EPI(128, 32, 64) FNO_EPI(128, 64, 32) FNO_EPI(128, 64, 64)
+  FNO_EPI(256, 32, 32) FNO_EPI(256, 32, 64) FNO_EPI(256, 64, 32) FNO_EPI(256, 64, 64)
 #undef FNO_EPI
-  set_error("fused 2D epilogue: unsupported W=%d Co=%d", W, Co);
+  set_error("fused 2D epilogue: unsupported W=%d Co=%d Ci=%d", W, Co, Ci);
   return FNO_ERR_UNSUPPORTED;
 }
 
@@ -452,13 +752,21 @@ int fast2d_block(const float* x, const float2* w, const float* bias, const float
   const int32_t sz[2] = {H, W};
   const float fscale = (float)forward_scale(norm, sz, 2);
   const float iscale = (float)inverse_scale(norm, sz, 2);
-  int rc = dispatch_fwd(H, W, x, xhat, (int64_t)B * Ci, m1, m2h, fscale, st);
+  int rc;
+  if (fwd_supported(H, W, m1, m2h)) {
+    rc = dispatch_fwd(H, W, x, xhat, (int64_t)B * Ci, m1, m2h, fscale, st);
+  } else {
+    // the generic forward's scratch goes where Z lives later
+    void* rest = zbuf;
+    rc = rfft_window(x, xhat, (int64_t)B * Ci, 2, sizes, modes, norm, rest,
+                     ws_bytes - (size_t)((int64_t)B * (Ci + Co) * M) * sizeof(float2), st);
+  }
   if (rc) return rc;
   rc = contract_dense(xhat, w, yhat, B, Ci, Co, M, (int64_t)Co * M, M, 1, st);
   if (rc) return rc;
-  rc = dispatch_inv(H, yhat, zbuf, (int64_t)B * Co, m1, m2h, st);
+  rc = dispatch_inv(H, yhat, zbuf, B, Co, m1, m2h, st);
   if (rc) return rc;
-  return dispatch_epi(W, Co, x, zbuf, skip_w, bias, y, B, H, Ci, m2h, skip_kind, act, iscale, st);
+  return dispatch_epi(W, Co, Ci, x, zbuf, skip_w, bias, y, B, H, m2h, skip_kind, act, iscale, st);
 }
 
 }  // namespace fno

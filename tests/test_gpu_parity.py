@@ -311,3 +311,22 @@ def test_errors_raise(cuda_device):
     with pytest.raises(NotImplementedError):
         x = torch.randn(1, 3, 8, 8, device=cuda_device, requires_grad=True)
         conv(x).sum().backward()
+
+
+def test_kernel_gelu_matches_exact_erf(cuda_device):
+    """The kernels' erf GELU (Abramowitz & Stegun 7.1.28 form) against exact
+    erf GELU in float64 over [-12, 12], through the C-ABI epilogue with no
+    skip.  The approximation's erf error is <= 3e-7 absolute, so: absolute
+    error <= 2e-6 everywhere (a float32 emulation of the formula gives 7e-7)
+    and relative <= 1e-5 where |GELU| >= 0.1 (emulation: 3e-6); in the far
+    negative tail only the absolute bound is meaningful."""
+    v = torch.linspace(-12.0, 12.0, 1 << 20, dtype=torch.float32)
+    spec = v.reshape(1, 1, -1).to(cuda_device)
+    y = Fh.block_epilogue(spec.clone(), None, nat.SKIP_NONE, None, nat.ACT_GELU)
+    torch.cuda.synchronize()
+    vd = v.double()
+    ref = 0.5 * vd * (1.0 + torch.erf(vd / 2 ** 0.5))
+    err = (y.double().cpu().reshape(-1) - ref).abs()
+    assert err.max().item() <= 2e-6
+    big = ref.abs() >= 0.1
+    assert (err[big] / ref.abs()[big]).max().item() <= 1e-5
