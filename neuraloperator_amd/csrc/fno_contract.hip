@@ -1,0 +1,178 @@
+// Mode-wise complex contraction on fp32 MFMA (v_mfma_f32_32x32x2f32):
+//
+//   Y[b, o, k] = sum_i X[b, i, k] W[i, o, k]      X [B][Ci][M], W [Ci][Co][M], Y [B][Co][M]
+//
+// (spectral_convolution.py:21-46, _contract_dense: einsum 'bixy,ioxy->boxy').
+// Per mode k this is the real GEMM
+//
+//   [Yr; Yi] (2Co x B) = A (2Co x 2Ci) * Bm (2Ci x B)
+//   A[o][2i]    =  Wr[i][o]     A[o][2i+1]    = -Wi[i][o]
+//   A[Co+o][2i] =  Wi[i][o]     A[Co+o][2i+1] =  Wr[i][o]
+//   Bm[2i][b]   =  Xr[b][i]     Bm[2i+1][b]   =  Xi[b][i]
+//
+// A workgroup owns KB = 16 consecutive modes (a 128-byte run of every X and W
+// row in their reference layouts), 32 batch entries and one half of the
+// output channels; wave w owns mode k0 + w, i.e. two 32x32 tiles (the Yr and
+// Yi rows of its 32 channels).  Input channels stream through LDS in chunks
+// of IC, transposed on the way in so each MFMA operand read is a run of
+// consecutive words, with the next chunk loaded into registers meanwhile.
+// The two channel halves of a mode block are placed on one XCD, next to each
+// other, so the second read of the block's X rows hits that XCD's L2.
+#include "fno_common.h"
+
+namespace fno {
+
+typedef float v16f_c __attribute__((ext_vector_type(16)));
+
+namespace {
+constexpr int KB = 16;            // modes per workgroup (one per wave)
+constexpr int IC = 8;             // input channels per LDS chunk
+constexpr int OH = 32;            // output channels per workgroup
+constexpr int PS = OH;            // plane stride of a W tile row (re, im planes)
+constexpr int MS = 2 * PS + 4;    // (i, mode) block stride of the W tile
+constexpr int XM = 64 + 4;        // (i, mode) block stride of the X tile: [c][b]
+constexpr int THREADS = 64 * KB;
+constexpr int WF4 = IC * OH * KB / 2 / THREADS;   // W float4 per thread per chunk
+constexpr int XF4 = IC * 32 * KB / 2 / THREADS;   // X float4 per thread per chunk
+}  // namespace
+
+__global__ void __launch_bounds__(THREADS)
+k_contract_mfma(const float2* __restrict__ X, const float2* __restrict__ W, float2* __restrict__ Y,
+                int B, int Ci, int Co, int64_t M, int nblocks) {
+  __shared__ float smem[IC * KB * MS + IC * KB * XM];
+  float* Ws = smem;                   // W chunk [i][mode][re/im plane][o]
+  float* Xs = smem + IC * KB * MS;    // X chunk [i][mode][re/im][b]
+  // pair (mode block, channel half) placement: the halves of block p run on
+  // one XCD (workgroup id mod 8), 8 ids apart
+  const int bid = blockIdx.x;
+  const int p = (bid / 16) * 8 + (bid % 8);
+  const int half = (bid / 8) % 2;
+  if (p >= nblocks) return;
+  const int64_t k0 = (int64_t)p * KB;
+  const int o0 = half * OH;
+  const int b0 = blockIdx.y * 32;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const float4* X4 = reinterpret_cast<const float4*>(X);
+  const float4* W4 = reinterpret_cast<const float4*>(W);
+
+  // float4 q of a chunk: part = q & 7 (modes 2*part, 2*part+1), row = q >> 3.
+  // W rows: o = row % OH fastest, then the chunk's input channel.
+  // X rows: b = row % 32 fastest, then the chunk's input channel.
+  float4 wr[WF4], xr[XF4];
+  auto load = [&](int i0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < WF4; ++j) {
+      const int q = tid + THREADS * j, part = q & 7, row = q >> 3;
+      const int o = o0 + row % OH, i = i0 + row / OH;
+      const int64_t k = k0 + 2 * part;
+      wr[j] = (k < M && o < Co)
+                  ? W4[(((int64_t)i * Co + o) * M + k) >> 1]
+                  : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int j = 0; j < XF4; ++j) {
+      const int q = tid + THREADS * j, part = q & 7, row = q >> 3;
+      const int b = b0 + (row & 31), i = i0 + (row >> 5);
+      const int64_t k = k0 + 2 * part;
+      xr[j] = (k < M && b < B) ? X4[(((int64_t)b * Ci + i) * M + k) >> 1]
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  auto stash = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < WF4; ++j) {
+      const int q = tid + THREADS * j, part = q & 7, row = q >> 3;
+      const int o = row % OH, ii = row / OH, m = 2 * part;
+      float* d = Ws + (ii * KB + m) * MS + o;
+      d[0] = wr[j].x;
+      d[PS] = wr[j].y;
+      d[MS] = wr[j].z;
+      d[MS + PS] = wr[j].w;
+    }
+#pragma unroll
+    for (int j = 0; j < XF4; ++j) {
+      const int q = tid + THREADS * j, part = q & 7, row = q >> 3;
+      const int b = row & 31, ii = row >> 5, m = 2 * part;
+      float* d = Xs + (ii * KB + m) * XM + b;
+      d[0] = xr[j].x;
+      d[32] = xr[j].y;
+      d[XM] = xr[j].z;
+      d[XM + 32] = xr[j].w;
+    }
+  };
+
+  v16f_c acc[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
+  const int c = lane >> 5, oo = lane & 31;
+  const float sgn = c ? -1.f : 1.f;   // A[o][2i+1] = -Wi
+
+  load(0);
+#pragma unroll 1
+  for (int i0 = 0; i0 < Ci; i0 += IC) {
+    __syncthreads();   // the previous chunk's operand reads are done
+    stash();
+    if (i0 + IC < Ci) load(i0 + IC);
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < IC; ++s) {
+      const float bv = Xs[(s * KB + w) * XM + c * 32 + oo];
+      const float* wrow = Ws + (s * KB + w) * MS + oo;
+      const float ar = sgn * wrow[c * PS];        // Yr rows: Wr (c=0), -Wi (c=1)
+      const float ai = wrow[(1 - c) * PS];        // Yi rows: Wi (c=0),  Wr (c=1)
+      acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(ar, bv, acc[0], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(ai, bv, acc[1], 0, 0, 0);
+    }
+  }
+  // D[m][n]: lane l, register r holds row 8(r/4) + 4(l/32) + r%4 (channel),
+  // column l%32 (batch entry).  Y rows [b][o][k0 .. k0+16) are 128-byte runs:
+  // transpose through LDS, 16 batch entries at a time, and store whole runs.
+  constexpr int YB = 32 * KB * 2 + 8;   // LDS stride of one batch entry: [o][mode][re/im]
+  static_assert(16 * YB <= IC * KB * (MS + XM), "transpose tile fits the chunk buffers");
+  const int64_t kw = k0 + w;
+#pragma unroll 1
+  for (int hb = 0; hb < 2; ++hb) {
+    __syncthreads();
+    if ((oo >> 4) == hb) {
+      float* d = smem + (oo & 15) * YB + w * 2;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) d[(8 * (r >> 2) + 4 * c + (r & 3)) * KB * 2 + t] = acc[t][r];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 16 * 32 * KB * 2 / 4 / THREADS; ++j) {
+      const int q = tid + THREADS * j, part = q & 7, row = q >> 3;
+      const int bl = row >> 5, o = row & 31;
+      const int b = b0 + 16 * hb + bl;
+      const int64_t k = k0 + 2 * part;
+      const float4 v = *reinterpret_cast<const float4*>(smem + bl * YB + o * KB * 2 + part * 4);
+      if (b < B && o0 + o < Co && k < M)
+        reinterpret_cast<float4*>(Y)[(((int64_t)b * Co + o0 + o) * M + k) >> 1] = v;
+    }
+  }
+  (void)kw;
+}
+
+// Host: covers the reference layouts (W [Ci][Co][M]) with Ci a multiple of
+// IC, at most two channel halves and an even mode count (16-byte aligned
+// float4 rows).
+bool contract_mfma_supported(int B, int Ci, int Co, int64_t M, int64_t sWi, int64_t sWo,
+                             int64_t sWk) {
+  return B >= 1 && Ci % IC == 0 && Co >= 1 && Co <= 2 * OH && M % 2 == 0 && sWk == 1 &&
+         sWo == M && sWi == (int64_t)Co * M;
+}
+
+int contract_mfma(const float2* X, const float2* W, float2* Y, int B, int Ci, int Co, int64_t M,
+                  hipStream_t st) {
+  const int nblocks = (int)((M + KB - 1) / KB);
+  const int pairs16 = (nblocks + 7) / 8;              // groups of 8 blocks
+  dim3 grid((unsigned)(pairs16 * 16), (unsigned)((B + 31) / 32));
+  hipLaunchKernelGGL(k_contract_mfma, grid, dim3(THREADS), 0, st, X, W, Y, B, Ci, Co, M, nblocks);
+  return launch_status("k_contract_mfma");
+}
+
+}  // namespace fno

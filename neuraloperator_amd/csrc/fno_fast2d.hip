@@ -543,6 +543,218 @@ k_row_epilogue(const float* __restrict__ x, const float2* __restrict__ z,
   step(TR, I0(), BF(), BT());   // TR even: row TR-1 sits in buffer 1
 }
 
+// ----------------------------------------------------------------------- K4R
+// Register-resident row epilogue for W = 256 (16-lane line FFTs).
+// MFMA 16x16x4 f32 operand/result layout (wave64):
+//   A (16 x 4):  lane l supplies A[l % 16][l / 16]
+//   B (4 x 16):  lane l supplies B[l / 16][l % 16]
+//   D (16 x 16): lane l, register r holds D[4*(l/16) + r][l % 16]
+// M = the wave's 16 output channels, N = 16 pixels of a tile, K = 4 input
+// channels.  Group G = l/16 of wave w runs the inverse row FFTs of channels
+// 16w+4G .. 16w+4G+3 (two lines, two channels packed per line); lane
+// t = l % 16 ends holding pixels t + 16u (u < 16), which is D of tile u.  So
+// the accumulators start as spec * scale + bias straight from the FFT
+// registers, the skip MFMAs add W_s x on top, and GELU + store read them
+// back: the spectral term never goes through LDS.  The x operand streams
+// through a double-buffered LDS ring of 16-channel chunks (loaded a row ahead
+// into registers), so a workgroup needs ~36 KB of LDS and two share a CU.
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+template <int CO, int CI, int NB>
+__global__ void __launch_bounds__(CO * 4) __attribute__((amdgpu_waves_per_eu(2, 2)))
+k_row_epilogue_r(const float* __restrict__ x, const float2* __restrict__ z,
+                 const float* __restrict__ skip_w, const float* __restrict__ bias,
+                 float* __restrict__ y, int H, int TR, int m2h, int skip_kind, int act,
+                 float inv_scale) {
+  constexpr int W = 256, T = 16, R = 16, Q = 1;
+  constexpr int NWAVE = CO / 16, BLOCK = 64 * NWAVE;
+  constexpr int KC = 16;                 // input channels per LDS chunk
+  constexpr int NCH = CI / KC;           // chunks per row
+  constexpr int XS = W + 16;             // LDS row stride of a chunk (floats)
+  constexpr int KS = CI / 4;             // MFMA k-steps per row
+  constexpr int LPT = KC * W / 4 / BLOCK;  // float4 loads per thread per chunk
+  constexpr int EXS = W + 8;             // exchange slice per group (float2)
+  static_assert(CO % 16 == 0 && CI % KC == 0 && LPT >= 1 && KC * W / 4 % BLOCK == 0, "shape");
+  extern __shared__ float4 smem4[];
+  float2* twW = reinterpret_cast<float2*>(smem4);
+  float* region = reinterpret_cast<float*>(twW + W);   // exchange slices / x ring
+
+  const int RB = H / TR;
+  const int b = blockIdx.x / RB, h0 = (blockIdx.x % RB) * TR;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int G = lane >> 4, t = lane & 15;
+  const uint32_t HW = (uint32_t)H * W;
+  const bool linear = (skip_kind == FNO_SKIP_LINEAR);
+  const bool gated = (skip_kind == FNO_SKIP_SOFT_GATING || skip_kind == FNO_SKIP_IDENTITY);
+  const bool gelu_on = (act == FNO_ACT_GELU);
+  const int o0 = 16 * wave + 4 * G;    // first of the lane's 4 output channels
+  const float* xs = x + (size_t)b * CI * HW;
+  const float2* zs = z + (size_t)b * H * CO * m2h;
+  float* ys = y + (size_t)b * CO * HW;
+  const uint32_t xbytes = CI * HW * 4u, ybytes = CO * HW * 4u;
+  const uint32_t zbytes = (uint32_t)H * CO * m2h * 8u;
+
+  fill_twiddles<W>(twW);
+  float aW[KS];
+  if (linear) {
+#pragma unroll
+    for (int k = 0; k < KS; ++k) aW[k] = skip_w[(16 * wave + (lane & 15)) * CI + 4 * k + (lane >> 4)];
+  }
+  float bch[4], gch[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    bch[r] = bias ? bias[o0 + r] : 0.f;
+    gch[r] = (skip_kind == FNO_SKIP_SOFT_GATING) ? skip_w[o0 + r] : 1.f;
+  }
+
+  float4 xst[2][LPT];
+  float2 za[2][NB], zc[2][NB];   // bins k = t + 16n of the two lines' channel pairs
+  v4f acc[R];
+
+  // x chunk c of row h into staging buffer sb: float4 q = tid + BLOCK*j is
+  // channel (q / 64) of the chunk, pixels 4*(q % 64) .. +3
+  auto load_chunk = [&](int h, int c, float4 (&dst)[LPT]) __attribute__((always_inline)) {
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(xs, xbytes);
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) {
+      const int q = tid + BLOCK * j;
+      const uint32_t off = ((uint32_t)(c * KC + (q >> 6)) * HW + (uint32_t)h * W + 4 * (q & 63)) * 4u;
+      dst[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0));
+    }
+  };
+  auto store_chunk = [&](int buf, const float4 (&src)[LPT]) __attribute__((always_inline)) {
+    float* ring = region + buf * KC * XS;
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) {
+      const int q = tid + BLOCK * j;
+      *reinterpret_cast<float4*>(ring + (q >> 6) * XS + 4 * (q & 63)) = src[j];
+    }
+  };
+  auto load_z = [&](int h) __attribute__((always_inline)) {
+    const __amdgpu_buffer_rsrc_t rz = make_rsrc(zs, zbytes);
+#pragma unroll
+    for (int L = 0; L < 2; ++L) {
+      const uint32_t zo = (((uint32_t)h * CO + o0 + 2 * L) * m2h + t) * 8u;
+#pragma unroll
+      for (int n = 0; n < NB; ++n) {
+        const bool in = t + T * n < m2h;
+        const float2 a = __builtin_bit_cast(
+            float2, __builtin_amdgcn_raw_buffer_load_b64(rz, (int)(zo + 8u * T * n), 0, 0));
+        const float2 c = __builtin_bit_cast(
+            float2, __builtin_amdgcn_raw_buffer_load_b64(rz, (int)(zo + 8u * (T * n + m2h)), 0, 0));
+        za[L][n] = in ? a : make_float2(0.f, 0.f);
+        zc[L][n] = in ? c : make_float2(0.f, 0.f);
+      }
+    }
+  };
+
+  // first row's operands
+  if (linear) {
+    load_chunk(h0, 0, xst[0]);
+    if (NCH > 1) load_chunk(h0, 1, xst[1]);
+  }
+  load_z(h0);
+  __syncthreads();
+
+#pragma unroll 1
+  for (int s = 0; s < TR; ++s) {
+    const int h = h0 + s;
+    // ---- inverse row FFTs: line L packs channels o0+2L (re) and o0+2L+1 (im)
+    {
+      float2* ex = reinterpret_cast<float2*>(region) + (4 * wave + G) * EXS;
+#pragma unroll
+      for (int L = 0; L < 2; ++L) {
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+          const int k = t + T * u;
+          if (k < m2h) {
+            ex[2 * k] = za[L][u];
+            ex[2 * k + 1] = zc[L][u];
+          }
+        }
+        wave_sync();
+        float2 v[R];
+#pragma unroll
+        for (int u = 0; u < R; ++u) {
+          const int k = t + T * u;
+          float2 val = make_float2(0.f, 0.f);
+          if (u < NB && k < m2h) {
+            float2 a = za[L][u < NB ? u : 0], c = zc[L][u < NB ? u : 0];
+            if (k == 0 || 2 * k == W) {  // Hermitian fix-up of the irfft input
+              a.y = 0.f;
+              c.y = 0.f;
+            }
+            val = make_float2(a.x - c.y, a.y + c.x);           // Za + i Zb
+          } else if (k > W / 2 && W - k < m2h) {
+            const float2 a = ex[2 * (W - k)], c = ex[2 * (W - k) + 1];
+            val = make_float2(a.x + c.y, c.x - a.y);           // conj Za + i conj Zb
+          }
+          v[u] = val;
+        }
+        wave_sync();
+        float2 out[Q][T];
+        line_fft<W, +1>(v, ex, twW, t, out);
+#pragma unroll
+        for (int u = 0; u < R; ++u) {
+          acc[u][2 * L] = fmaf(out[0][u].x, inv_scale, bch[2 * L]);
+          acc[u][2 * L + 1] = fmaf(out[0][u].y, inv_scale, bch[2 * L + 1]);
+        }
+      }
+    }
+    if (gated) {
+#pragma unroll
+      for (int u = 0; u < R; ++u)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          acc[u][r] += gch[r] * xs[(size_t)(o0 + r) * HW + (size_t)h * W + 16 * u + t];
+    }
+    __syncthreads();   // exchange slices free: the region becomes the x ring
+    if (linear) {
+      store_chunk(0, xst[0]);
+      if (NCH > 2) load_chunk(h, 2, xst[0]);
+      __syncthreads();
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        const float* ring = region + (c & 1) * KC * XS + (lane >> 4) * XS + (lane & 15);
+#pragma unroll
+        for (int kk = 0; kk < KC / 4; ++kk)
+#pragma unroll
+          for (int u = 0; u < R; ++u)
+            acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(aW[c * (KC / 4) + kk],
+                                                          ring[4 * kk * XS + 16 * u], acc[u], 0, 0, 0);
+        if (c + 1 < NCH) {
+          store_chunk((c + 1) & 1, xst[(c + 1) & 1]);
+          if (c + 3 < NCH) load_chunk(h, c + 3, xst[(c + 1) & 1]);
+        }
+        __syncthreads();
+      }
+    }
+    // ---- next row's operands in flight during GELU + store and its FFTs
+    if (s + 1 < TR) {
+      if (linear) {
+        load_chunk(h + 1, 0, xst[0]);
+        if (NCH > 1) load_chunk(h + 1, 1, xst[1]);
+      }
+      load_z(h + 1);
+    }
+    // ---- activation and store: channel o0 + r, pixel 16u + t
+    {
+      const __amdgpu_buffer_rsrc_t ry = make_rsrc(ys, ybytes);
+      const uint32_t yo = ((uint32_t)o0 * HW + (uint32_t)h * W + t) * 4u;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int u = 0; u < R; ++u) {
+          float v = acc[u][r];
+          v = gelu_on ? gelu_erf(v) : v;
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ry,
+                                                (int)(yo + 64u * u),
+                                                __builtin_amdgcn_readfirstlane((int)(r * HW * 4u)), 0);
+        }
+    }
+  }
+}
+
 // ============================================================== host side
 int contract_dense(const float2* X, const float2* W, float2* Y, int B, int Ci, int Co, int64_t M,
                    int64_t sWi, int64_t sWo, int64_t sWk, hipStream_t st);
@@ -594,7 +806,12 @@ static int epi_bins(int W, int m2h) {
 
 static int epi_rows_per_block(int H) { return H >= 64 ? 16 : H; }
 
+static bool epi_r_supported(int H, int W, int Ci, int Co, int m2h, int skip_kind);
+
 static bool epi_supported(int H, int W, int Ci, int Co, int m1, int m2h, int skip_kind) {
+  if (m1 >= 1 && m1 <= H && epi_r_supported(H, W, Ci, Co, m2h, skip_kind) &&
+      inv_lds_bytes(H, m2h) <= kMaxLds)
+    return true;
   if (!(W == 128 || W == 256)) return false;
   if (!(H == 64 || H == 128 || H == 256)) return false;
   if (!(Co == 32 || Co == 64)) return false;
@@ -720,6 +937,56 @@ static int launch_epi_h(const float* x, const float2* z, const float* skip_w, co
   return FNO_ERR_UNSUPPORTED;
 }
 
+// ---- register-resident epilogue (W = 256)
+static size_t epi_r_lds_bytes(int Co) {
+  const size_t ex = (size_t)4 * (Co / 16) * (256 + 8) * 2;   // exchange slices (floats)
+  const size_t ring = (size_t)2 * 16 * (256 + 16);            // x ring (floats)
+  return (2 * 256 + (ex > ring ? ex : ring)) * sizeof(float);
+}
+
+static bool epi_r_supported(int H, int W, int Ci, int Co, int m2h, int skip_kind) {
+  if (W != 256 || H % 16 != 0) return false;
+  if (!(Co == 64 || Co == 128)) return false;
+  const int ci = (skip_kind == FNO_SKIP_LINEAR) ? Ci : Co;
+  if (!(ci == 32 || ci == 64 || ci == 128)) return false;
+  if ((skip_kind == FNO_SKIP_IDENTITY || skip_kind == FNO_SKIP_SOFT_GATING) && Ci != Co)
+    return false;
+  if (m2h < 1 || m2h > 128) return false;   // mirror staging fits a 264-entry slice
+  return epi_r_lds_bytes(Co) <= kMaxLds;
+}
+
+template <int CO, int CI, int NB>
+static int launch_epi_r(const float* x, const float2* z, const float* skip_w, const float* bias,
+                        float* y, int B, int H, int m2h, int skip_kind, int act, float inv_scale,
+                        hipStream_t st) {
+  const size_t lds = epi_r_lds_bytes(CO);
+  int rc = allow_lds(k_row_epilogue_r<CO, CI, NB>, lds);
+  if (rc) return rc;
+  const int TR = 16;
+  const int64_t grid = (int64_t)B * (H / TR);
+  hipLaunchKernelGGL((k_row_epilogue_r<CO, CI, NB>), dim3((unsigned)grid), dim3(CO * 4), lds, st,
+                     x, z, skip_w, bias, y, H, TR, m2h, skip_kind, act, inv_scale);
+  return launch_status("k_row_epilogue_r");
+}
+
+static int dispatch_epi_r(int Co, int Ci, const float* x, const float2* z, const float* skip_w,
+                          const float* bias, float* y, int B, int H, int m2h, int skip_kind,
+                          int act, float inv_scale, hipStream_t st) {
+  const int ci = (skip_kind == FNO_SKIP_LINEAR) ? Ci : Co;
+  const bool few = (m2h + 15) / 16 <= 3;
+#define FNO_EPI_R(co, cin)                                                                   \
+  if (Co == co && ci == cin)                                                                 \
+    return few ? launch_epi_r<co, cin, 3>(x, z, skip_w, bias, y, B, H, m2h, skip_kind, act,  \
+                                          inv_scale, st)                                     \
+               : launch_epi_r<co, cin, 8>(x, z, skip_w, bias, y, B, H, m2h, skip_kind, act,  \
+                                          inv_scale, st);
+  FNO_EPI_R(64, 32) FNO_EPI_R(64, 64) FNO_EPI_R(64, 128)
+  FNO_EPI_R(128, 32) FNO_EPI_R(128, 64) FNO_EPI_R(128, 128)
+#undef FNO_EPI_R
+  set_error("fused 2D epilogue: unsupported Co=%d Ci=%d", Co, Ci);
+  return FNO_ERR_UNSUPPORTED;
+}
+
 static int dispatch_epi(int W, int Co, int Ci, const float* x, const float2* z,
                         const float* skip_w, const float* bias, float* y, int B, int H, int m2h,
                         int skip_kind, int act, float inv_scale, hipStream_t st) {
@@ -766,6 +1033,8 @@ int fast2d_block(const float* x, const float2* w, const float* bias, const float
   if (rc) return rc;
   rc = dispatch_inv(H, yhat, zbuf, B, Co, m1, m2h, st);
   if (rc) return rc;
+  if (epi_r_supported(H, W, Ci, Co, m2h, skip_kind))
+    return dispatch_epi_r(Co, Ci, x, zbuf, skip_w, bias, y, B, H, m2h, skip_kind, act, iscale, st);
   return dispatch_epi(W, Co, Ci, x, zbuf, skip_w, bias, y, B, H, m2h, skip_kind, act, iscale, st);
 }
 

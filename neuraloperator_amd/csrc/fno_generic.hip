@@ -453,8 +453,15 @@ int irfft_window(const float2* yhat, const float* bias, float* y, int64_t batch,
   return FNO_OK;
 }
 
+bool contract_mfma_supported(int B, int Ci, int Co, int64_t M, int64_t sWi, int64_t sWo,
+                             int64_t sWk);
+int contract_mfma(const float2* X, const float2* W, float2* Y, int B, int Ci, int Co, int64_t M,
+                  hipStream_t st);
+
 int contract_dense(const float2* X, const float2* W, float2* Y, int B, int Ci, int Co, int64_t M,
                    int64_t sWi, int64_t sWo, int64_t sWk, hipStream_t st) {
+  if (contract_mfma_supported(B, Ci, Co, M, sWi, sWo, sWk))
+    return contract_mfma(X, W, Y, B, Ci, Co, M, st);
   constexpr int TB = 4, TO = 8;
   const int nTiles = ((B + TB - 1) / TB) * ((Co + TO - 1) / TO);
   const int wavesPerBlock = kThreads / 64;
