@@ -40,12 +40,66 @@ namespace fno {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
 
+// exp(+2 pi i k / 256), k < 256, evaluated at compile time in double
+// precision (octant reduction + Taylor series to x^23, error << 1e-16) and
+// rounded once to float, so every twiddle is within half an ulp.
+namespace twd {
+constexpr double kPi = 3.14159265358979323846264338327950288;
+constexpr double sin_series(double x) {  // |x| <= pi/4
+  double x2 = x * x, term = x, sum = x;
+  for (int n = 1; n < 12; ++n) {
+    term *= -x2 / ((2.0 * n) * (2.0 * n + 1.0));
+    sum += term;
+  }
+  return sum;
+}
+constexpr double cos_series(double x) {
+  double x2 = x * x, term = 1.0, sum = 1.0;
+  for (int n = 1; n < 12; ++n) {
+    term *= -x2 / ((2.0 * n - 1.0) * (2.0 * n));
+    sum += term;
+  }
+  return sum;
+}
+struct Table256 {
+  float re[256], im[256];
+};
+constexpr Table256 make_table() {
+  Table256 t{};
+  for (int k = 0; k < 256; ++k) {
+    const int q = k / 64, m = k % 64;   // quadrant, position in it
+    double c = 0, sn = 0;
+    if (m <= 32) {
+      c = cos_series(2.0 * kPi * m / 256.0);
+      sn = sin_series(2.0 * kPi * m / 256.0);
+    } else {
+      c = sin_series(2.0 * kPi * (64 - m) / 256.0);
+      sn = cos_series(2.0 * kPi * (64 - m) / 256.0);
+    }
+    double cr = c, sr = sn;
+    if (q == 1) { cr = -sn; sr = c; }
+    else if (q == 2) { cr = -c; sr = -sn; }
+    else if (q == 3) { cr = sn; sr = -c; }
+    t.re[k] = (float)cr;
+    t.im[k] = (float)sr;
+  }
+  return t;
+}
+}  // namespace twd
+__constant__ const twd::Table256 kTw256 = twd::make_table();
+
+// LDS table of exp(+2 pi i t / N), t < N, for N dividing 256
 template <int N>
 __device__ __forceinline__ void fill_twiddles(float2* tw) {
-  for (int i = threadIdx.x; i < N; i += blockDim.x) tw[i] = twiddle_pos(i, N);
+  static_assert(256 % N == 0, "N must divide 256");
+  for (int i = threadIdx.x; i < N; i += blockDim.x)
+    tw[i] = make_float2(kTw256.re[i * (256 / N)], kTw256.im[i * (256 / N)]);
 }
 
 // ------------------------------------------------------------------------ K1
+// Row stride (float2) of K1's chunk spectrum: >= m2h and = 8 (mod 32).
+__host__ __device__ constexpr int fwd_row_stride(int m2h) { return (m2h + 23) / 32 * 32 + 8; }
+
 // Kept window of a plane: rows kh in [kmin, kmin + m1), kmin = -(m1/2), stored
 // at window row kh - kmin; columns kw < m2h.  A kept row kh is reached from its
 // residue k' = kh mod 32 as kh = k0(k') + 32 e, k0 = kmin + ((k' - kmin) & 31).
@@ -60,9 +114,12 @@ k_fwd_stream(const float* __restrict__ x, float2* __restrict__ xhat, int m1, int
   extern __shared__ float4 smem4[];
   float2* twW = reinterpret_cast<float2*>(smem4);  // w_W^t, t < W
   float2* twH = twW + W;                             // w_H^t, t < H
-  float2* exall = twH + H;                           // 16 lines x W
-  float2* S = exall + 16 * W;                        // [32][SP] chunk spectrum
-  const int SP = m2h | 1;
+  constexpr int EXS = W + 16;                        // padded exchange slice
+  float2* exall = twH + H;                           // 16 lines x EXS
+  float2* S = exall + 16 * EXS;                      // [32][SP] chunk spectrum
+  // row stride of S: SP = 8 (mod 32) float2 puts the 4 rows a half-wave reads
+  // in the column stage 16 banks apart (conflict-free)
+  const int SP = fwd_row_stride(m2h);
   fill_twiddles<W>(twW);
   fill_twiddles<H>(twH);
 
@@ -82,18 +139,26 @@ k_fwd_stream(const float* __restrict__ x, float2* __restrict__ xhat, int m1, int
 #pragma unroll
       for (int e = 0; e < KPR; ++e) acc[a][b][e] = make_float2(0.f, 0.f);
 
-  // rows of line L in chunk c: h = c + D*(2L), c + D*(2L+1)
-  // x is addressed as a uniform plane base plus 32-bit lane offsets, so the
-  // compiler keeps one offset register per row instead of 64-bit pointers
-  float va[R], vb[R];
-  {
-    const uint32_t oa = (uint32_t)(D * (2 * L)) * W + t;
+  // rows of line L in chunk c: h = c + D*(2L), c + D*(2L+1).  Each lane
+  // loads 4 float4 of each row (16 lanes x 16 B = 256 contiguous bytes per
+  // load instruction) one chunk ahead; at the chunk they are staged in the
+  // line's own LDS exchange slice and read back in the FFT's stride-T layout.
+  constexpr int NF4 = W / (4 * T);   // float4 per lane and row
+  static_assert(NF4 * 4 * T == W, "row split");
+  const __amdgpu_buffer_rsrc_t rxp = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(xp), (short)0, H * W * 4, 0x00020000);
+  auto load_rows = [&](uint32_t row, int lt, float4 (&dst)[2 * NF4]) __attribute__((always_inline)) {
+    const uint32_t off = (row * W + 4 * lt) * 4u;
 #pragma unroll
-    for (int s = 0; s < R; ++s) {
-      va[s] = xp[oa + T * s];
-      vb[s] = xp[oa + D * W + T * s];
+    for (int k = 0; k < NF4; ++k) {
+      dst[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              rxp, (int)(off + 16u * T * k), 0, 0));
+      dst[NF4 + k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                    rxp, (int)(off + 16u * T * k), D * W * 4, 0));
     }
-  }
+  };
+  float4 xs4[2 * NF4];
+  load_rows((uint32_t)(D * (2 * L)), t, xs4);
   __syncthreads();
 
 #pragma unroll 1
@@ -104,19 +169,22 @@ k_fwd_stream(const float* __restrict__ x, float2* __restrict__ xhat, int m1, int
     asm volatile("" : "+v"(tl));
     const int Ll = tl / T, tt = tl % T;
     float2 v[R];
+    {
+      float* exf = reinterpret_cast<float*>(exall + Ll * EXS);   // rows a | b
 #pragma unroll
-    for (int s = 0; s < R; ++s) v[s] = make_float2(va[s], vb[s]);
-    if (c + 1 < D) {  // next chunk's rows in flight during this chunk
-      const uint32_t oa = (uint32_t)(c + 1 + D * (2 * Ll)) * W + tt;
-#pragma unroll
-      for (int s = 0; s < R; ++s) {
-        va[s] = xp[oa + T * s];
-        vb[s] = xp[oa + D * W + T * s];
+      for (int k = 0; k < NF4; ++k) {
+        reinterpret_cast<float4*>(exf)[tt + T * k] = xs4[k];
+        reinterpret_cast<float4*>(exf + W)[tt + T * k] = xs4[NF4 + k];
       }
+      if (c + 1 < D)  // next chunk's rows in flight during this chunk
+        load_rows((uint32_t)(c + 1 + D * (2 * Ll)), tt, xs4);
+      wave_sync();
+#pragma unroll
+      for (int s = 0; s < R; ++s) v[s] = make_float2(exf[tt + T * s], exf[W + tt + T * s]);
     }
     // ---- row pair FFT, keep bins k < m2h and their mirrors
     {
-      float2* exl = exall + Ll * W;
+      float2* exl = exall + Ll * EXS;
       float2 out[Q][T];
       line_fft<W, -1>(v, exl, twW, tt, out);
 #pragma unroll
@@ -145,15 +213,19 @@ k_fwd_stream(const float* __restrict__ x, float2* __restrict__ xhat, int m1, int
       dft8<-1>(f);
 #pragma unroll
       for (int k1 = 1; k1 < 8; ++k1) f[k1] = cmulc(f[k1], twH[((j * k1) & 31) * D]);
-      wave_sync();
+      // exchange among the column's 4 lanes through the (idle) row-exchange
+      // slices, slot (col, j, k1) at (col/8)*284 + col%8 + 8j + 36k1: both the
+      // writes (fixed k1) and the reads (fixed jj, k1 = 2j+e2) of a half-wave
+      // hit 32 distinct float2 bank pairs
+      float2* xc = exall + (col >> 3) * 284 + (col & 7);
 #pragma unroll
-      for (int k1 = 0; k1 < 8; ++k1) S[(j * 8 + k1) * SP + col] = f[k1];
+      for (int k1 = 0; k1 < 8; ++k1) xc[8 * j + 36 * k1] = f[k1];
       wave_sync();
 #pragma unroll
       for (int e2 = 0; e2 < 2; ++e2) {
         const int k1 = 2 * j + e2;
-        float2 g0 = S[(0 * 8 + k1) * SP + col], g1 = S[(1 * 8 + k1) * SP + col];
-        float2 g2 = S[(2 * 8 + k1) * SP + col], g3 = S[(3 * 8 + k1) * SP + col];
+        float2 g0 = xc[0 + 36 * k1], g1 = xc[8 + 36 * k1];
+        float2 g2 = xc[16 + 36 * k1], g3 = xc[24 + 36 * k1];
         dft4<-1>(g0, g1, g2, g3);
         const float2 P[4] = {g0, g1, g2, g3};
 #pragma unroll
@@ -767,8 +839,8 @@ static constexpr size_t kMaxLds = 160 * 1024;
 static int line_lanes(int n) { return n >= 256 ? 16 : 8; }
 
 static size_t fwd_lds_bytes(int H, int W, int m2h) {
-  const int SP = m2h | 1;
-  return (size_t)(W + H + 16 * W + 32 * SP) * sizeof(float2);
+  const int SP = fwd_row_stride(m2h);
+  return (size_t)(W + H + 16 * (W + 16) + 32 * SP) * sizeof(float2);
 }
 
 static int fwd_kpr(int m1) { return m1 <= 32 ? 1 : (m1 <= 64 ? 2 : 4); }
