@@ -65,6 +65,13 @@ __device__ __forceinline__ float gelu_erf(float v) {
   return v >= 0.f ? v - h : h;
 }
 
+// Raw buffer resource over [base, base + bytes): loads past the end return
+// zero, and offsets are 32-bit, so address arithmetic stays in 32-bit VGPRs.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
 // ------------------------------------------------------------------ host side
 void set_error(const char* fmt, ...);
 int hip_status(hipError_t e, const char* what);

@@ -12,8 +12,10 @@
 //
 // A workgroup owns KB = 16 consecutive modes (a 128-byte run of every X and W
 // row in their reference layouts), 32 batch entries and one half of the
-// output channels; wave w owns mode k0 + w, i.e. two 32x32 tiles (the Yr and
-// Yi rows of its 32 channels).  Input channels stream through LDS in chunks
+// output channels; wave w owns modes k0 + 2w and k0 + 2w + 1, i.e. four 32x32
+// tiles (the Yr and Yi rows of its 32 channels for both modes).  Eight waves
+// and <= 128 VGPRs per workgroup let two workgroups share a CU, so the 2 x 132
+// workgroups of a 64x33-mode layer run in one wave of the grid.  Input channels stream through LDS in chunks
 // of IC, transposed on the way in so each MFMA operand read is a run of
 // consecutive words, with the next chunk loaded into registers meanwhile.
 // The two channel halves of a mode block are placed on one XCD, next to each
@@ -25,18 +27,19 @@ namespace fno {
 typedef float v16f_c __attribute__((ext_vector_type(16)));
 
 namespace {
-constexpr int KB = 16;            // modes per workgroup (one per wave)
+constexpr int KB = 16;            // modes per workgroup (two per wave)
+constexpr int MPW = 2;            // modes per wave
 constexpr int IC = 8;             // input channels per LDS chunk
 constexpr int OH = 32;            // output channels per workgroup
 constexpr int PS = OH;            // plane stride of a W tile row (re, im planes)
 constexpr int MS = 2 * PS + 4;    // (i, mode) block stride of the W tile
 constexpr int XM = 64 + 4;        // (i, mode) block stride of the X tile: [c][b]
-constexpr int THREADS = 64 * KB;
+constexpr int THREADS = 64 * KB / MPW;
 constexpr int WF4 = IC * OH * KB / 2 / THREADS;   // W float4 per thread per chunk
 constexpr int XF4 = IC * 32 * KB / 2 / THREADS;   // X float4 per thread per chunk
 }  // namespace
 
-__global__ void __launch_bounds__(THREADS)
+__global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(4, 4)))
 k_contract_mfma(const float2* __restrict__ X, const float2* __restrict__ W, float2* __restrict__ Y,
                 int B, int Ci, int Co, int64_t M, int nblocks) {
   __shared__ float smem[IC * KB * MS + IC * KB * XM];
@@ -52,30 +55,39 @@ k_contract_mfma(const float2* __restrict__ X, const float2* __restrict__ W, floa
   const int o0 = half * OH;
   const int b0 = blockIdx.y * 32;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const float4* X4 = reinterpret_cast<const float4*>(X);
-  const float4* W4 = reinterpret_cast<const float4*>(W);
+  const uint32_t xbytes = (uint32_t)((int64_t)B * Ci * M * 8);
+  const uint32_t wbytes = (uint32_t)((int64_t)Ci * Co * M * 8);
+  const int Mi = (int)M;
 
   // float4 q of a chunk: part = q & 7 (modes 2*part, 2*part+1), row = q >> 3.
   // W rows: o = row % OH fastest, then the chunk's input channel.
   // X rows: b = row % 32 fastest, then the chunk's input channel.
   float4 wr[WF4], xr[XF4];
+  // Entries outside the operands (mode >= M, channel >= Co, batch >= B) get
+  // an offset past the buffer end, which the buffer load returns as zero: no
+  // select on the loaded value, so every load of a chunk stays in flight.
+  constexpr uint32_t kOut = 0x80000000u;
   auto load = [&](int i0) __attribute__((always_inline)) {
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(W, wbytes), rx = make_rsrc(X, xbytes);
 #pragma unroll
     for (int j = 0; j < WF4; ++j) {
       const int q = tid + THREADS * j, part = q & 7, row = q >> 3;
       const int o = o0 + row % OH, i = i0 + row / OH;
-      const int64_t k = k0 + 2 * part;
-      wr[j] = (k < M && o < Co)
-                  ? W4[(((int64_t)i * Co + o) * M + k) >> 1]
-                  : make_float4(0.f, 0.f, 0.f, 0.f);
+      const int k = (int)k0 + 2 * part;
+      const uint32_t off = (k < Mi && o < Co)
+                               ? ((uint32_t)(i * Co + o) * (uint32_t)Mi + (uint32_t)k) * 8u
+                               : kOut;
+      wr[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)off, 0, 0));
     }
 #pragma unroll
     for (int j = 0; j < XF4; ++j) {
       const int q = tid + THREADS * j, part = q & 7, row = q >> 3;
       const int b = b0 + (row & 31), i = i0 + (row >> 5);
-      const int64_t k = k0 + 2 * part;
-      xr[j] = (k < M && b < B) ? X4[(((int64_t)b * Ci + i) * M + k) >> 1]
-                               : make_float4(0.f, 0.f, 0.f, 0.f);
+      const int k = (int)k0 + 2 * part;
+      const uint32_t off = (k < Mi && b < B)
+                               ? ((uint32_t)(b * Ci + i) * (uint32_t)Mi + (uint32_t)k) * 8u
+                               : kOut;
+      xr[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0));
     }
   };
   auto stash = [&]() __attribute__((always_inline)) {
@@ -101,11 +113,13 @@ k_contract_mfma(const float2* __restrict__ X, const float2* __restrict__ W, floa
     }
   };
 
-  v16f_c acc[2];
+  v16f_c acc[MPW][2];
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+  for (int mm = 0; mm < MPW; ++mm)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[mm][t][r] = 0.f;
   const int c = lane >> 5, oo = lane & 31;
   const float sgn = c ? -1.f : 1.f;   // A[o][2i+1] = -Wi
 
@@ -117,30 +131,36 @@ k_contract_mfma(const float2* __restrict__ X, const float2* __restrict__ W, floa
     if (i0 + IC < Ci) load(i0 + IC);
     __syncthreads();
 #pragma unroll
-    for (int s = 0; s < IC; ++s) {
-      const float bv = Xs[(s * KB + w) * XM + c * 32 + oo];
-      const float* wrow = Ws + (s * KB + w) * MS + oo;
-      const float ar = sgn * wrow[c * PS];        // Yr rows: Wr (c=0), -Wi (c=1)
-      const float ai = wrow[(1 - c) * PS];        // Yi rows: Wi (c=0),  Wr (c=1)
-      acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(ar, bv, acc[0], 0, 0, 0);
-      acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(ai, bv, acc[1], 0, 0, 0);
-    }
+    for (int s = 0; s < IC; ++s)
+#pragma unroll
+      for (int mm = 0; mm < MPW; ++mm) {
+        const int m = MPW * w + mm;
+        const float bv = Xs[(s * KB + m) * XM + c * 32 + oo];
+        const float* wrow = Ws + (s * KB + m) * MS + oo;
+        const float ar = sgn * wrow[c * PS];        // Yr rows: Wr (c=0), -Wi (c=1)
+        const float ai = wrow[(1 - c) * PS];        // Yi rows: Wi (c=0),  Wr (c=1)
+        acc[mm][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(ar, bv, acc[mm][0], 0, 0, 0);
+        acc[mm][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(ai, bv, acc[mm][1], 0, 0, 0);
+      }
   }
   // D[m][n]: lane l, register r holds row 8(r/4) + 4(l/32) + r%4 (channel),
   // column l%32 (batch entry).  Y rows [b][o][k0 .. k0+16) are 128-byte runs:
   // transpose through LDS, 16 batch entries at a time, and store whole runs.
   constexpr int YB = 32 * KB * 2 + 8;   // LDS stride of one batch entry: [o][mode][re/im]
   static_assert(16 * YB <= IC * KB * (MS + XM), "transpose tile fits the chunk buffers");
-  const int64_t kw = k0 + w;
 #pragma unroll 1
   for (int hb = 0; hb < 2; ++hb) {
     __syncthreads();
     if ((oo >> 4) == hb) {
-      float* d = smem + (oo & 15) * YB + w * 2;
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int mm = 0; mm < MPW; ++mm) {
+        float* d = smem + (oo & 15) * YB + (MPW * w + mm) * 2;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) d[(8 * (r >> 2) + 4 * c + (r & 3)) * KB * 2 + t] = acc[t][r];
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            d[(8 * (r >> 2) + 4 * c + (r & 3)) * KB * 2 + t] = acc[mm][t][r];
+      }
     }
     __syncthreads();
 #pragma unroll
@@ -154,16 +174,17 @@ k_contract_mfma(const float2* __restrict__ X, const float2* __restrict__ W, floa
         reinterpret_cast<float4*>(Y)[(((int64_t)b * Co + o0 + o) * M + k) >> 1] = v;
     }
   }
-  (void)kw;
 }
 
 // Host: covers the reference layouts (W [Ci][Co][M]) with Ci a multiple of
-// IC, at most two channel halves and an even mode count (16-byte aligned
-// float4 rows).
+// IC, at most two channel halves, an even mode count (16-byte aligned float4
+// rows) and operands under 2 GiB.
 bool contract_mfma_supported(int B, int Ci, int Co, int64_t M, int64_t sWi, int64_t sWo,
                              int64_t sWk) {
+  // 32-bit buffer offsets: both operands under 2 GiB
   return B >= 1 && Ci % IC == 0 && Co >= 1 && Co <= 2 * OH && M % 2 == 0 && sWk == 1 &&
-         sWo == M && sWi == (int64_t)Co * M;
+         sWo == M && sWi == (int64_t)Co * M && (int64_t)B * Ci * M * 8 < (int64_t(1) << 31) &&
+         (int64_t)Ci * Co * M * 8 < (int64_t(1) << 31);
 }
 
 int contract_mfma(const float2* X, const float2* W, float2* Y, int B, int Ci, int Co, int64_t M,

@@ -12,22 +12,23 @@
 //                          every frequency mod 32;
 //                        * the twiddle w_H^(-kh c) folds it into register
 //                          accumulators of the m1 kept rows.
-//                      x is read once with the next chunk's rows in flight;
-//                      LDS holds one chunk, so 3 workgroups share a CU.
-// K2  contraction      fno_generic.hip (mode-wise complex GEMM).
-// K3  k_epilogue_fold  one workgroup per (b, r), TH output rows h = r + s*H/TH:
-//                        * the inverse column transform of those TH rows is
-//                          folded from the m1 window rows of every output
-//                          channel (m1/TH complex MACs per value + a TH-point
-//                          DFT), straight from the contraction output -- no
-//                          column-transformed intermediate goes through HBM;
-//                        * per row: inverse row real FFTs of all output
-//                          channels (two channels per complex line) into LDS,
-//                          the 1x1-conv skip on fp32 MFMA
-//                          (v_mfma_f32_32x32x2f32, x operand prefetched one row
-//                          ahead), bias and erf GELU, one coalesced write of y.
-//                      Workgroups of one sample are placed on one XCD so the
-//                      sample's spectrum stays in that XCD's L2.
+//                      x is read once, 16-byte loads, the next chunk's rows in
+//                      flight; 39 KB of LDS and <= 128 VGPRs let 4 workgroups
+//                      share a CU.
+// K2  contraction      fno_contract.hip (mode-wise complex GEMM on fp32 MFMA).
+// K3  k_inv_cols       one workgroup per (b, o) plane: inverse FFT along H of
+//                      the m2h kept columns (zero-padded window rows), written
+//                      row-major as Z[b][h][o][kw].
+// K4  k_row_epilogue_r one workgroup per (b, TR consecutive rows); per row:
+//                        * inverse row real FFTs of all output channels (two
+//                          channels per complex line) straight into the
+//                          accumulators of the skip GEMM (v_mfma_f32_16x16x4f32
+//                          output layout = line FFT output layout);
+//                        * the 1x1-conv skip on fp32 MFMA, x streamed through
+//                          an LDS ring with the next row's loads in flight;
+//                        * bias, gated skip add and erf GELU in registers, one
+//                          write of y.
+//                      (k_row_epilogue: the LDS-staged variant for W = 128.)
 //
 // Semantics follow SpectralConv.forward (neuralop/layers/spectral_convolution.py
 // :429-568) with output size == input size, and the post-activation block of
@@ -103,23 +104,35 @@ __host__ __device__ constexpr int fwd_row_stride(int m2h) { return (m2h + 23) / 
 // Kept window of a plane: rows kh in [kmin, kmin + m1), kmin = -(m1/2), stored
 // at window row kh - kmin; columns kw < m2h.  A kept row kh is reached from its
 // residue k' = kh mod 32 as kh = k0(k') + 32 e, k0 = kmin + ((k' - kmin) & 31).
+//
+// LDS: twW [W] | twH [H] | 16 line slices of EXS float2.  The 4 (W = 256) or
+// 8 (W = 128) slices of one wavefront form its region; the chunk spectrum rows
+// of the wavefront's lines (2 per line, stride SP) sit at the end of that
+// region, so a wavefront writes them without waiting for the others.  The
+// column stage exchanges its partial DFTs through the spectrum entries it has
+// just read.
 template <int H, int W, int KPR>
 __global__ void __launch_bounds__(16 * LinePlan<W>::T)
 k_fwd_stream(const float* __restrict__ x, float2* __restrict__ xhat, int m1, int m2h, float scale) {
   using PW = LinePlan<W>;
   constexpr int T = PW::T, R = PW::R, Q = PW::Q;
-  constexpr int BLOCK = 16 * T;
   constexpr int D = H / 32;
   static_assert(H % 32 == 0 && D >= 1, "H must be a multiple of 32");
+  constexpr int EXS = W + 16;                 // padded line slice (float2)
+  constexpr int LPW = 64 / T;                 // lines per wavefront
+  constexpr int WREG = LPW * EXS;             // wavefront region (float2)
+  constexpr int NS = 4;                       // m2h <= 4T: split passes per lane
   extern __shared__ float4 smem4[];
   float2* twW = reinterpret_cast<float2*>(smem4);  // w_W^t, t < W
   float2* twH = twW + W;                             // w_H^t, t < H
-  constexpr int EXS = W + 16;                        // padded exchange slice
-  float2* exall = twH + H;                           // 16 lines x EXS
-  float2* S = exall + 16 * EXS;                      // [32][SP] chunk spectrum
-  // row stride of S: SP = 8 (mod 32) float2 puts the 4 rows a half-wave reads
-  // in the column stage 16 banks apart (conflict-free)
+  float2* exall = twH + H;
+  // spectrum row r = 2 * line + (0 | 1): SP = 8 (mod 32) float2 puts the 4
+  // rows a half-wave reads in the column stage 16 banks apart
   const int SP = fwd_row_stride(m2h);
+  const int sbase = WREG - 2 * LPW * SP;
+  auto srow = [&](int r) __attribute__((always_inline)) {
+    return exall + (r / (2 * LPW)) * WREG + sbase + (r % (2 * LPW)) * SP;
+  };
   fill_twiddles<W>(twW);
   fill_twiddles<H>(twH);
 
@@ -142,7 +155,7 @@ k_fwd_stream(const float* __restrict__ x, float2* __restrict__ xhat, int m1, int
   // rows of line L in chunk c: h = c + D*(2L), c + D*(2L+1).  Each lane
   // loads 4 float4 of each row (16 lanes x 16 B = 256 contiguous bytes per
   // load instruction) one chunk ahead; at the chunk they are staged in the
-  // line's own LDS exchange slice and read back in the FFT's stride-T layout.
+  // line's own LDS slice and read back in the FFT's stride-T layout.
   constexpr int NF4 = W / (4 * T);   // float4 per lane and row
   static_assert(NF4 * 4 * T == W, "row split");
   const __amdgpu_buffer_rsrc_t rxp = __builtin_amdgcn_make_buffer_rsrc(
@@ -157,50 +170,70 @@ k_fwd_stream(const float* __restrict__ x, float2* __restrict__ xhat, int m1, int
                                                     rxp, (int)(off + 16u * T * k), D * W * 4, 0));
     }
   };
+  // Chunk order: workgroups that share an XCD (ids 8 apart) start at
+  // different residues, which spreads the concurrent row reads (D rows apart
+  // within a chunk) over the HBM channels: ~4.5 -> ~5.8 TB/s for this pattern.
+  const int rot = (int)(blockIdx.x >> 3) & (D - 1);
   float4 xs4[2 * NF4];
-  load_rows((uint32_t)(D * (2 * L)), t, xs4);
+  load_rows((uint32_t)(rot + D * (2 * L)), t, xs4);
   __syncthreads();
 
 #pragma unroll 1
-  for (int c = 0; c < D; ++c) {
+  for (int cs = 0; cs < D; ++cs) {
+    const int c = (cs + rot) & (D - 1);
     // thread index laundered through an empty asm so per-lane addresses are
     // recomputed in the loop rather than hoisted into live registers
     int tl = tid;
     asm volatile("" : "+v"(tl));
     const int Ll = tl / T, tt = tl % T;
+    float2* exl = exall + Ll * EXS;
     float2 v[R];
     {
-      float* exf = reinterpret_cast<float*>(exall + Ll * EXS);   // rows a | b
+      float* exf = reinterpret_cast<float*>(exl);   // rows a | b
 #pragma unroll
       for (int k = 0; k < NF4; ++k) {
         reinterpret_cast<float4*>(exf)[tt + T * k] = xs4[k];
         reinterpret_cast<float4*>(exf + W)[tt + T * k] = xs4[NF4 + k];
       }
-      if (c + 1 < D)  // next chunk's rows in flight during this chunk
-        load_rows((uint32_t)(c + 1 + D * (2 * Ll)), tt, xs4);
+      if (cs + 1 < D)  // next chunk's rows in flight during this chunk
+        load_rows((uint32_t)(((c + 1) & (D - 1)) + D * (2 * Ll)), tt, xs4);
       wave_sync();
 #pragma unroll
       for (int s = 0; s < R; ++s) v[s] = make_float2(exf[tt + T * s], exf[W + tt + T * s]);
     }
-    // ---- row pair FFT, keep bins k < m2h and their mirrors
+    // ---- row pair FFT; bins k < 4T and k > W - 4T (a superset of the kept
+    // k < m2h and their mirrors) go back to the slice
     {
-      float2* exl = exall + Ll * EXS;
       float2 out[Q][T];
       line_fft<W, -1>(v, exl, twW, tt, out);
 #pragma unroll
       for (int q = 0; q < Q; ++q)
 #pragma unroll
         for (int s = 0; s < T; ++s) {
-          const int k = tt + T * q + R * s;
-          if (k < m2h || k > W - m2h) exl[k] = out[q][s];
+          if (T * q + R * s < 4 * T || T * q + R * s + T - 1 > W - 4 * T)
+            exl[tt + T * q + R * s] = out[q][s];
         }
       wave_sync();
       // X_a[k] = (Z[k] + conj Z[W-k]) / 2,  X_b[k] = -i (Z[k] - conj Z[W-k]) / 2
-      for (int k = tt; k < m2h; k += T) {
+      float2 xa[NS], xb[NS];
+#pragma unroll
+      for (int i = 0; i < NS; ++i) {
+        const int k = tt + T * i;
         const float2 zk = exl[k];
         const float2 zn = exl[(W - k) & (W - 1)];
-        S[(2 * Ll) * SP + k] = make_float2(0.5f * (zk.x + zn.x), 0.5f * (zk.y - zn.y));
-        S[(2 * Ll + 1) * SP + k] = make_float2(0.5f * (zk.y + zn.y), 0.5f * (zn.x - zk.x));
+        xa[i] = make_float2(0.5f * (zk.x + zn.x), 0.5f * (zk.y - zn.y));
+        xb[i] = make_float2(0.5f * (zk.y + zn.y), 0.5f * (zn.x - zk.x));
+      }
+      wave_sync();
+      float2* sa = srow(2 * Ll);
+      float2* sb = srow(2 * Ll + 1);
+#pragma unroll
+      for (int i = 0; i < NS; ++i) {
+        const int k = tt + T * i;
+        if (k < m2h) {
+          sa[k] = xa[i];
+          sb[k] = xb[i];
+        }
       }
     }
     __syncthreads();
@@ -209,34 +242,37 @@ k_fwd_stream(const float* __restrict__ x, float2* __restrict__ xhat, int m1, int
       const int col = tl >> 2, j = tl & 3;
       float2 f[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) f[u] = S[(j + 4 * u) * SP + col];
+      for (int u = 0; u < 8; ++u) f[u] = srow(j + 4 * u)[col];
       dft8<-1>(f);
 #pragma unroll
       for (int k1 = 1; k1 < 8; ++k1) f[k1] = cmulc(f[k1], twH[((j * k1) & 31) * D]);
-      // exchange among the column's 4 lanes through the (idle) row-exchange
-      // slices, slot (col, j, k1) at (col/8)*284 + col%8 + 8j + 36k1: both the
-      // writes (fixed k1) and the reads (fixed jj, k1 = 2j+e2) of a half-wave
-      // hit 32 distinct float2 bank pairs
-      float2* xc = exall + (col >> 3) * 284 + (col & 7);
+      // exchange among the column's 4 lanes through the column's own 32
+      // spectrum entries (all read above): slot (lane jj, k1) is row
+      // ((jj + k1/2) & 3) + 4 k1, so both the writes (fixed k1) and the reads
+      // (fixed jj, k1 = 2j + e2) of a half-wave touch 4 distinct rows mod 4
 #pragma unroll
-      for (int k1 = 0; k1 < 8; ++k1) xc[8 * j + 36 * k1] = f[k1];
+      for (int k1 = 0; k1 < 8; ++k1) srow(((j + (k1 >> 1)) & 3) + 4 * k1)[col] = f[k1];
       wave_sync();
+      // w_H^(-kh c) for kh = k0 + 32 e is w_H^(-k0 c) * u^e, u = w_H^(-32 c)
+      const float2 u = twH[(-32 * c) & (H - 1)];
 #pragma unroll
       for (int e2 = 0; e2 < 2; ++e2) {
         const int k1 = 2 * j + e2;
-        float2 g0 = xc[0 + 36 * k1], g1 = xc[8 + 36 * k1];
-        float2 g2 = xc[16 + 36 * k1], g3 = xc[24 + 36 * k1];
+        float2 g0 = srow(((0 + j) & 3) + 4 * k1)[col], g1 = srow(((1 + j) & 3) + 4 * k1)[col];
+        float2 g2 = srow(((2 + j) & 3) + 4 * k1)[col], g3 = srow(((3 + j) & 3) + 4 * k1)[col];
         dft4<-1>(g0, g1, g2, g3);
         const float2 P[4] = {g0, g1, g2, g3};
 #pragma unroll
         for (int k2 = 0; k2 < 4; ++k2) {
           const int kr = k1 + 8 * k2;  // frequency mod 32
           const int k0 = kmin + ((kr - kmin) & 31);
+          // rows kh >= kmin + m1 accumulate too; they are never written
+          float2 q = cmul(P[k2], twH[(-k0 * c) & (H - 1)]);
+          acc[e2][k2][0] = cadd(acc[e2][k2][0], q);
 #pragma unroll
-          for (int e = 0; e < KPR; ++e) {
-            const int kh = k0 + 32 * e;
-            // w_H^(-kh c): the positive-exponent table at (-kh c) mod H
-            if (kh < kmin + m1) cfma(acc[e2][k2][e], P[k2], twH[(-kh * c) & (H - 1)]);
+          for (int e = 1; e < KPR; ++e) {
+            q = cmul(q, u);
+            acc[e2][k2][e] = cadd(acc[e2][k2][e], q);
           }
         }
       }
@@ -334,10 +370,6 @@ __host__ __device__ constexpr int spec_stride() { return W + 8; }
 // Raw buffer resource over [base, base + bytes): loads and stores take a
 // 32-bit VGPR byte offset plus an SGPR byte offset, so per-element address
 // arithmetic stays 32-bit and mostly scalar.  Reads past the end return 0.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
-                                           0x00020000);
-}
 // soff must be wave-uniform; readfirstlane states that to the compiler so it
 // stays in an SGPR.  The b32/b64 builtins move raw bits: values are bit-cast.
 __device__ __forceinline__ float ld_f32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
@@ -839,8 +871,8 @@ static constexpr size_t kMaxLds = 160 * 1024;
 static int line_lanes(int n) { return n >= 256 ? 16 : 8; }
 
 static size_t fwd_lds_bytes(int H, int W, int m2h) {
-  const int SP = fwd_row_stride(m2h);
-  return (size_t)(W + H + 16 * (W + 16) + 32 * SP) * sizeof(float2);
+  (void)m2h;   // the chunk spectrum lives inside the line slices
+  return (size_t)(W + H + 16 * (W + 16)) * sizeof(float2);
 }
 
 static int fwd_kpr(int m1) { return m1 <= 32 ? 1 : (m1 <= 64 ? 2 : 4); }
