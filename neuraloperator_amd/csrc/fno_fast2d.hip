@@ -752,17 +752,22 @@ k_row_epilogue_r(const float* __restrict__ x, const float2* __restrict__ z,
     }
   };
 
+  // Row order: workgroups that share an XCD (ids 8 apart) start at different
+  // rows of their block, so concurrent x reads spread over the HBM channels.
+  const int rot = (int)(blockIdx.x >> 3) % TR;
+  auto row_at = [&](int s) __attribute__((always_inline)) { return h0 + (s + rot) % TR; };
+
   // first row's operands
   if (linear) {
-    load_chunk(h0, 0, xst[0]);
-    if (NCH > 1) load_chunk(h0, 1, xst[1]);
+    load_chunk(row_at(0), 0, xst[0]);
+    if (NCH > 1) load_chunk(row_at(0), 1, xst[1]);
   }
-  load_z(h0);
+  load_z(row_at(0));
   __syncthreads();
 
 #pragma unroll 1
   for (int s = 0; s < TR; ++s) {
-    const int h = h0 + s;
+    const int h = row_at(s);
     // ---- inverse row FFTs: line L packs channels o0+2L (re) and o0+2L+1 (im)
     {
       float2* ex = reinterpret_cast<float2*>(region) + (4 * wave + G) * EXS;
@@ -836,10 +841,10 @@ k_row_epilogue_r(const float* __restrict__ x, const float2* __restrict__ z,
     // ---- next row's operands in flight during GELU + store and its FFTs
     if (s + 1 < TR) {
       if (linear) {
-        load_chunk(h + 1, 0, xst[0]);
-        if (NCH > 1) load_chunk(h + 1, 1, xst[1]);
+        load_chunk(row_at(s + 1), 0, xst[0]);
+        if (NCH > 1) load_chunk(row_at(s + 1), 1, xst[1]);
       }
-      load_z(h + 1);
+      load_z(row_at(s + 1));
     }
     // ---- activation and store: channel o0 + r, pixel 16u + t
     {
