@@ -18,7 +18,7 @@
 // K2  contraction      fno_contract.hip (mode-wise complex GEMM on fp32 MFMA).
 // K3  k_inv_cols       one workgroup per (b, o) plane: inverse FFT along H of
 //                      the m2h kept columns (zero-padded window rows), written
-//                      row-major as Z[b][h][o][kw].
+//                      as one contiguous block Z[b][o][h][kw].
 // K4  k_row_epilogue_r one workgroup per (b, TR consecutive rows); per row:
 //                        * inverse row real FFTs of all output channels (two
 //                          channels per complex line) straight into the
@@ -95,6 +95,19 @@ __device__ __forceinline__ void fill_twiddles(float2* tw) {
   static_assert(256 % N == 0, "N must divide 256");
   for (int i = threadIdx.x; i < N; i += blockDim.x)
     tw[i] = make_float2(kTw256.re[i * (256 / N)], kTw256.im[i * (256 / N)]);
+}
+
+// Activation on/off without a branch: the compiler turns `on ? gelu(v) : v`
+// into a uniform branch around every element's GELU, so the choice is a
+// bit-select (v_bfi_b32) against a mask it cannot see through.
+__device__ __forceinline__ uint32_t act_mask(bool on) {
+  uint32_t m = (uint32_t)__builtin_amdgcn_readfirstlane(on ? -1 : 0);
+  asm volatile("" : "+s"(m));
+  return m;
+}
+__device__ __forceinline__ float act_select(float g, float v, uint32_t m) {
+  return __builtin_bit_cast(float, (__builtin_bit_cast(uint32_t, g) & m) |
+                                       (__builtin_bit_cast(uint32_t, v) & ~m));
 }
 
 // ------------------------------------------------------------------------ K1
@@ -299,28 +312,32 @@ k_fwd_stream(const float* __restrict__ x, float2* __restrict__ xhat, int m1, int
 // ------------------------------------------------------------------------ K3
 // Inverse column transform of one (b, o) plane: the m2h kept columns of the
 // window spectrum, zero-padded to H rows at their frequencies, inverse
-// FFT-ed along H and written row-major as Z[b][h][o][kw] so that K4 reads one
-// contiguous block per output row.
-template <int H, int BLOCK>
-__global__ void __launch_bounds__(BLOCK)
+// FFT-ed along H and written as Z[b][o][h][kw]: one contiguous block per
+// plane, so the stores stream; K4 reads a 8*m2h-byte row per channel.  One group of T lanes per column, all
+// columns in one pass; each group exchanges through its own column of the
+// LDS result tile (odd row stride), so the tile is the only LDS (~70 KB at
+// H = 256, m2h = 33).
+template <int H>
+__global__ void __launch_bounds__(1024)
 k_inv_cols(const float2* __restrict__ yhat, float2* __restrict__ z, int Co, int m1, int m2h) {
   using PH = LinePlan<H>;
   constexpr int T = PH::T, R = PH::R, Q = PH::Q;
-  constexpr int G = BLOCK / T;
   extern __shared__ float4 smem4[];
   float2* twH = reinterpret_cast<float2*>(smem4);
   const int TS = m2h | 1;
   float2* zs = twH + H;          // [H][TS]
-  float2* exall = zs + H * TS;   // G x H
   fill_twiddles<H>(twH);
   const int plane = blockIdx.x;  // b * Co + o
   const int b = plane / Co, o = plane - b * Co;
   const float2* win = yhat + (int64_t)plane * m1 * m2h;   // [m1][m2h] window
+  const int nthreads = blockDim.x;
   __syncthreads();
   {
     const int g = threadIdx.x / T, t = threadIdx.x % T;
-    float2* ex = exall + g * H;
+    const int G = nthreads / T;
     const int pos = m1 - m1 / 2, neg = m1 / 2;
+    // rows outside the window read past the end of the buffer: zero
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(win, (uint32_t)(m1 * m2h * 8));
     for (int kw = g; kw < m2h; kw += G) {
       float2 v[R];
 #pragma unroll
@@ -329,21 +346,41 @@ k_inv_cols(const float2* __restrict__ yhat, float2* __restrict__ z, int Co, int 
         int j = -1;
         if (k < pos) j = k + neg;
         else if (k >= H - neg) j = k - H + neg;
-        v[s] = (j >= 0) ? win[j * m2h + kw] : make_float2(0.f, 0.f);
+        const uint32_t off = j >= 0 ? (uint32_t)(j * m2h + kw) * 8u : 0x80000000u;
+        v[s] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rw, (int)off, 0, 0));
       }
-      float2 out[Q][T];
-      line_fft<H, +1>(v, ex, twH, t, out);
+      // the four-step line FFT of fno_fft_lds.h, exchanging through the
+      // column itself and storing the second pass straight back into it
+      float2* col = zs + kw;
+      dft_small<R, +1>(v);
+#pragma unroll
+      for (int k1 = 1; k1 < R; ++k1) v[k1] = cmul(v[k1], twH[t * k1]);
+      wave_sync();
+#pragma unroll
+      for (int k1 = 0; k1 < R; ++k1) col[(k1 * T + (t ^ (k1 & (T - 1)))) * TS] = v[k1];
+      wave_sync();
+      float2 u[Q][T];
 #pragma unroll
       for (int q = 0; q < Q; ++q)
 #pragma unroll
-        for (int s = 0; s < T; ++s) zs[(t + T * q + R * s) * TS + kw] = out[q][s];
+        for (int s = 0; s < T; ++s) u[q][s] = col[((t + T * q) * T + (s ^ t)) * TS];
+#pragma unroll
+      for (int q = 0; q < Q; ++q) dft_small<T, +1>(u[q]);
+      wave_sync();
+#pragma unroll
+      for (int q = 0; q < Q; ++q)
+#pragma unroll
+        for (int s = 0; s < T; ++s) col[(t + T * q + R * s) * TS] = u[q][s];
     }
   }
   __syncthreads();
-  float2* zp = z + ((int64_t)b * H * Co + o) * m2h;   // + h * Co * m2h
-  for (int i = threadIdx.x; i < H * m2h; i += BLOCK) {
-    const int h = i / m2h, kw = i - h * m2h;
-    zp[(int64_t)h * Co * m2h + kw] = zs[h * TS + kw];
+  // the plane's H x m2h block is contiguous in Z: 16-byte stores of bin pairs
+  float4* zp = reinterpret_cast<float4*>(z + (int64_t)plane * H * m2h);
+  for (int i = threadIdx.x; i < H * m2h / 2; i += nthreads) {
+    const int i0 = 2 * i, h0 = i0 / m2h, k0 = i0 - h0 * m2h;
+    const int i1 = i0 + 1, h1 = i1 / m2h, k1 = i1 - h1 * m2h;
+    const float2 a = zs[h0 * TS + k0], c = zs[h1 * TS + k1];
+    zp[i] = make_float4(a.x, a.y, c.x, c.y);
   }
 }
 
@@ -419,6 +456,7 @@ k_row_epilogue(const float* __restrict__ x, const float2* __restrict__ z,
   const bool linear = (skip_kind == FNO_SKIP_LINEAR);
   const bool gated = (skip_kind == FNO_SKIP_SOFT_GATING || skip_kind == FNO_SKIP_IDENTITY);
   const bool gelu_on = (act == FNO_ACT_GELU);
+  const uint32_t gmask = act_mask(gelu_on);
   const int pxt0 = (CO >= 64) ? (wave % NPX) : 2 * wave;
   const int mt0 = (CO >= 64) ? 2 * (wave / NPX) : 0;
   // per-sample bases (uniform); buffer descriptors are built where used so
@@ -458,17 +496,15 @@ k_row_epilogue(const float* __restrict__ x, const float2* __restrict__ z,
     }
     const __amdgpu_buffer_rsrc_t rz = make_rsrc(zs, zbytes);
     const int tl = tv % T;
-    const uint32_t zo = (((uint32_t)h * CO + 2 * (tv / T)) * m2h + tl) * 8u;
-    const int m2o = __builtin_amdgcn_readfirstlane(m2h * 8);
+    // Z[b][o][h][kw]; bins past m2h read past the buffer end: zero
+    const uint32_t zo = (((uint32_t)(2 * (tv / T)) * H + h) * m2h + tl) * 8u;
+    const int m2o = __builtin_amdgcn_readfirstlane(H * m2h * 8);
 #pragma unroll
     for (int n = 0; n < NB; ++n) {
-      const bool in = tl + T * n < m2h;
-      const float2 a = __builtin_bit_cast(
-          float2, __builtin_amdgcn_raw_buffer_load_b64(rz, (int)(zo + 8u * T * n), 0, 0));
-      const float2 c = __builtin_bit_cast(
-          float2, __builtin_amdgcn_raw_buffer_load_b64(rz, (int)(zo + 8u * T * n), m2o, 0));
-      za[buf][n] = in ? a : make_float2(0.f, 0.f);
-      zc[buf][n] = in ? c : make_float2(0.f, 0.f);
+      const uint32_t off = (tl + T * n < m2h) ? zo + 8u * T * n : 0x80000000u;
+      za[buf][n] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rz, (int)off, 0, 0));
+      zc[buf][n] = __builtin_bit_cast(float2,
+                                      __builtin_amdgcn_raw_buffer_load_b64(rz, (int)off, m2o, 0));
     }
   };
 
@@ -536,7 +572,7 @@ k_row_epilogue(const float* __restrict__ x, const float2* __restrict__ z,
     const int r = e % 16;
     const uint32_t oc = 32 * (mt0 + el_m(e)) + 8 * (r >> 2) + (r & 3);   // o minus the lane part
     float v = accv + specv;
-    v = gelu_on ? gelu_erf(v) : v;   // branch-free: the select keeps one basic block
+    v = act_select(gelu_erf(v), v, gmask);
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), make_rsrc(ys, ybytes),
                                           (int)(yo + 128u * el_n(e)), (int)(oc * HW * 4u), 0);
   };
@@ -691,6 +727,7 @@ k_row_epilogue_r(const float* __restrict__ x, const float2* __restrict__ z,
   const bool linear = (skip_kind == FNO_SKIP_LINEAR);
   const bool gated = (skip_kind == FNO_SKIP_SOFT_GATING || skip_kind == FNO_SKIP_IDENTITY);
   const bool gelu_on = (act == FNO_ACT_GELU);
+  const uint32_t gmask = act_mask(gelu_on);
   const int o0 = 16 * wave + 4 * G;    // first of the lane's 4 output channels
   const float* xs = x + (size_t)b * CI * HW;
   const float2* zs = z + (size_t)b * H * CO * m2h;
@@ -734,20 +771,20 @@ k_row_epilogue_r(const float* __restrict__ x, const float2* __restrict__ z,
       *reinterpret_cast<float4*>(ring + (q >> 6) * XS + 4 * (q & 63)) = src[j];
     }
   };
+  // Z[b][o][h][kw]: bins of channel o0 + 2L (za) and the next channel (zc,
+  // one H x m2h plane further); bins past m2h read past the buffer end: zero
+  const int zplane = __builtin_amdgcn_readfirstlane(H * m2h * 8);
   auto load_z = [&](int h) __attribute__((always_inline)) {
     const __amdgpu_buffer_rsrc_t rz = make_rsrc(zs, zbytes);
 #pragma unroll
     for (int L = 0; L < 2; ++L) {
-      const uint32_t zo = (((uint32_t)h * CO + o0 + 2 * L) * m2h + t) * 8u;
+      const uint32_t zo = (((uint32_t)(o0 + 2 * L) * H + h) * m2h + t) * 8u;
 #pragma unroll
       for (int n = 0; n < NB; ++n) {
-        const bool in = t + T * n < m2h;
-        const float2 a = __builtin_bit_cast(
-            float2, __builtin_amdgcn_raw_buffer_load_b64(rz, (int)(zo + 8u * T * n), 0, 0));
-        const float2 c = __builtin_bit_cast(
-            float2, __builtin_amdgcn_raw_buffer_load_b64(rz, (int)(zo + 8u * (T * n + m2h)), 0, 0));
-        za[L][n] = in ? a : make_float2(0.f, 0.f);
-        zc[L][n] = in ? c : make_float2(0.f, 0.f);
+        const uint32_t off = (t + T * n < m2h) ? zo + 8u * T * n : 0x80000000u;
+        za[L][n] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rz, (int)off, 0, 0));
+        zc[L][n] = __builtin_bit_cast(float2,
+                                      __builtin_amdgcn_raw_buffer_load_b64(rz, (int)off, zplane, 0));
       }
     }
   };
@@ -855,7 +892,7 @@ k_row_epilogue_r(const float* __restrict__ x, const float2* __restrict__ z,
 #pragma unroll
         for (int u = 0; u < R; ++u) {
           float v = acc[u][r];
-          v = gelu_on ? gelu_erf(v) : v;
+          v = act_select(gelu_erf(v), v, gmask);
           __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ry,
                                                 (int)(yo + 64u * u),
                                                 __builtin_amdgcn_readfirstlane((int)(r * HW * 4u)), 0);
@@ -892,11 +929,16 @@ static bool fwd_supported(int H, int W, int m1, int m2h) {
   return fwd_lds_bytes(H, W, m2h) <= kMaxLds;
 }
 
-static int inv_block(int H) { return H >= 256 ? 512 : 256; }
+// one group of line_lanes(H) lanes per kept column, whole waves, <= 1024
+static int inv_block(int H, int m2h) {
+  const int t = line_lanes(H);
+  const int g = m2h < 1024 / t ? m2h : 1024 / t;
+  return (g * t + 63) / 64 * 64;
+}
 
 static size_t inv_lds_bytes(int H, int m2h) {
   const int TS = m2h | 1;
-  return (size_t)(H + H * TS + inv_block(H) / line_lanes(H) * H) * sizeof(float2);
+  return (size_t)(H + H * TS) * sizeof(float2);
 }
 
 static size_t epi_lds_bytes(int W, int Co, int Ci, int skip_kind) {
@@ -996,11 +1038,11 @@ static int dispatch_fwd(int H, int W, const float* x, float2* xhat, int64_t plan
 template <int H>
 static int launch_inv(const float2* yhat, float2* zbuf, int B, int Co, int m1, int m2h,
                       hipStream_t st) {
-  constexpr int BLOCK = (H >= 256) ? 512 : 256;
+  const int block = inv_block(H, m2h);
   const size_t lds = inv_lds_bytes(H, m2h);
-  int rc = allow_lds(k_inv_cols<H, BLOCK>, lds);
+  int rc = allow_lds(k_inv_cols<H>, lds);
   if (rc) return rc;
-  hipLaunchKernelGGL((k_inv_cols<H, BLOCK>), dim3((unsigned)(B * Co)), dim3(BLOCK), lds, st, yhat,
+  hipLaunchKernelGGL((k_inv_cols<H>), dim3((unsigned)(B * Co)), dim3(block), lds, st, yhat,
                      zbuf, Co, m1, m2h);
   return launch_status("k_inv_cols");
 }

@@ -131,11 +131,12 @@ __device__ __forceinline__ void dft_small(float2 (&v)[M]) {
 }
 
 // Line FFT.  tw[i] = exp(+2 pi i i / N) for i < N (LDS table); ex is the
-// group's exchange slice of N float2.  t = lane index within the group.
+// group's exchange slice of N float2 at a stride of exs float2 (1: a
+// contiguous slice).  t = lane index within the group.
 template <int N, int SIGN>
-__device__ __forceinline__ void line_fft(float2 (&v)[LinePlan<N>::R], float2* ex, const float2* tw,
-                                         int t,
-                                         float2 (&out)[LinePlan<N>::Q][LinePlan<N>::T]) {
+__device__ __forceinline__ void line_fft_strided(float2 (&v)[LinePlan<N>::R], float2* ex, int exs,
+                                                 const float2* tw, int t,
+                                                 float2 (&out)[LinePlan<N>::Q][LinePlan<N>::T]) {
   constexpr int T = LinePlan<N>::T, R = LinePlan<N>::R, Q = LinePlan<N>::Q;
   dft_small<R, SIGN>(v);
 #pragma unroll
@@ -145,19 +146,26 @@ __device__ __forceinline__ void line_fft(float2 (&v)[LinePlan<N>::R], float2* ex
   }
   wave_sync();
 #pragma unroll
-  for (int k1 = 0; k1 < R; ++k1) ex[k1 * T + (t ^ (k1 & (T - 1)))] = v[k1];
+  for (int k1 = 0; k1 < R; ++k1) ex[(k1 * T + (t ^ (k1 & (T - 1)))) * exs] = v[k1];
   wave_sync();
 #pragma unroll
   for (int q = 0; q < Q; ++q) {
     const int k1 = t + T * q;
     float2 u[T];
 #pragma unroll
-    for (int s = 0; s < T; ++s) u[s] = ex[k1 * T + (s ^ t)];
+    for (int s = 0; s < T; ++s) u[s] = ex[(k1 * T + (s ^ t)) * exs];
     dft_small<T, SIGN>(u);
 #pragma unroll
     for (int s = 0; s < T; ++s) out[q][s] = u[s];
   }
   wave_sync();
+}
+
+template <int N, int SIGN>
+__device__ __forceinline__ void line_fft(float2 (&v)[LinePlan<N>::R], float2* ex, const float2* tw,
+                                         int t,
+                                         float2 (&out)[LinePlan<N>::Q][LinePlan<N>::T]) {
+  line_fft_strided<N, SIGN>(v, ex, 1, tw, t, out);
 }
 
 }  // namespace fno
