@@ -313,10 +313,10 @@ k_fwd_stream(const float* __restrict__ x, float2* __restrict__ xhat, int m1, int
 // Inverse column transform of one (b, o) plane: the m2h kept columns of the
 // window spectrum, zero-padded to H rows at their frequencies, inverse
 // FFT-ed along H and written as Z[b][o][h][kw]: one contiguous block per
-// plane, so the stores stream; K4 reads a 8*m2h-byte row per channel.  One group of T lanes per column, all
-// columns in one pass; each group exchanges through its own column of the
-// LDS result tile (odd row stride), so the tile is the only LDS (~70 KB at
-// H = 256, m2h = 33).
+// plane, so the stores stream; K4 reads a 8*m2h-byte row per channel.  One
+// group of T lanes per column; each group exchanges through its own column of
+// the LDS result tile (odd row stride), so the tile is the only LDS (~70 KB at
+// H = 256, m2h = 33) and two 512-thread workgroups share a CU.
 template <int H>
 __global__ void __launch_bounds__(1024)
 k_inv_cols(const float2* __restrict__ yhat, float2* __restrict__ z, int Co, int m1, int m2h) {
@@ -929,10 +929,12 @@ static bool fwd_supported(int H, int W, int m1, int m2h) {
   return fwd_lds_bytes(H, W, m2h) <= kMaxLds;
 }
 
-// one group of line_lanes(H) lanes per kept column, whole waves, <= 1024
+// one group of line_lanes(H) lanes per kept column, whole waves, <= 512
+// threads: with the ~70 KB tile two workgroups then share a CU, which pays for
+// an extra pass when more than 512 / T columns are kept
 static int inv_block(int H, int m2h) {
   const int t = line_lanes(H);
-  const int g = m2h < 1024 / t ? m2h : 1024 / t;
+  const int g = m2h < 512 / t ? m2h : 512 / t;
   return (g * t + 63) / 64 * 64;
 }
 
