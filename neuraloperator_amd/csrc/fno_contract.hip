@@ -27,22 +27,34 @@ namespace fno {
 typedef float v16f_c __attribute__((ext_vector_type(16)));
 
 namespace {
-constexpr int KB = 16;            // modes per workgroup (two per wave)
 constexpr int MPW = 2;            // modes per wave
 constexpr int IC = 8;             // input channels per LDS chunk
 constexpr int OH = 32;            // output channels per workgroup
 constexpr int PS = OH;            // plane stride of a W tile row (re, im planes)
 constexpr int MS = 2 * PS + 4;    // (i, mode) block stride of the W tile
 constexpr int XM = 64 + 4;        // (i, mode) block stride of the X tile: [c][b]
-constexpr int THREADS = 64 * KB / MPW;
-constexpr int WF4 = IC * OH * KB / 2 / THREADS;   // W float4 per thread per chunk
-constexpr int XF4 = IC * 32 * KB / 2 / THREADS;   // X float4 per thread per chunk
+constexpr int WF4 = 4;            // W float4 per thread per chunk (IC*OH*KB/2/THREADS)
+constexpr int XF4 = 4;            // X float4 per thread per chunk (IC*32*KB/2/THREADS)
+__host__ __device__ constexpr int contract_threads(int kb) { return 64 * kb / MPW; }
+__host__ __device__ constexpr size_t contract_lds(int kb) {
+  return (size_t)IC * kb * (MS + XM) * sizeof(float);
+}
 }  // namespace
 
-__global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(4, 4)))
+// KB modes per workgroup (KB/2 waves): 16 normally (two workgroups per CU,
+// so <= 128 VGPRs); 18..32 when that keeps the grid within one workgroup per
+// CU, which then needs only two waves per SIMD.
+template <int KB>
+__global__ void __launch_bounds__(contract_threads(KB))
+__attribute__((amdgpu_waves_per_eu(KB == 16 ? 4 : 2, 4)))
 k_contract_mfma(const float2* __restrict__ X, const float2* __restrict__ W, float2* __restrict__ Y,
                 int B, int Ci, int Co, int64_t M, int nblocks) {
-  __shared__ float smem[IC * KB * MS + IC * KB * XM];
+  constexpr int THREADS = contract_threads(KB);
+  constexpr int NP = KB / 2;          // float4 (mode pairs) per operand row
+  static_assert(KB % 2 == 0 && IC * OH * KB / 2 == WF4 * THREADS && IC * 32 * KB / 2 == XF4 * THREADS,
+                "tile split");
+  extern __shared__ float4 smem4[];
+  float* smem = reinterpret_cast<float*>(smem4);
   float* Ws = smem;                   // W chunk [i][mode][re/im plane][o]
   float* Xs = smem + IC * KB * MS;    // X chunk [i][mode][re/im][b]
   // pair (mode block, channel half) placement: the halves of block p run on
@@ -59,7 +71,7 @@ k_contract_mfma(const float2* __restrict__ X, const float2* __restrict__ W, floa
   const uint32_t wbytes = (uint32_t)((int64_t)Ci * Co * M * 8);
   const int Mi = (int)M;
 
-  // float4 q of a chunk: part = q & 7 (modes 2*part, 2*part+1), row = q >> 3.
+  // float4 q of a chunk: part = q % NP (modes 2*part, 2*part+1), row = q / NP.
   // W rows: o = row % OH fastest, then the chunk's input channel.
   // X rows: b = row % 32 fastest, then the chunk's input channel.
   float4 wr[WF4], xr[XF4];
@@ -71,7 +83,7 @@ k_contract_mfma(const float2* __restrict__ X, const float2* __restrict__ W, floa
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(W, wbytes), rx = make_rsrc(X, xbytes);
 #pragma unroll
     for (int j = 0; j < WF4; ++j) {
-      const int q = tid + THREADS * j, part = q & 7, row = q >> 3;
+      const int q = tid + THREADS * j, part = q % NP, row = q / NP;
       const int o = o0 + row % OH, i = i0 + row / OH;
       const int k = (int)k0 + 2 * part;
       const uint32_t off = (k < Mi && o < Co)
@@ -81,7 +93,7 @@ k_contract_mfma(const float2* __restrict__ X, const float2* __restrict__ W, floa
     }
 #pragma unroll
     for (int j = 0; j < XF4; ++j) {
-      const int q = tid + THREADS * j, part = q & 7, row = q >> 3;
+      const int q = tid + THREADS * j, part = q % NP, row = q / NP;
       const int b = b0 + (row & 31), i = i0 + (row >> 5);
       const int k = (int)k0 + 2 * part;
       const uint32_t off = (k < Mi && b < B)
@@ -93,7 +105,7 @@ k_contract_mfma(const float2* __restrict__ X, const float2* __restrict__ W, floa
   auto stash = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < WF4; ++j) {
-      const int q = tid + THREADS * j, part = q & 7, row = q >> 3;
+      const int q = tid + THREADS * j, part = q % NP, row = q / NP;
       const int o = row % OH, ii = row / OH, m = 2 * part;
       float* d = Ws + (ii * KB + m) * MS + o;
       d[0] = wr[j].x;
@@ -103,7 +115,7 @@ k_contract_mfma(const float2* __restrict__ X, const float2* __restrict__ W, floa
     }
 #pragma unroll
     for (int j = 0; j < XF4; ++j) {
-      const int q = tid + THREADS * j, part = q & 7, row = q >> 3;
+      const int q = tid + THREADS * j, part = q % NP, row = q / NP;
       const int b = row & 31, ii = row >> 5, m = 2 * part;
       float* d = Xs + (ii * KB + m) * XM + b;
       d[0] = xr[j].x;
@@ -144,7 +156,7 @@ k_contract_mfma(const float2* __restrict__ X, const float2* __restrict__ W, floa
       }
   }
   // D[m][n]: lane l, register r holds row 8(r/4) + 4(l/32) + r%4 (channel),
-  // column l%32 (batch entry).  Y rows [b][o][k0 .. k0+16) are 128-byte runs:
+  // column l%32 (batch entry).  Y rows [b][o][k0 .. k0+KB) are 8*KB-byte runs:
   // transpose through LDS, 16 batch entries at a time, and store whole runs.
   constexpr int YB = 32 * KB * 2 + 8;   // LDS stride of one batch entry: [o][mode][re/im]
   static_assert(16 * YB <= IC * KB * (MS + XM), "transpose tile fits the chunk buffers");
@@ -165,7 +177,7 @@ k_contract_mfma(const float2* __restrict__ X, const float2* __restrict__ W, floa
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < 16 * 32 * KB * 2 / 4 / THREADS; ++j) {
-      const int q = tid + THREADS * j, part = q & 7, row = q >> 3;
+      const int q = tid + THREADS * j, part = q % NP, row = q / NP;
       const int bl = row >> 5, o = row & 31;
       const int b = b0 + 16 * hb + bl;
       const int64_t k = k0 + 2 * part;
@@ -187,13 +199,38 @@ bool contract_mfma_supported(int B, int Ci, int Co, int64_t M, int64_t sWi, int6
          (int64_t)Ci * Co * M * 8 < (int64_t(1) << 31);
 }
 
-int contract_mfma(const float2* X, const float2* W, float2* Y, int B, int Ci, int Co, int64_t M,
-                  hipStream_t st) {
+template <int KB>
+static int launch_contract(const float2* X, const float2* W, float2* Y, int B, int Ci, int Co,
+                           int64_t M, hipStream_t st) {
   const int nblocks = (int)((M + KB - 1) / KB);
   const int pairs16 = (nblocks + 7) / 8;              // groups of 8 blocks
   dim3 grid((unsigned)(pairs16 * 16), (unsigned)((B + 31) / 32));
-  hipLaunchKernelGGL(k_contract_mfma, grid, dim3(THREADS), 0, st, X, W, Y, B, Ci, Co, M, nblocks);
+  const size_t lds = contract_lds(KB);
+  if (lds > 64 * 1024) {
+    int rc = hip_status(hipFuncSetAttribute(reinterpret_cast<const void*>(k_contract_mfma<KB>),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+                        "hipFuncSetAttribute(MaxDynamicSharedMemorySize)");
+    if (rc) return rc;
+  }
+  hipLaunchKernelGGL(k_contract_mfma<KB>, grid, dim3(contract_threads(KB)), lds, st, X, W, Y, B,
+                     Ci, Co, M, nblocks);
   return launch_status("k_contract_mfma");
+}
+
+// Workgroups of 16 modes pair up on a CU (8 waves, <= 128 VGPRs); a grid just
+// over one workgroup per CU would then leave a few CUs with two and double the
+// kernel time, so such grids take the smallest wider block that fits one per CU.
+int contract_mfma(const float2* X, const float2* W, float2* Y, int B, int Ci, int Co, int64_t M,
+                  hipStream_t st) {
+  const int64_t bt = (B + 31) / 32, cus = 256;
+  auto wgs = [&](int kb) { return 2 * ((M + kb - 1) / kb) * bt; };
+  if (wgs(16) > cus && wgs(16) <= 2 * cus) {
+    if (wgs(18) <= cus) return launch_contract<18>(X, W, Y, B, Ci, Co, M, st);
+    if (wgs(20) <= cus) return launch_contract<20>(X, W, Y, B, Ci, Co, M, st);
+    if (wgs(24) <= cus) return launch_contract<24>(X, W, Y, B, Ci, Co, M, st);
+    if (wgs(32) <= cus) return launch_contract<32>(X, W, Y, B, Ci, Co, M, st);
+  }
+  return launch_contract<16>(X, W, Y, B, Ci, Co, M, st);
 }
 
 }  // namespace fno
