@@ -37,6 +37,27 @@ WORKLOADS = {
 }
 
 
+PROFILES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
+
+
+def profiled_traffic(workload):
+    """HBM bytes per block call measured with rocprofv3 --pmc FETCH_SIZE and
+    WRITE_SIZE passes over this script, each scaled by what the counter reads
+    for a plain 1 GiB device copy (see the profile's calibration table), summed
+    over the four kernels; None when no such profile is committed."""
+    B, C, H, W, nm = WORKLOADS[workload]
+    m1, m2h = nm[0], nm[1] // 2 + 1
+    path = os.path.join(PROFILES, f"fused2d_block_b{B}c{C}_{H}x{W}_m{m1}x{m2h}_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_call:"):
+                    return int(line.split(":", 1)[1].strip().replace(",", ""))
+    except OSError:
+        pass
+    return None
+
+
 def algorithmic_bytes(B, C, H, W, m1, m2h):
     x = B * C * H * W * 4
     w = C * C * m1 * m2h * 8
@@ -236,9 +257,9 @@ def main():
                    "fused_path": bool(fused), "algorithmic_bytes": total_bytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved_block, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved_block / HBM_PEAK_GBS, 4),
-                     "traffic": None,
-                     "kernel": "whole block call (k_fwd_stream, k_contract_dense, k_inv_cols, "
-                               "k_row_epilogue on one stream), HIP events on that stream"},
+                     "traffic": profiled_traffic(args.workload),
+                     "kernel": "fno_spectral_block_f32: k_fwd_stream, k_contract_mfma, k_inv_cols, "
+                               "k_row_epilogue_r on one stream, HIP events on that stream"},
         "copy_bandwidth_gbs": round(copy_gbs, 1),
         "torch_rocm_baseline": rocm,
     }
