@@ -831,7 +831,9 @@ k_row_epilogue_r(const float* __restrict__ x, const float2* __restrict__ z,
               c.y = 0.f;
             }
             val = make_float2(a.x - c.y, a.y + c.x);           // Za + i Zb
-          } else if (k > W / 2 && W - k < m2h) {
+          } else if (u >= R - NB && k > W / 2 && W - k < m2h) {
+            // mirrors of bins < m2h <= 16 NB sit at u >= R - NB: the lanes'
+            // other inputs are compile-time zeros, which prunes the first pass
             const float2 a = ex[2 * (W - k)], c = ex[2 * (W - k) + 1];
             val = make_float2(a.x + c.y, c.x - a.y);           // conj Za + i conj Zb
           }
