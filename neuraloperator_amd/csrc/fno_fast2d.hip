@@ -173,14 +173,18 @@ k_fwd_stream(const float* __restrict__ x, float2* __restrict__ xhat, int m1, int
   static_assert(NF4 * 4 * T == W, "row split");
   const __amdgpu_buffer_rsrc_t rxp = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<float*>(xp), (short)0, H * W * 4, 0x00020000);
+  // cache policy 2 = non-temporal (nt): x streams through once here, and
+  // keeping it out of the caches' recent set measured 17 us faster at
+  // B32 C64 256^2 (the caches keep what the following kernels reuse)
+  constexpr int kNT = 2;
   auto load_rows = [&](uint32_t row, int lt, float4 (&dst)[2 * NF4]) __attribute__((always_inline)) {
     const uint32_t off = (row * W + 4 * lt) * 4u;
 #pragma unroll
     for (int k = 0; k < NF4; ++k) {
       dst[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
-                                              rxp, (int)(off + 16u * T * k), 0, 0));
+                                              rxp, (int)(off + 16u * T * k), 0, kNT));
       dst[NF4 + k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                    rxp, (int)(off + 16u * T * k), D * W * 4, 0));
+                                                    rxp, (int)(off + 16u * T * k), D * W * 4, kNT));
     }
   };
   // Chunk order: workgroups that share an XCD (ids 8 apart) start at
