@@ -140,6 +140,42 @@ def test_headline_block_per_sample_slice(cuda_device):
     assert err <= TOL, err
 
 
+def test_headline_full_batch_properties(cuda_device):
+    """The headline block at its full size (B32 C64 256^2, n_modes (64,64),
+    fused path) through properties that do not need the oracle at that size:
+    every sample equals the same block run on that sample alone (batch
+    indexing to the end of the buffers), the spectral part is linear, and the
+    last sample matches the float64 oracle."""
+    print("headline full batch B32 C64 256x256 modes 64x64", flush=True)
+    B, C, H, W = 32, 64, 256, 256
+    assert Fh.spectral_block_is_fused(B, C, C, [H, W], [64, 33], nat.SKIP_LINEAR)
+    g = torch.Generator().manual_seed(21)
+    w = (torch.complex(torch.randn(C, C, 64, 33, generator=g),
+                       torch.randn(C, C, 64, 33, generator=g)) / 64).to(cuda_device)
+    ws = (torch.randn(C, C, generator=g) / 8).to(cuda_device)
+    bias = (torch.randn(C, generator=g) / 8).to(cuda_device)
+    x = gaussian_random_field((B, C, H, W), seed=22, device=cuda_device)
+    with torch.no_grad():
+        y = Fh.spectral_block(x, w, bias, [64, 33], nat.SKIP_LINEAR, ws, nat.ACT_GELU)
+        for b in (0, 17, B - 1):
+            yb = Fh.spectral_block(x[b:b + 1].contiguous(), w, bias, [64, 33], nat.SKIP_LINEAR, ws,
+                                   nat.ACT_GELU)
+            assert (yb[0] - y[b]).abs().max().item() <= 1e-6 * y[b].abs().max().item(), b
+        # linearity of the spectral part: no skip, no bias, no activation
+        x2 = gaussian_random_field((B, C, H, W), seed=23, device=cuda_device)
+        f = lambda t: Fh.spectral_block(t, w, None, [64, 33], nat.SKIP_NONE, None, nat.ACT_NONE)
+        lhs = f(x + 2.0 * x2)
+        rhs = f(x) + 2.0 * f(x2)
+        assert rel_err(lhs, rhs) <= 1e-5
+        del x2, lhs, rhs
+    torch.cuda.synchronize()
+    xl = x[B - 1:].double().cpu()
+    ref = R.spectral_conv_forward(xl, w.cpu().to(torch.complex128), bias.cpu().double().view(-1, 1, 1),
+                                  [64, 33], [64, 33])
+    ref = R.gelu(ref + R.linear_skip(xl, ws.cpu().double()))
+    assert rel_err(y[B - 1:], ref) <= TOL
+
+
 @pytest.mark.parametrize("dim,sizes,nm", [
     (1, (1024,), (30,)),
     (1, (37,), (12,)),
