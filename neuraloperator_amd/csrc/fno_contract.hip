@@ -37,16 +37,15 @@ constexpr int WF4 = 4;            // W float4 per thread per chunk (IC*OH*KB/2/T
 constexpr int XF4 = 4;            // X float4 per thread per chunk (IC*32*KB/2/THREADS)
 __host__ __device__ constexpr int contract_threads(int kb) { return 64 * kb / MPW; }
 __host__ __device__ constexpr size_t contract_lds(int kb) {
-  return (size_t)IC * kb * (MS + XM) * sizeof(float);
+  return 2 * (size_t)IC * kb * (MS + XM) * sizeof(float);   // two chunk buffers
 }
 }  // namespace
 
-// KB modes per workgroup (KB/2 waves): 16 normally (two workgroups per CU,
-// so <= 128 VGPRs); 18..32 when that keeps the grid within one workgroup per
-// CU, which then needs only two waves per SIMD.
+// KB modes per workgroup (KB/2 waves, one workgroup per CU): 16 normally, 18
+// when that keeps the grid within one round.
 template <int KB>
 __global__ void __launch_bounds__(contract_threads(KB))
-__attribute__((amdgpu_waves_per_eu(KB == 16 ? 4 : 2, 4)))
+__attribute__((amdgpu_waves_per_eu(2, 4)))
 k_contract_mfma(const float2* __restrict__ X, const float2* __restrict__ W, float2* __restrict__ Y,
                 int B, int Ci, int Co, int64_t M, int nblocks) {
   constexpr int THREADS = contract_threads(KB);
@@ -55,8 +54,11 @@ k_contract_mfma(const float2* __restrict__ X, const float2* __restrict__ W, floa
                 "tile split");
   extern __shared__ float4 smem4[];
   float* smem = reinterpret_cast<float*>(smem4);
-  float* Ws = smem;                   // W chunk [i][mode][re/im plane][o]
-  float* Xs = smem + IC * KB * MS;    // X chunk [i][mode][re/im][b]
+  // two chunk buffers, each W chunk [i][mode][re/im plane][o] then
+  // X chunk [i][mode][re/im][b]
+  constexpr int BUF = IC * KB * (MS + XM);
+  auto Wbuf = [&](int d) __attribute__((always_inline)) { return smem + d * BUF; };
+  auto Xbuf = [&](int d) __attribute__((always_inline)) { return smem + d * BUF + IC * KB * MS; };
   // pair (mode block, channel half) placement: the halves of block p run on
   // one XCD (workgroup id mod 8), 8 ids apart
   const int bid = blockIdx.x;
@@ -102,7 +104,9 @@ k_contract_mfma(const float2* __restrict__ X, const float2* __restrict__ W, floa
       xr[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0));
     }
   };
-  auto stash = [&]() __attribute__((always_inline)) {
+  auto stash = [&](int buf) __attribute__((always_inline)) {
+    float* Ws = Wbuf(buf);
+    float* Xs = Xbuf(buf);
 #pragma unroll
     for (int j = 0; j < WF4; ++j) {
       const int q = tid + THREADS * j, part = q % NP, row = q / NP;
@@ -135,31 +139,54 @@ k_contract_mfma(const float2* __restrict__ X, const float2* __restrict__ W, floa
   const int c = lane >> 5, oo = lane & 31;
   const float sgn = c ? -1.f : 1.f;   // A[o][2i+1] = -Wi
 
+  // Double-buffered chunks: chunk n+1 is transposed into the other buffer
+  // while the MFMAs of chunk n run, and chunk n+2 is in flight meanwhile, so
+  // one barrier per chunk separates the phases.
   load(0);
+  stash(0);
+  if (IC < Ci) load(IC);
+  __syncthreads();
 #pragma unroll 1
-  for (int i0 = 0; i0 < Ci; i0 += IC) {
-    __syncthreads();   // the previous chunk's operand reads are done
-    stash();
-    if (i0 + IC < Ci) load(i0 + IC);
-    __syncthreads();
-#pragma unroll
-    for (int s = 0; s < IC; ++s)
+  for (int i0 = 0, cb = 0; i0 < Ci; i0 += IC, cb ^= 1) {
+    if (i0 + IC < Ci) {
+      stash(cb ^ 1);
+      if (i0 + 2 * IC < Ci) load(i0 + 2 * IC);
+    }
+    const float* Ws = Wbuf(cb);
+    const float* Xs = Xbuf(cb);
+    // operands of input channel s + 1 are read while the MFMAs of s run
+    float bv[2][MPW], ar[2][MPW], ai[2][MPW];
+    auto operands = [&](int s, int d) __attribute__((always_inline)) {
 #pragma unroll
       for (int mm = 0; mm < MPW; ++mm) {
         const int m = MPW * w + mm;
-        const float bv = Xs[(s * KB + m) * XM + c * 32 + oo];
+        bv[d][mm] = Xs[(s * KB + m) * XM + c * 32 + oo];
         const float* wrow = Ws + (s * KB + m) * MS + oo;
-        const float ar = sgn * wrow[c * PS];        // Yr rows: Wr (c=0), -Wi (c=1)
-        const float ai = wrow[(1 - c) * PS];        // Yi rows: Wi (c=0),  Wr (c=1)
-        acc[mm][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(ar, bv, acc[mm][0], 0, 0, 0);
-        acc[mm][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(ai, bv, acc[mm][1], 0, 0, 0);
+        ar[d][mm] = wrow[c * PS];         // Yr rows: Wr (c=0), Wi (c=1, negated below)
+        ai[d][mm] = wrow[(1 - c) * PS];   // Yi rows: Wi (c=0), Wr (c=1)
       }
+    };
+    operands(0, 0);
+#pragma unroll
+    for (int s = 0; s < IC; ++s) {
+      if (s + 1 < IC) operands(s + 1, (s + 1) & 1);
+      __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead of the MFMAs
+#pragma unroll
+      for (int mm = 0; mm < MPW; ++mm) {
+        acc[mm][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(sgn * ar[s & 1][mm], bv[s & 1][mm],
+                                                          acc[mm][0], 0, 0, 0);
+        acc[mm][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(ai[s & 1][mm], bv[s & 1][mm],
+                                                          acc[mm][1], 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    __syncthreads();   // chunk n+1 is in place; chunk n's buffer is free
   }
   // D[m][n]: lane l, register r holds row 8(r/4) + 4(l/32) + r%4 (channel),
   // column l%32 (batch entry).  Y rows [b][o][k0 .. k0+KB) are 8*KB-byte runs:
   // transpose through LDS, 16 batch entries at a time, and store whole runs.
   constexpr int YB = 32 * KB * 2 + 8;   // LDS stride of one batch entry: [o][mode][re/im]
-  static_assert(16 * YB <= IC * KB * (MS + XM), "transpose tile fits the chunk buffers");
+  static_assert(16 * YB <= 2 * IC * KB * (MS + XM), "transpose tile fits the chunk buffers");
 #pragma unroll 1
   for (int hb = 0; hb < 2; ++hb) {
     __syncthreads();
@@ -217,18 +244,15 @@ static int launch_contract(const float2* X, const float2* W, float2* Y, int B, i
   return launch_status("k_contract_mfma");
 }
 
-// Workgroups of 16 modes pair up on a CU (8 waves, <= 128 VGPRs); a grid just
-// over one workgroup per CU would then leave a few CUs with two and double the
-// kernel time, so such grids take the smallest wider block that fits one per CU.
+// One workgroup per CU (the double-buffered tile takes 136-157 KB of LDS at
+// 16-18 modes); a grid just over the CU count would leave a few CUs a second
+// round, so such grids take the smallest wider block that fits one round.
 int contract_mfma(const float2* X, const float2* W, float2* Y, int B, int Ci, int Co, int64_t M,
                   hipStream_t st) {
   const int64_t bt = (B + 31) / 32, cus = 256;
   auto wgs = [&](int kb) { return 2 * ((M + kb - 1) / kb) * bt; };
   if (wgs(16) > cus && wgs(16) <= 2 * cus) {
     if (wgs(18) <= cus) return launch_contract<18>(X, W, Y, B, Ci, Co, M, st);
-    if (wgs(20) <= cus) return launch_contract<20>(X, W, Y, B, Ci, Co, M, st);
-    if (wgs(24) <= cus) return launch_contract<24>(X, W, Y, B, Ci, Co, M, st);
-    if (wgs(32) <= cus) return launch_contract<32>(X, W, Y, B, Ci, Co, M, st);
   }
   return launch_contract<16>(X, W, Y, B, Ci, Co, M, st);
 }
