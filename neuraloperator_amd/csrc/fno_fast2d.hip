@@ -868,12 +868,27 @@ k_row_epilogue_r(const float* __restrict__ x, const float2* __restrict__ z,
 #pragma unroll
       for (int c = 0; c < NCH; ++c) {
         const float* ring = region + (c & 1) * KC * XS + (lane >> 4) * XS + (lane & 15);
+        // B operands in groups of 4 tiles: group g + 1 is read while the 4
+        // MFMAs of group g run, so the LDS latency hides under them
+        constexpr int GT = 4, NG = KC / 4 * R / GT;
+        float bq[2][GT];
 #pragma unroll
-        for (int kk = 0; kk < KC / 4; ++kk)
+        for (int u = 0; u < GT; ++u) bq[0][u] = ring[16 * u];
 #pragma unroll
-          for (int u = 0; u < R; ++u)
-            acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(aW[c * (KC / 4) + kk],
-                                                          ring[4 * kk * XS + 16 * u], acc[u], 0, 0, 0);
+        for (int g = 0; g < NG; ++g) {
+          if (g + 1 < NG) {
+            const int kn = (g + 1) * GT / R, un = (g + 1) * GT % R;
+#pragma unroll
+            for (int u = 0; u < GT; ++u) bq[(g + 1) & 1][u] = ring[4 * kn * XS + 16 * (un + u)];
+          }
+          __builtin_amdgcn_sched_barrier(0);
+          const int kk = g * GT / R, u0 = g * GT % R;
+#pragma unroll
+          for (int u = 0; u < GT; ++u)
+            acc[u0 + u] = __builtin_amdgcn_mfma_f32_16x16x4f32(aW[c * (KC / 4) + kk], bq[g & 1][u],
+                                                               acc[u0 + u], 0, 0, 0);
+          __builtin_amdgcn_sched_barrier(0);
+        }
         if (c + 1 < NCH) {
           store_chunk((c + 1) & 1, xst[(c + 1) & 1]);
           if (c + 3 < NCH) load_chunk(h, c + 3, xst[(c + 1) & 1]);
