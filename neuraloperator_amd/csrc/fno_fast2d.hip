@@ -111,8 +111,6 @@ __device__ __forceinline__ float act_select(float g, float v, uint32_t m) {
 }
 
 // ------------------------------------------------------------------------ K1
-// Row stride (float2) of K1's chunk spectrum: >= m2h and = 8 (mod 32).
-__host__ __device__ constexpr int fwd_row_stride(int m2h) { return (m2h + 23) / 32 * 32 + 8; }
 
 // Kept window of a plane: rows kh in [kmin, kmin + m1), kmin = -(m1/2), stored
 // at window row kh - kmin; columns kw < m2h.  A kept row kh is reached from its
@@ -139,12 +137,15 @@ k_fwd_stream(const float* __restrict__ x, float2* __restrict__ xhat, int m1, int
   float2* twW = reinterpret_cast<float2*>(smem4);  // w_W^t, t < W
   float2* twH = twW + W;                             // w_H^t, t < H
   float2* exall = twH + H;
-  // spectrum row r = 2 * line + (0 | 1): SP = 8 (mod 32) float2 puts the 4
-  // rows a half-wave reads in the column stage 16 banks apart
-  const int SP = fwd_row_stride(m2h);
-  const int sbase = WREG - 2 * LPW * SP;
+  // spectrum row r = 2 * line + (0 | 1), stride SP float2: >= m2h (<= 64),
+  // = 8 (mod 32) so the 4 rows a half-wave reads in the column stage sit 16
+  // banks apart, and a compile-time constant so row addresses fold into
+  // instruction offsets
+  constexpr int SP = 72;
+  constexpr int sbase = WREG - 2 * LPW * SP;
+  static_assert(sbase >= 0, "spectrum rows fit the wavefront region");
   auto srow = [&](int r) __attribute__((always_inline)) {
-    return exall + (r / (2 * LPW)) * WREG + sbase + (r % (2 * LPW)) * SP;
+    return exall + (__mul24(r / (2 * LPW), WREG) + sbase + __mul24(r % (2 * LPW), SP));
   };
   fill_twiddles<W>(twW);
   fill_twiddles<H>(twH);
@@ -271,7 +272,7 @@ k_fwd_stream(const float* __restrict__ x, float2* __restrict__ xhat, int m1, int
       for (int k1 = 0; k1 < 8; ++k1) srow(((j + (k1 >> 1)) & 3) + 4 * k1)[col] = f[k1];
       wave_sync();
       // w_H^(-kh c) for kh = k0 + 32 e is w_H^(-k0 c) * u^e, u = w_H^(-32 c)
-      const float2 u = twH[(-32 * c) & (H - 1)];
+      const float2 u = twH[(H - 32 * c) & (H - 1)];
 #pragma unroll
       for (int e2 = 0; e2 < 2; ++e2) {
         const int k1 = 2 * j + e2;
@@ -284,7 +285,8 @@ k_fwd_stream(const float* __restrict__ x, float2* __restrict__ xhat, int m1, int
           const int kr = k1 + 8 * k2;  // frequency mod 32
           const int k0 = kmin + ((kr - kmin) & 31);
           // rows kh >= kmin + m1 accumulate too; they are never written
-          float2 q = cmul(P[k2], twH[(-k0 * c) & (H - 1)]);
+          // (-k0 c) mod H with a 24-bit multiply (|k0| <= 64, c < 8)
+          float2 q = cmul(P[k2], twH[__mul24(-k0, c) & (H - 1)]);
           acc[e2][k2][0] = cadd(acc[e2][k2][0], q);
 #pragma unroll
           for (int e = 1; e < KPR; ++e) {
