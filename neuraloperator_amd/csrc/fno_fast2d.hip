@@ -28,7 +28,10 @@
 //                          an LDS ring with the next row's loads in flight;
 //                        * bias, gated skip add and erf GELU in registers, one
 //                          write of y.
-//                      (k_row_epilogue: the LDS-staged variant for W = 128.)
+//                      At W = 128 a step is two adjacent rows, one per 8-lane
+//                      half of each 16-lane group.
+//                      (k_row_epilogue: the LDS-staged variant for the
+//                      channel counts K4 does not cover.)
 //
 // Semantics follow SpectralConv.forward (neuralop/layers/spectral_convolution.py
 // :429-568) with output size == input size, and the post-activation block of
@@ -706,21 +709,29 @@ k_row_epilogue(const float* __restrict__ x, const float2* __restrict__ z,
 // into registers), so a workgroup needs ~36 KB of LDS and two share a CU.
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-template <int CO, int CI, int NB>
+template <int W, int CO, int CI, int NB>
 __global__ void __launch_bounds__(CO * 4) __attribute__((amdgpu_waves_per_eu(2, 2)))
 k_row_epilogue_r(const float* __restrict__ x, const float2* __restrict__ z,
                  const float* __restrict__ skip_w, const float* __restrict__ bias,
                  float* __restrict__ y, int H, int TR, int m2h, int skip_kind, int act,
                  float inv_scale) {
-  constexpr int W = 256, T = 16, R = 16, Q = 1;
+  // A step covers PW = 256 pixels of every channel: one row at W = 256, two
+  // adjacent rows at W = 128 (the two 8-lane halves of each 16-lane group run
+  // one row each).  Lane t of a group holds pixel p(u, t) = (t / T) W + t % T
+  // + T u of tile u, which is column t of MFMA tile u.
+  using PL = LinePlan<W>;
+  constexpr int T = PL::T, R = PL::R, Q = PL::Q;
+  constexpr int PW = 256, ROWS = PW / W;
+  static_assert(R == 16 && T * ROWS == 16, "16 tiles of 16 pixels per step");
   constexpr int NWAVE = CO / 16, BLOCK = 64 * NWAVE;
   constexpr int KC = 16;                 // input channels per LDS chunk
-  constexpr int NCH = CI / KC;           // chunks per row
-  constexpr int XS = W + 16;             // LDS row stride of a chunk (floats)
-  constexpr int KS = CI / 4;             // MFMA k-steps per row
-  constexpr int LPT = KC * W / 4 / BLOCK;  // float4 loads per thread per chunk
-  constexpr int EXS = W + 8;             // exchange slice per group (float2)
-  static_assert(CO % 16 == 0 && CI % KC == 0 && LPT >= 1 && KC * W / 4 % BLOCK == 0, "shape");
+  constexpr int NCH = CI / KC;           // chunks per step
+  constexpr int XS = PW + 16;            // LDS row stride of a chunk (floats)
+  constexpr int KS = CI / 4;             // MFMA k-steps per step
+  constexpr int LPT = KC * PW / 4 / BLOCK; // float4 loads per thread per chunk
+  constexpr int EXS = PW + 8;            // exchange slice per 16-lane group (float2)
+  constexpr int HS = EXS / ROWS;         // ... per line (one per half at W = 128)
+  static_assert(CO % 16 == 0 && CI % KC == 0 && LPT >= 1 && KC * PW / 4 % BLOCK == 0, "shape");
   extern __shared__ float4 smem4[];
   float2* twW = reinterpret_cast<float2*>(smem4);
   float* region = reinterpret_cast<float*>(twW + W);   // exchange slices / x ring
@@ -729,6 +740,7 @@ k_row_epilogue_r(const float* __restrict__ x, const float2* __restrict__ z,
   const int b = blockIdx.x / RB, h0 = (blockIdx.x % RB) * TR;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int G = lane >> 4, t = lane & 15;
+  const int half = t / T, tl = t % T;  // row of the step, lane within the line
   const uint32_t HW = (uint32_t)H * W;
   const bool linear = (skip_kind == FNO_SKIP_LINEAR);
   const bool gated = (skip_kind == FNO_SKIP_SOFT_GATING || skip_kind == FNO_SKIP_IDENTITY);
@@ -778,16 +790,17 @@ k_row_epilogue_r(const float* __restrict__ x, const float2* __restrict__ z,
     }
   };
   // Z[b][o][h][kw]: bins of channel o0 + 2L (za) and the next channel (zc,
-  // one H x m2h plane further); bins past m2h read past the buffer end: zero
+  // one H x m2h plane further) in the lane's row; bins past m2h read past the
+  // buffer end: zero
   const int zplane = __builtin_amdgcn_readfirstlane(H * m2h * 8);
   auto load_z = [&](int h) __attribute__((always_inline)) {
     const __amdgpu_buffer_rsrc_t rz = make_rsrc(zs, zbytes);
 #pragma unroll
     for (int L = 0; L < 2; ++L) {
-      const uint32_t zo = (((uint32_t)(o0 + 2 * L) * H + h) * m2h + t) * 8u;
+      const uint32_t zo = (((uint32_t)(o0 + 2 * L) * H + h + half) * m2h + tl) * 8u;
 #pragma unroll
       for (int n = 0; n < NB; ++n) {
-        const uint32_t off = (t + T * n < m2h) ? zo + 8u * T * n : 0x80000000u;
+        const uint32_t off = (tl + T * n < m2h) ? zo + 8u * T * n : 0x80000000u;
         za[L][n] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rz, (int)off, 0, 0));
         zc[L][n] = __builtin_bit_cast(float2,
                                       __builtin_amdgcn_raw_buffer_load_b64(rz, (int)off, zplane, 0));
@@ -797,8 +810,9 @@ k_row_epilogue_r(const float* __restrict__ x, const float2* __restrict__ z,
 
   // Row order: workgroups that share an XCD (ids 8 apart) start at different
   // rows of their block, so concurrent x reads spread over the HBM channels.
-  const int rot = (int)(blockIdx.x >> 3) % TR;
-  auto row_at = [&](int s) __attribute__((always_inline)) { return h0 + (s + rot) % TR; };
+  const int NS = TR / ROWS;              // steps per workgroup
+  const int rot = (int)(blockIdx.x >> 3) % NS;
+  auto row_at = [&](int s) __attribute__((always_inline)) { return h0 + ROWS * ((s + rot) % NS); };
 
   // first row's operands
   if (linear) {
@@ -809,16 +823,16 @@ k_row_epilogue_r(const float* __restrict__ x, const float2* __restrict__ z,
   __syncthreads();
 
 #pragma unroll 1
-  for (int s = 0; s < TR; ++s) {
+  for (int s = 0; s < NS; ++s) {
     const int h = row_at(s);
     // ---- inverse row FFTs: line L packs channels o0+2L (re) and o0+2L+1 (im)
     {
-      float2* ex = reinterpret_cast<float2*>(region) + (4 * wave + G) * EXS;
+      float2* ex = reinterpret_cast<float2*>(region) + (4 * wave + G) * EXS + half * HS;
 #pragma unroll
       for (int L = 0; L < 2; ++L) {
 #pragma unroll
         for (int u = 0; u < NB; ++u) {
-          const int k = t + T * u;
+          const int k = tl + T * u;
           if (k < m2h) {
             ex[2 * k] = za[L][u];
             ex[2 * k + 1] = zc[L][u];
@@ -828,7 +842,7 @@ k_row_epilogue_r(const float* __restrict__ x, const float2* __restrict__ z,
         float2 v[R];
 #pragma unroll
         for (int u = 0; u < R; ++u) {
-          const int k = t + T * u;
+          const int k = tl + T * u;
           float2 val = make_float2(0.f, 0.f);
           if (u < NB && k < m2h) {
             float2 a = za[L][u < NB ? u : 0], c = zc[L][u < NB ? u : 0];
@@ -847,11 +861,12 @@ k_row_epilogue_r(const float* __restrict__ x, const float2* __restrict__ z,
         }
         wave_sync();
         float2 out[Q][T];
-        line_fft<W, +1>(v, ex, twW, t, out);
+        line_fft<W, +1>(v, ex, twW, tl, out);
+        // out[q][s] is pixel tl + T (q + Q s) of the line: tile u = q + Q s
 #pragma unroll
         for (int u = 0; u < R; ++u) {
-          acc[u][2 * L] = fmaf(out[0][u].x, inv_scale, bch[2 * L]);
-          acc[u][2 * L + 1] = fmaf(out[0][u].y, inv_scale, bch[2 * L + 1]);
+          acc[u][2 * L] = fmaf(out[u % Q][u / Q].x, inv_scale, bch[2 * L]);
+          acc[u][2 * L + 1] = fmaf(out[u % Q][u / Q].y, inv_scale, bch[2 * L + 1]);
         }
       }
     }
@@ -860,7 +875,7 @@ k_row_epilogue_r(const float* __restrict__ x, const float2* __restrict__ z,
       for (int u = 0; u < R; ++u)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          acc[u][r] += gch[r] * xs[(size_t)(o0 + r) * HW + (size_t)h * W + 16 * u + t];
+          acc[u][r] += gch[r] * xs[(size_t)(o0 + r) * HW + (size_t)(h + half) * W + T * u + tl];
     }
     __syncthreads();   // exchange slices free: the region becomes the x ring
     if (linear) {
@@ -869,19 +884,19 @@ k_row_epilogue_r(const float* __restrict__ x, const float2* __restrict__ z,
       __syncthreads();
 #pragma unroll
       for (int c = 0; c < NCH; ++c) {
-        const float* ring = region + (c & 1) * KC * XS + (lane >> 4) * XS + (lane & 15);
+        const float* ring = region + (c & 1) * KC * XS + (lane >> 4) * XS + half * W + tl;
         // B operands in groups of 4 tiles: group g + 1 is read while the 4
         // MFMAs of group g run, so the LDS latency hides under them
         constexpr int GT = 4, NG = KC / 4 * R / GT;
         float bq[2][GT];
 #pragma unroll
-        for (int u = 0; u < GT; ++u) bq[0][u] = ring[16 * u];
+        for (int u = 0; u < GT; ++u) bq[0][u] = ring[T * u];
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
           if (g + 1 < NG) {
             const int kn = (g + 1) * GT / R, un = (g + 1) * GT % R;
 #pragma unroll
-            for (int u = 0; u < GT; ++u) bq[(g + 1) & 1][u] = ring[4 * kn * XS + 16 * (un + u)];
+            for (int u = 0; u < GT; ++u) bq[(g + 1) & 1][u] = ring[4 * kn * XS + T * (un + u)];
           }
           __builtin_amdgcn_sched_barrier(0);
           const int kk = g * GT / R, u0 = g * GT % R;
@@ -899,17 +914,17 @@ k_row_epilogue_r(const float* __restrict__ x, const float2* __restrict__ z,
       }
     }
     // ---- next row's operands in flight during GELU + store and its FFTs
-    if (s + 1 < TR) {
+    if (s + 1 < NS) {
       if (linear) {
         load_chunk(row_at(s + 1), 0, xst[0]);
         if (NCH > 1) load_chunk(row_at(s + 1), 1, xst[1]);
       }
       load_z(row_at(s + 1));
     }
-    // ---- activation and store: channel o0 + r, pixel 16u + t
+    // ---- activation and store: channel o0 + r, pixel p(u, t)
     {
       const __amdgpu_buffer_rsrc_t ry = make_rsrc(ys, ybytes);
-      const uint32_t yo = ((uint32_t)o0 * HW + (uint32_t)h * W + t) * 4u;
+      const uint32_t yo = ((uint32_t)o0 * HW + (uint32_t)(h + half) * W + tl) * 4u;
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -917,7 +932,7 @@ k_row_epilogue_r(const float* __restrict__ x, const float2* __restrict__ z,
           float v = acc[u][r];
           v = act_select(gelu_erf(v), v, gmask);
           __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ry,
-                                                (int)(yo + 64u * u),
+                                                (int)(yo + 4u * T * u),
                                                 __builtin_amdgcn_readfirstlane((int)(r * HW * 4u)), 0);
         }
     }
@@ -1121,46 +1136,59 @@ static size_t epi_r_lds_bytes(int Co) {
 }
 
 static bool epi_r_supported(int H, int W, int Ci, int Co, int m2h, int skip_kind) {
-  if (W != 256 || H % 16 != 0) return false;
+  if (!(W == 128 || W == 256) || H % 16 != 0) return false;
   if (!(Co == 64 || Co == 128)) return false;
   const int ci = (skip_kind == FNO_SKIP_LINEAR) ? Ci : Co;
   if (!(ci == 32 || ci == 64 || ci == 128)) return false;
   if ((skip_kind == FNO_SKIP_IDENTITY || skip_kind == FNO_SKIP_SOFT_GATING) && Ci != Co)
     return false;
-  if (m2h < 1 || m2h > 128) return false;   // mirror staging fits a 264-entry slice
+  // 8 bins per lane at most (NB = 8, T = W / 16 lanes per line); the mirror
+  // staging (2 m2h entries) fits the line's 264 / (256 / W) entry slice
+  if (m2h < 1 || m2h > W / 2) return false;
   return epi_r_lds_bytes(Co) <= kMaxLds;
 }
 
-template <int CO, int CI, int NB>
+template <int W, int CO, int CI, int NB>
 static int launch_epi_r(const float* x, const float2* z, const float* skip_w, const float* bias,
                         float* y, int B, int H, int m2h, int skip_kind, int act, float inv_scale,
                         hipStream_t st) {
   const size_t lds = epi_r_lds_bytes(CO);
-  int rc = allow_lds(k_row_epilogue_r<CO, CI, NB>, lds);
+  int rc = allow_lds(k_row_epilogue_r<W, CO, CI, NB>, lds);
   if (rc) return rc;
   const int TR = 16;
   const int64_t grid = (int64_t)B * (H / TR);
-  hipLaunchKernelGGL((k_row_epilogue_r<CO, CI, NB>), dim3((unsigned)grid), dim3(CO * 4), lds, st,
-                     x, z, skip_w, bias, y, H, TR, m2h, skip_kind, act, inv_scale);
+  hipLaunchKernelGGL((k_row_epilogue_r<W, CO, CI, NB>), dim3((unsigned)grid), dim3(CO * 4), lds,
+                     st, x, z, skip_w, bias, y, H, TR, m2h, skip_kind, act, inv_scale);
   return launch_status("k_row_epilogue_r");
 }
 
-static int dispatch_epi_r(int Co, int Ci, const float* x, const float2* z, const float* skip_w,
-                          const float* bias, float* y, int B, int H, int m2h, int skip_kind,
-                          int act, float inv_scale, hipStream_t st) {
+template <int W>
+static int dispatch_epi_r_w(int Co, int Ci, const float* x, const float2* z, const float* skip_w,
+                            const float* bias, float* y, int B, int H, int m2h, int skip_kind,
+                            int act, float inv_scale, hipStream_t st) {
   const int ci = (skip_kind == FNO_SKIP_LINEAR) ? Ci : Co;
-  const bool few = (m2h + 15) / 16 <= 3;
-#define FNO_EPI_R(co, cin)                                                                   \
-  if (Co == co && ci == cin)                                                                 \
-    return few ? launch_epi_r<co, cin, 3>(x, z, skip_w, bias, y, B, H, m2h, skip_kind, act,  \
-                                          inv_scale, st)                                     \
-               : launch_epi_r<co, cin, 8>(x, z, skip_w, bias, y, B, H, m2h, skip_kind, act,  \
-                                          inv_scale, st);
+  const bool few = m2h <= 3 * (W / 16);   // 3 bins per lane
+#define FNO_EPI_R(co, cin)                                                                      \
+  if (Co == co && ci == cin)                                                                    \
+    return few ? launch_epi_r<W, co, cin, 3>(x, z, skip_w, bias, y, B, H, m2h, skip_kind, act,  \
+                                             inv_scale, st)                                     \
+               : launch_epi_r<W, co, cin, 8>(x, z, skip_w, bias, y, B, H, m2h, skip_kind, act,  \
+                                             inv_scale, st);
   FNO_EPI_R(64, 32) FNO_EPI_R(64, 64) FNO_EPI_R(64, 128)
   FNO_EPI_R(128, 32) FNO_EPI_R(128, 64) FNO_EPI_R(128, 128)
 #undef FNO_EPI_R
   set_error("fused 2D epilogue: unsupported Co=%d Ci=%d", Co, Ci);
   return FNO_ERR_UNSUPPORTED;
+}
+
+static int dispatch_epi_r(int W, int Co, int Ci, const float* x, const float2* z,
+                          const float* skip_w, const float* bias, float* y, int B, int H, int m2h,
+                          int skip_kind, int act, float inv_scale, hipStream_t st) {
+  if (W == 128)
+    return dispatch_epi_r_w<128>(Co, Ci, x, z, skip_w, bias, y, B, H, m2h, skip_kind, act,
+                                 inv_scale, st);
+  return dispatch_epi_r_w<256>(Co, Ci, x, z, skip_w, bias, y, B, H, m2h, skip_kind, act,
+                               inv_scale, st);
 }
 
 static int dispatch_epi(int W, int Co, int Ci, const float* x, const float2* z,
@@ -1210,7 +1238,8 @@ int fast2d_block(const float* x, const float2* w, const float* bias, const float
   rc = dispatch_inv(H, yhat, zbuf, B, Co, m1, m2h, st);
   if (rc) return rc;
   if (epi_r_supported(H, W, Ci, Co, m2h, skip_kind))
-    return dispatch_epi_r(Co, Ci, x, zbuf, skip_w, bias, y, B, H, m2h, skip_kind, act, iscale, st);
+    return dispatch_epi_r(W, Co, Ci, x, zbuf, skip_w, bias, y, B, H, m2h, skip_kind, act, iscale,
+                          st);
   return dispatch_epi(W, Co, Ci, x, zbuf, skip_w, bias, y, B, H, m2h, skip_kind, act, iscale, st);
 }
 

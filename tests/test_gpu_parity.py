@@ -73,6 +73,9 @@ FUSED_CASES = [
     (2, 32, 64, 256, 128, (33, 30)),
     (1, 64, 32, 128, 256, (20, 64)),
     (1, 32, 32, 64, 128, (64, 128)),    # every row and the Nyquist column kept
+    (1, 64, 64, 128, 128, (48, 60)),    # 128-wide rows in pairs, 8 bins per lane
+    (1, 64, 64, 64, 128, (32, 126)),    # ... with the widest window that path takes
+    (1, 64, 128, 64, 128, (16, 16)),    # ... with 8 waves per workgroup
 ]
 
 
