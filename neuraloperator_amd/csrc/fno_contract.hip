@@ -41,8 +41,9 @@ __host__ __device__ constexpr size_t contract_lds(int kb) {
 }
 }  // namespace
 
-// KB modes per workgroup (KB/2 waves, one workgroup per CU): 16 normally, 18
-// when that keeps the grid within one round.
+// KB modes per workgroup (KB/2 waves): 16 normally (one workgroup per CU), 18
+// when that keeps the grid within one round, 8 when even 16 leaves most CUs
+// idle.
 template <int KB>
 __global__ void __launch_bounds__(contract_threads(KB))
 __attribute__((amdgpu_waves_per_eu(2, 4)))
@@ -254,6 +255,8 @@ int contract_mfma(const float2* X, const float2* W, float2* Y, int B, int Ci, in
   if (wgs(16) > cus && wgs(16) <= 2 * cus) {
     if (wgs(18) <= cus) return launch_contract<18>(X, W, Y, B, Ci, Co, M, st);
   }
+  // few modes (e.g. 32 x 17): halve the block so twice the CUs take part
+  if (2 * wgs(16) <= cus) return launch_contract<8>(X, W, Y, B, Ci, Co, M, st);
   return launch_contract<16>(X, W, Y, B, Ci, Co, M, st);
 }
 
