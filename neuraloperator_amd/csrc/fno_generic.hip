@@ -1,8 +1,10 @@
 // Generic kernels of the FNO spectral path: any spatial size (up to 4096 per
 // axis), 1-3 spatial dims, any mode window.  Each spatial axis is handled by a
 // direct pruned DFT (only the kept frequencies are computed, O(N*m) per line),
-// which is the right tool when m << N or N is not a power of two; the fused 2D
-// kernels in fno_fast2d.hip take over for large power-of-two planes.
+// which is the right tool when m << N or N is not a power of two; the last
+// axis of 64-, 128- and 256-point lines goes through line FFTs instead
+// (fno_generic_fft.hip), and the fused 2D kernels in fno_fast2d.hip take over
+// for large power-of-two planes.
 //
 // Frequency bookkeeping follows SpectralConv.forward
 // (neuralop/layers/spectral_convolution.py:429-568):
@@ -15,6 +17,7 @@
 //   last     irfft(n = N') with the imaginary parts of bin 0 (and of bin N/2
 //            when N' is even, enforce_hermitian_symmetry) zeroed (:550-559)
 #include "fno_common.h"
+#include "fno_twiddle.h"
 
 #include <cmath>
 #include <cstdarg>
@@ -76,7 +79,7 @@ k_r2c_direct(const float* __restrict__ x, float2* __restrict__ out, int64_t rows
   extern __shared__ float smem[];
   float2* tw = reinterpret_cast<float2*>(smem);
   float* xs = reinterpret_cast<float*>(tw + N);
-  for (int t = threadIdx.x; t < N; t += blockDim.x) tw[t] = twiddle_pos(t, N);
+  for (int t = threadIdx.x; t < N; t += blockDim.x) tw[t] = twiddle_any(t, N);
   const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
   const int nr = (int)min((int64_t)rows_per_block, rows - r0);
   const float* xg = x + r0 * N;
@@ -106,7 +109,7 @@ k_c2c_fwd_direct(const float2* __restrict__ in, float2* __restrict__ out, int64_
                  int64_t inner, int m, float scale) {
   extern __shared__ float smem[];
   float2* tw = reinterpret_cast<float2*>(smem);
-  for (int t = threadIdx.x; t < N; t += blockDim.x) tw[t] = twiddle_pos(t, N);
+  for (int t = threadIdx.x; t < N; t += blockDim.x) tw[t] = twiddle_any(t, N);
   __syncthreads();
   const int64_t total = outer * m * inner;
   for (int64_t task = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; task < total;
@@ -141,7 +144,7 @@ k_c2c_inv_direct(const float2* __restrict__ in, float2* __restrict__ out, int64_
                  int Np, int64_t inner, int m, float scale) {
   extern __shared__ float smem[];
   float2* tw = reinterpret_cast<float2*>(smem);
-  for (int t = threadIdx.x; t < Np; t += blockDim.x) tw[t] = twiddle_pos(t, Np);
+  for (int t = threadIdx.x; t < Np; t += blockDim.x) tw[t] = twiddle_any(t, Np);
   __syncthreads();
   const int64_t total = outer * Np * inner;
   for (int64_t task = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; task < total;
@@ -172,7 +175,7 @@ k_c2r_direct(const float2* __restrict__ in, float* __restrict__ out, const float
   extern __shared__ float smem[];
   float2* tw = reinterpret_cast<float2*>(smem);
   float2* zs = tw + Np;
-  for (int t = threadIdx.x; t < Np; t += blockDim.x) tw[t] = twiddle_pos(t, Np);
+  for (int t = threadIdx.x; t < Np; t += blockDim.x) tw[t] = twiddle_any(t, Np);
   const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
   const int nr = (int)min((int64_t)rows_per_block, rows - r0);
   const int K = min(m, Np / 2 + 1);
@@ -347,6 +350,18 @@ static int64_t fwd_stage_elems(int64_t planes, int32_t ndim, const int32_t* size
   return e;
 }
 
+// line-FFT last-axis transforms (fno_generic_fft.hip)
+bool r2c_fft_supported(int N, int m, int64_t rows);
+int r2c_fft(const float* x, float2* out, int64_t rows, int N, int m, float scale, hipStream_t st);
+bool c2r_fft_supported(int Np, int64_t rows);
+int c2r_fft(const float2* in, float* out, const float* bias, int64_t rows, int64_t rows_per_plane,
+            int channels, int N, int Np, int m, int enforce, float scale, hipStream_t st);
+bool c2c_fft_supported(int L, int64_t outer, int64_t inner);
+int c2c_fft_fwd(const float2* in, float2* out, int64_t outer, int64_t inner, int N, int m,
+                float scale, hipStream_t st);
+int c2c_fft_inv(const float2* in, float2* out, int64_t outer, int64_t inner, int N, int Np, int m,
+                float scale, hipStream_t st);
+
 int rfft_window(const float* x, float2* xhat, int64_t planes, int32_t ndim, const int32_t* sizes,
                 const int32_t* modes, int32_t norm, void* ws, size_t ws_bytes, hipStream_t st) {
   // stage s transforms axis (ndim-1-s); stage outputs go to the workspace
@@ -366,18 +381,23 @@ int rfft_window(const float* x, float2* xhat, int64_t planes, int32_t ndim, cons
     const int N = sizes[ndim - 1], m = modes[ndim - 1];
     int64_t rows = planes;
     for (int d = 0; d < ndim - 1; ++d) rows *= sizes[d];
-    int rpb = (int)((48 * 1024 - 8 * N) / (4 * N));
-    if (rpb < 1) rpb = 1;
-    if (rpb > 64) rpb = 64;
-    const size_t lds = (size_t)N * 8 + (size_t)rpb * N * 4;
     float2* dst = ndim == 1 ? xhat : bufA;
-    const int64_t blocks = (rows + rpb - 1) / rpb;
     // only the last stage of the chain carries the scale
     const float sc = (ndim == 1) ? (float)scale : 1.f;
-    hipLaunchKernelGGL(k_r2c_direct, dim3((unsigned)blocks), dim3(kThreads), lds, st, x, dst, rows,
-                       N, m, rpb, sc);
-    int rc = launch_status("k_r2c_direct");
-    if (rc) return rc;
+    if (r2c_fft_supported(N, m, rows)) {
+      int rc = r2c_fft(x, dst, rows, N, m, sc, st);
+      if (rc) return rc;
+    } else {
+      int rpb = (int)((48 * 1024 - 8 * N) / (4 * N));
+      if (rpb < 1) rpb = 1;
+      if (rpb > 64) rpb = 64;
+      const size_t lds = (size_t)N * 8 + (size_t)rpb * N * 4;
+      const int64_t blocks = (rows + rpb - 1) / rpb;
+      hipLaunchKernelGGL(k_r2c_direct, dim3((unsigned)blocks), dim3(kThreads), lds, st, x, dst,
+                         rows, N, m, rpb, sc);
+      int rc = launch_status("k_r2c_direct");
+      if (rc) return rc;
+    }
   }
   // middle axes, innermost first
   const float2* src = bufA;
@@ -389,9 +409,14 @@ int rfft_window(const float* x, float2* xhat, int64_t planes, int32_t ndim, cons
     const int N = sizes[d], m = modes[d];
     float2* dst = (d == 0) ? xhat : bufB;
     const float sc = (d == 0) ? (float)scale : 1.f;
-    hipLaunchKernelGGL(k_c2c_fwd_direct, dim3(grid_for(outer * m * inner)), dim3(kThreads),
-                       (size_t)N * 8, st, src, dst, outer, N, inner, m, sc);
-    int rc = launch_status("k_c2c_fwd_direct");
+    int rc;
+    if (c2c_fft_supported(N, outer, inner)) {
+      rc = c2c_fft_fwd(src, dst, outer, inner, N, m, sc, st);
+    } else {
+      hipLaunchKernelGGL(k_c2c_fwd_direct, dim3(grid_for(outer * m * inner)), dim3(kThreads),
+                         (size_t)N * 8, st, src, dst, outer, N, inner, m, sc);
+      rc = launch_status("k_c2c_fwd_direct");
+    }
     if (rc) return rc;
     src = dst;
   }
@@ -426,9 +451,14 @@ int irfft_window(const float2* yhat, const float* bias, float* y, int64_t batch,
     for (int a = d + 1; a < ndim; ++a) inner *= modes[a];
     float2* dst = (d == 0) ? bufA : bufB;
     const int N = in_sizes[d], Np = out_sizes[d], m = modes[d];
-    hipLaunchKernelGGL(k_c2c_inv_direct, dim3(grid_for(outer * Np * inner)), dim3(kThreads),
-                       (size_t)Np * 8, st, src, dst, outer, N, Np, inner, m, 1.f);
-    int rc = launch_status("k_c2c_inv_direct");
+    int rc;
+    if (c2c_fft_supported(Np, outer, inner)) {
+      rc = c2c_fft_inv(src, dst, outer, inner, N, Np, m, 1.f, st);
+    } else {
+      hipLaunchKernelGGL(k_c2c_inv_direct, dim3(grid_for(outer * Np * inner)), dim3(kThreads),
+                         (size_t)Np * 8, st, src, dst, outer, N, Np, inner, m, 1.f);
+      rc = launch_status("k_c2c_inv_direct");
+    }
     if (rc) return rc;
     src = dst;
   }
@@ -436,19 +466,25 @@ int irfft_window(const float2* yhat, const float* bias, float* y, int64_t batch,
     int64_t rows = planes;
     for (int a = 0; a < ndim - 1; ++a) rows *= out_sizes[a];
     const int N = in_sizes[ndim - 1], Np = out_sizes[ndim - 1], m = modes[ndim - 1];
-    const int K = m < Np / 2 + 1 ? m : Np / 2 + 1;
-    int rpb = kThreads / (Np < kThreads ? Np : kThreads);
-    if (rpb < 1) rpb = 1;
-    if (rpb > 32) rpb = 32;
-    const size_t lds = (size_t)Np * 8 + (size_t)rpb * K * 8;
     // rows run over (b, c, outer spatial...): the channel of a row is
     // (row / rows_per_plane) mod channels
     const int64_t rows_per_plane = rows / planes;
-    hipLaunchKernelGGL(k_c2r_direct, dim3((unsigned)((rows + rpb - 1) / rpb)), dim3(kThreads), lds,
-                       st, src, y, bias, rows, rows_per_plane, channels, N, Np, m, enforce, rpb,
-                       (float)scale);
-    int rc = launch_status("k_c2r_direct");
-    if (rc) return rc;
+    if (c2r_fft_supported(Np, rows)) {
+      int rc = c2r_fft(src, y, bias, rows, rows_per_plane, channels, N, Np, m, enforce,
+                       (float)scale, st);
+      if (rc) return rc;
+    } else {
+      const int K = m < Np / 2 + 1 ? m : Np / 2 + 1;
+      int rpb = kThreads / (Np < kThreads ? Np : kThreads);
+      if (rpb < 1) rpb = 1;
+      if (rpb > 32) rpb = 32;
+      const size_t lds = (size_t)Np * 8 + (size_t)rpb * K * 8;
+      hipLaunchKernelGGL(k_c2r_direct, dim3((unsigned)((rows + rpb - 1) / rpb)), dim3(kThreads),
+                         lds, st, src, y, bias, rows, rows_per_plane, channels, N, Np, m, enforce,
+                         rpb, (float)scale);
+      int rc = launch_status("k_c2r_direct");
+      if (rc) return rc;
+    }
   }
   return FNO_OK;
 }

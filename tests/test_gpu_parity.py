@@ -186,6 +186,17 @@ def test_headline_full_batch_properties(cuda_device):
     (2, (9, 10), (4, 5)),
     (3, (16, 16, 16), (8, 8, 8)),
     (3, (8, 9, 10), (4, 4, 4)),
+    # last axis through the line-FFT kernels (64 / 128 / 256 points)
+    (1, (64,), (10,)),
+    (1, (256,), (256,)),                # every bin, Nyquist included
+    (2, (12, 128), (6, 40)),
+    (2, (9, 256), (4, 20)),
+    (3, (8, 16, 64), (4, 8, 18)),
+    # non-last axes through the tiled line-FFT kernels
+    (2, (64, 20), (31, 7)),             # odd window, inner run shorter than a tile
+    (2, (128, 64), (64, 20)),
+    (2, (256, 16), (256, 5)),           # every bin of the middle axis
+    (3, (64, 128, 12), (16, 32, 5)),
 ])
 @pytest.mark.parametrize("norm", ["forward", "backward", "ortho"])
 def test_generic_spectral_conv(dim, sizes, nm, norm, cuda_device):
@@ -217,6 +228,28 @@ def test_resolution_scaling(scale, dim, size, cuda_device):
     ref = R.spectral_conv_forward(x.double(), conv.weight.to_tensor().detach().cpu().to(torch.complex128),
                                   conv.bias.detach().cpu().double(), conv.n_modes, conv.max_n_modes,
                                   resolution_scaling_factor=[scale] * dim)
+    assert rel_err(y, ref) <= TOL
+
+
+@pytest.mark.parametrize("enforce", [True, False])
+@pytest.mark.parametrize("shape_in,shape_out,nm", [
+    ((16, 64), (16, 128), (8, 20)),     # line-FFT inverse onto a longer row
+    ((16, 128), (16, 64), (8, 40)),     # ... onto a shorter one (bins past 33 dropped)
+    ((7, 256), (7, 256), (4, 130)),     # odd number of rows, Nyquist kept
+    ((64, 24), (128, 24), (20, 8)),     # middle axis onto a longer line
+    ((128, 24), (64, 24), (40, 8)),     # ... onto a shorter one (bins past 32 dropped)
+    ((256, 8), (256, 8), (255, 4)),     # odd window over all 256 bins
+])
+def test_line_fft_output_shapes(enforce, shape_in, shape_out, nm, cuda_device):
+    torch.manual_seed(15)
+    conv = na.SpectralConv(3, 5, nm, enforce_hermitian_symmetry=enforce).to(cuda_device)
+    x = torch.randn(1, 3, *shape_in)
+    with torch.no_grad():
+        y = conv(x.to(cuda_device), output_shape=shape_out)
+    assert list(y.shape) == [1, 5, *shape_out]
+    ref = R.spectral_conv_forward(x.double(), conv.weight.to_tensor().detach().cpu().to(torch.complex128),
+                                  conv.bias.detach().cpu().double(), conv.n_modes, conv.max_n_modes,
+                                  output_shape=shape_out, enforce_hermitian_symmetry=enforce)
     assert rel_err(y, ref) <= TOL
 
 
