@@ -38,6 +38,17 @@ WORKLOADS = {
 }
 
 
+# Workloads timed through the nn.Module API (one forward per step)
+MODULE_WORKLOADS = {
+    "c0": "1D SpectralConv x[16,64,1024] ~N(0,1), n_modes 30 -> 16 rfft modes, dense W[64,64,16]",
+    "c3": "4-layer FNO forward x[64,1,256,256] bf16 GRF (+2 grid channels), lifting 3->128->64, "
+          "4 blocks hidden 64 n_modes (64,64) with channel MLP 64->32->64 and soft-gating, "
+          "projection 64->128->1",
+    "c4": "3D TFNO block x[8,32,64,64,64] GRF, Tucker rank 0.1 spectral conv n_modes (16,16,16) "
+          "-> 16x16x9 modes (factorized), 1x1 skip, bias, erf GELU",
+}
+
+
 PROFILES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
 
 
@@ -152,12 +163,142 @@ def cpu_baseline(B, C, H, W, nm, total_bytes, budget_s=20.0):
     }
 
 
+def _oracle_layer(blocks, i):
+    """Parameters of FNOBlocks layer i as float64 CPU tensors for the oracle."""
+    conv = blocks.convs[i]
+    d = lambda t: t.detach().cpu().double()
+    layer = {"conv": dict(weight=conv.weight.to_tensor().detach().cpu().to(torch.complex128),
+                          bias=d(conv.bias), n_modes=conv.n_modes, max_n_modes=conv.max_n_modes),
+             "fno_skip": {"type": "linear", "w": d(blocks.fno_skips[i].conv.weight)[:, :, 0]}}
+    if blocks.use_channel_mlp:
+        m = blocks.channel_mlp[i]
+        layer["mlp"] = {"weights": [d(f.weight) for f in m.fcs], "biases": [d(f.bias) for f in m.fcs]}
+        layer["mlp_skip"] = {"type": "soft-gating", "w": d(blocks.channel_mlp_skips[i].weight)}
+    return layer
+
+
+def module_workload(name, dev):
+    """(step function, algorithmic bytes, dtype, cpu-baseline runner or None)
+    for the workloads timed through the module API."""
+    import neuraloperator_amd as na
+    from neuraloperator_amd import _native as nat
+    from neuraloperator_amd.synthetic import gaussian_random_field
+    torch.manual_seed(7)
+    if name == "c0":
+        B, C, N = 16, 64, 1024
+        conv = na.SpectralConv(C, C, (30,)).to(dev)            # 30 // 2 + 1 = 16 modes
+        g = torch.Generator().manual_seed(7)
+        with torch.no_grad():
+            w = torch.complex(torch.randn(C, C, 16, generator=g), torch.randn(C, C, 16, generator=g)) / 64
+            conv.weight.tensor.copy_(w.to(dev))
+        x = torch.randn(B, C, N, generator=g).to(dev)
+        nbytes = 2 * B * C * N * 4 + C * C * 16 * 8 + C * 4
+
+        def cpu():
+            from oracle import spectral_ref as R
+            xc = x.cpu()
+            return lambda: R.spectral_conv_forward(
+                xc, conv.weight.to_tensor().detach().cpu(), conv.bias.detach().cpu(), conv.n_modes,
+                conv.max_n_modes), B, B
+        return (lambda: conv(x)), nbytes, "f32", cpu
+    if name == "c4":
+        B, C, S = 8, 32, 64
+        conv = na.SpectralConv(C, C, (16, 16, 16), factorization="Tucker", rank=0.1,
+                               implementation="factorized").to(dev)
+        x = gaussian_random_field((B, C, S, S, S), seed=2024, device=dev)
+        ws = (torch.randn(C, C) / (C ** 0.5)).to(dev)
+        nbytes = 2 * B * C * S ** 3 * 4 + C * C * 4 + C * 4 + sum(
+            p.numel() * p.element_size() for p in conv.weight.parameters())
+
+        def cpu():
+            from oracle import spectral_ref as R
+            xs = x[:1].cpu()
+            core = conv.weight.core.detach().cpu()
+            factors = [f.detach().cpu() for f in conv.weight.factors]
+            wsc = ws.cpu()
+            return lambda: R.gelu(R.spectral_conv_forward(
+                xs, {"tucker": (core, factors)}, conv.bias.detach().cpu(), conv.n_modes,
+                conv.max_n_modes, implementation="factorized") + R.linear_skip(xs, wsc)), 1, B
+        return (lambda: conv._forward_hip(x, None, nat.SKIP_LINEAR, ws, nat.ACT_GELU)), nbytes, "f32", cpu
+    # c3
+    B, H = 64, 256
+    model = na.FNO((64, 64), in_channels=1, out_channels=1, hidden_channels=64, n_layers=4).to(dev)
+    x = gaussian_random_field((B, 1, H, H), seed=2024, device=dev).to(torch.bfloat16)
+    # per block: bf16 activation in and out, the block's weights once
+    blk = model.fno_blocks
+    wbytes = sum(p.numel() * p.element_size() for p in blk.parameters()) // blk.n_layers
+    nbytes = blk.n_layers * (2 * B * 64 * H * H * 2 + wbytes)
+
+    def cpu():
+        from oracle import spectral_ref as R
+        d = lambda t: t.detach().cpu().double()
+        mlp = lambda m: {"weights": [d(f.weight) for f in m.fcs], "biases": [d(f.bias) for f in m.fcs]}
+        params = {"lifting": mlp(model.lifting), "projection": mlp(model.projection),
+                  "layers": [_oracle_layer(blk, i) for i in range(blk.n_layers)]}
+        xs = x[:1].float().cpu().double()
+        return lambda: R.fno_forward(xs, params), 1, B
+    # activations are fp32 inside the model; the bf16 input is widened on entry
+    return (lambda: model(x.float())), nbytes, "f32 (bf16 input widened on entry)", cpu
+
+
+def bench_module(args):
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    step, nbytes, dtype, cpu = module_workload(args.workload, dev)
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+        warm = event_times(step, max(args.steps, 20), stream)
+    us_warm = statistics.median(warm) * 1e3
+    line = {
+        "metric": f"µs/call + achieved HBM GB/s, {MODULE_WORKLOADS[args.workload]}",
+        "value": round(nbytes / (ms_per_step * 1e-3) / 1e9, 1),
+        "unit": "GB/s",
+        "us_per_call": round(ms_per_step * 1e3, 1),
+        "us_per_call_median_warm": round(us_warm, 1),
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": dtype,
+        "data": "synthetic (seeded Gaussian random field / normal inputs, seeded random-init weights)",
+        "config": {"workload": MODULE_WORKLOADS[args.workload], "algorithmic_bytes": nbytes},
+        "roofline": {"bound": "hbm", "achieved": round(nbytes / (us_warm * 1e-6) / 1e9, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(nbytes / (us_warm * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": "whole forward, HIP events on the launch stream"},
+    }
+    if not args.no_cpu:
+        torch.set_num_threads(os.cpu_count() or 1)
+        run, done, total = cpu()
+        with torch.no_grad():
+            run()
+            times = []
+            t_start = time.perf_counter()
+            while len(times) < 3 or (time.perf_counter() - t_start < 20 and len(times) < 20):
+                t1 = time.perf_counter()
+                run()
+                times.append(time.perf_counter() - t1)
+        per_call = statistics.median(times) * total / done
+        line["cpu_baseline"] = {"value": round(nbytes / per_call / 1e9, 3), "unit": "GB/s",
+                                "us_per_call": round(per_call * 1e6, 1),
+                                "cores": torch.get_num_threads(), "kind": "port",
+                                "sample": f"{done} of {total} samples, median of {len(times)} runs, "
+                                          f"scaled x{total // done} to one call"}
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS) + sorted(MODULE_WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-torch", action="store_true", help="skip the torch ROCm baseline")
     args = ap.parse_args()
@@ -168,6 +309,9 @@ def main():
                                    "(the block shards by batch with no communication)",
                           "n_gpus": args.gpus}))
         sys.exit(2)
+
+    if args.workload in MODULE_WORKLOADS:
+        return bench_module(args)
 
     import neuraloperator_amd  # noqa: F401  (loads the library early)
     from neuraloperator_amd import _native as nat

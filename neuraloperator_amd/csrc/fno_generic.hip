@@ -277,41 +277,70 @@ k_axis_matmul(const float2* __restrict__ in, const float2* __restrict__ mat, flo
 }
 
 // ------------------------------------------------------------------- epilogue
-// y[b, o, p] = act(spec[b, o, p] + skip(x)[b, o, p]); spec may alias y.
-template <int OT>
+// y[b, o, p] = act(spec[b, o, p] + skip(x)[b, o, p]); spec may alias y (each
+// thread reads its spec entries before writing the same entries).
+// A thread owns PP consecutive points and OT output channels, so x is read once
+// per OT output channels; the linear skip's weights sit transposed in LDS
+// (wT[i][o]) and are read as broadcast float4s.
+template <int OT, int PP>
 __global__ void __launch_bounds__(kThreads)
 k_epilogue(const float* spec, const float* __restrict__ x, const float* __restrict__ ws, float* y,
            int B, int Ci, int Co, int64_t P, int skip_kind, int act) {
-  const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  typedef float vpp __attribute__((ext_vector_type(PP)));
+  extern __shared__ float4 smem4[];
+  float* wT = reinterpret_cast<float*>(smem4);   // [Ci][OT], linear skip only
   const int o0 = blockIdx.y * OT;
   const int b = blockIdx.z;
+  const int on = min(OT, Co - o0);
+  const bool linear = skip_kind == FNO_SKIP_LINEAR;
+  if (linear) {
+    for (int e = threadIdx.x; e < Ci * OT; e += kThreads) {
+      const int i = e / OT, c = e % OT;
+      wT[e] = c < on ? ws[(int64_t)(o0 + c) * Ci + i] : 0.f;
+    }
+    __syncthreads();
+  }
+  const int64_t p = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * PP;
   if (p >= P) return;
-  float acc[OT];
+  vpp acc[OT];
 #pragma unroll
-  for (int c = 0; c < OT; ++c) acc[c] = 0.f;
-  if (skip_kind == FNO_SKIP_LINEAR) {
+  for (int c = 0; c < OT; ++c) acc[c] = (vpp)0.f;
+  if (linear) {
     const float* xb = x + (int64_t)b * Ci * P + p;
+    // x of the next input channel is in flight while this one is used
+    vpp vn = *reinterpret_cast<const vpp*>(xb);
+#pragma unroll 2
     for (int i = 0; i < Ci; ++i) {
-      const float v = xb[(int64_t)i * P];
+      const vpp v = vn;
+      if (i + 1 < Ci) vn = *reinterpret_cast<const vpp*>(xb + (int64_t)(i + 1) * P);
+      const float4* w4 = reinterpret_cast<const float4*>(wT + i * OT);
 #pragma unroll
-      for (int c = 0; c < OT; ++c)
-        if (o0 + c < Co) acc[c] = fmaf(ws[(int64_t)(o0 + c) * Ci + i], v, acc[c]);
+      for (int c4 = 0; c4 < OT / 4; ++c4) {
+        const float4 w = w4[c4];
+        acc[4 * c4 + 0] += w.x * v;
+        acc[4 * c4 + 1] += w.y * v;
+        acc[4 * c4 + 2] += w.z * v;
+        acc[4 * c4 + 3] += w.w * v;
+      }
     }
   } else if (skip_kind == FNO_SKIP_SOFT_GATING || skip_kind == FNO_SKIP_IDENTITY) {
 #pragma unroll
     for (int c = 0; c < OT; ++c)
-      if (o0 + c < Co) {
-        const float v = x[((int64_t)b * Ci + o0 + c) * P + p];
+      if (c < on) {
+        const vpp v = *reinterpret_cast<const vpp*>(x + ((int64_t)b * Ci + o0 + c) * P + p);
         acc[c] = (skip_kind == FNO_SKIP_SOFT_GATING) ? ws[o0 + c] * v : v;
       }
   }
 #pragma unroll
   for (int c = 0; c < OT; ++c) {
-    if (o0 + c >= Co) break;
+    if (c >= on) break;
     const int64_t idx = ((int64_t)b * Co + o0 + c) * P + p;
-    float v = spec[idx] + acc[c];
-    if (act == FNO_ACT_GELU) v = gelu_erf(v);
-    y[idx] = v;
+    vpp v = *reinterpret_cast<const vpp*>(spec + idx) + acc[c];
+    if (act == FNO_ACT_GELU) {
+#pragma unroll
+      for (int k = 0; k < PP; ++k) v[k] = gelu_erf(v[k]);
+    }
+    *reinterpret_cast<vpp*>(y + idx) = v;
   }
 }
 
@@ -522,13 +551,45 @@ int axis_matmul(const float2* in, const float2* mat, float2* out, int64_t outer,
   return launch_status("k_axis_matmul");
 }
 
+template <int OT, int PP>
+static int launch_epilogue(const float* spec, const float* x, const float* ws, float* y, int B,
+                           int Ci, int Co, int64_t P, int skip_kind, int act, hipStream_t st) {
+  const int64_t per = (int64_t)kThreads * PP;
+  dim3 grid((unsigned)((P + per - 1) / per), (unsigned)((Co + OT - 1) / OT), (unsigned)B);
+  const size_t lds = skip_kind == FNO_SKIP_LINEAR ? (size_t)Ci * OT * sizeof(float) : 0;
+  if (lds > 160 * 1024) {
+    set_error("block epilogue: %d input channels exceed the staged skip weights", Ci);
+    return FNO_ERR_UNSUPPORTED;
+  }
+  if (lds > 48 * 1024) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_epilogue<OT, PP>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) {
+      set_error("block epilogue: %s", hipGetErrorString(e));
+      return FNO_ERR_HIP;
+    }
+  }
+  hipLaunchKernelGGL((k_epilogue<OT, PP>), grid, dim3(kThreads), lds, st, spec, x, ws, y, B, Ci, Co,
+                     P, skip_kind, act);
+  return launch_status("k_epilogue");
+}
+
 int block_epilogue(const float* spec, const float* x, const float* ws, float* y, int B, int Ci,
                    int Co, int64_t P, int skip_kind, int act, hipStream_t st) {
-  constexpr int OT = 16;
-  dim3 grid((unsigned)((P + kThreads - 1) / kThreads), (unsigned)((Co + OT - 1) / OT), (unsigned)B);
-  hipLaunchKernelGGL((k_epilogue<OT>), grid, dim3(kThreads), 0, st, spec, x, ws, y, B, Ci, Co, P,
-                     skip_kind, act);
-  return launch_status("k_epilogue");
+  // vector access needs every (b, c) row to start on the vector boundary
+  const uintptr_t addr = reinterpret_cast<uintptr_t>(spec) | reinterpret_cast<uintptr_t>(x) |
+                         reinterpret_cast<uintptr_t>(y);
+  const bool v4 = P % 4 == 0 && addr % 16 == 0, v2 = P % 2 == 0 && addr % 8 == 0;
+  // wide output blocks while their staged weights stay small
+  const bool wide_ok = skip_kind != FNO_SKIP_LINEAR || (size_t)Ci * 64 * sizeof(float) <= 64 * 1024;
+  if (Co <= 16 || !wide_ok)
+    return v4 ? launch_epilogue<16, 4>(spec, x, ws, y, B, Ci, Co, P, skip_kind, act, st)
+              : launch_epilogue<16, 1>(spec, x, ws, y, B, Ci, Co, P, skip_kind, act, st);
+  if (Co <= 32)
+    return v4 ? launch_epilogue<32, 4>(spec, x, ws, y, B, Ci, Co, P, skip_kind, act, st)
+              : launch_epilogue<32, 1>(spec, x, ws, y, B, Ci, Co, P, skip_kind, act, st);
+  return v2 ? launch_epilogue<64, 2>(spec, x, ws, y, B, Ci, Co, P, skip_kind, act, st)
+            : launch_epilogue<64, 1>(spec, x, ws, y, B, Ci, Co, P, skip_kind, act, st);
 }
 
 int validate_window(int32_t ndim, const int32_t* sizes, const int32_t* modes) {

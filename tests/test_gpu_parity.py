@@ -385,6 +385,56 @@ def test_errors_raise(cuda_device):
         conv(x).sum().backward()
 
 
+@pytest.mark.parametrize("Ci,Co,S", [(3, 4, (8, 9)), (32, 32, (16, 16, 16)), (20, 24, (37,)),
+                                      (64, 48, (10, 12)), (64, 64, (33, 7)), (32, 96, (64,)),
+                                      (300, 40, (16,))])
+@pytest.mark.parametrize("skip", ["linear", "soft-gating", "identity", "none"])
+def test_block_epilogue(Ci, Co, S, skip, cuda_device):
+    """Generic epilogue act(spec + skip(x)) against float64 torch: channel
+    counts on and off the 16/32/64 output blocks, point counts with and without
+    4- and 2-point vectors, more input channels than the wide blocks stage."""
+    if skip in ("soft-gating", "identity") and Ci != Co:
+        Ci = Co
+    g = torch.Generator().manual_seed(21)
+    B = 2
+    spec = torch.randn(B, Co, *S, generator=g)
+    x = torch.randn(B, Ci, *S, generator=g)
+    kind = {"linear": nat.SKIP_LINEAR, "soft-gating": nat.SKIP_SOFT_GATING,
+            "identity": nat.SKIP_IDENTITY, "none": nat.SKIP_NONE}[skip]
+    ws = {"linear": torch.randn(Co, Ci, generator=g) / Ci ** 0.5,
+          "soft-gating": torch.rand(Co, generator=g) + 0.5}.get(skip)
+    ref = spec.double()
+    if skip == "linear":
+        ref = ref + torch.einsum("oi,bi...->bo...", ws.double(), x.double())
+    elif skip == "soft-gating":
+        ref = ref + ws.double().view(1, -1, *([1] * len(S))) * x.double()
+    elif skip == "identity":
+        ref = ref + x.double()
+    ref = R.gelu(ref)
+    with torch.no_grad():
+        y = Fh.block_epilogue(spec.to(cuda_device), x.to(cuda_device) if skip != "none" else None, kind,
+                              None if ws is None else ws.to(cuda_device), nat.ACT_GELU)
+    torch.cuda.synchronize()
+    assert rel_err(y, ref) <= TOL
+
+
+def test_block_epilogue_unaligned_views(cuda_device):
+    """Tensors that start one float past a 16-byte boundary take the scalar
+    path and still match."""
+    g = torch.Generator().manual_seed(22)
+    B, C, P = 2, 32, 64
+    sbuf = torch.randn(B * C * P + 1, generator=g)
+    xbuf = torch.randn(B * C * P + 1, generator=g)
+    ws = torch.randn(C, C, generator=g) / C ** 0.5
+    spec, x = sbuf[1:].view(B, C, P), xbuf[1:].view(B, C, P)
+    ref = R.gelu(spec.double() + torch.einsum("oi,bip->bop", ws.double(), x.double()))
+    sd, xd = sbuf.to(cuda_device)[1:].view(B, C, P), xbuf.to(cuda_device)[1:].view(B, C, P)
+    with torch.no_grad():
+        y = Fh.block_epilogue(sd, xd, nat.SKIP_LINEAR, ws.to(cuda_device), nat.ACT_GELU)
+    torch.cuda.synchronize()
+    assert rel_err(y, ref) <= TOL
+
+
 def test_kernel_gelu_matches_exact_erf(cuda_device):
     """The kernels' erf GELU (Abramowitz & Stegun 7.1.28 form) against exact
     erf GELU in float64 over [-12, 12], through the C-ABI epilogue with no
