@@ -131,6 +131,29 @@ int fno_block_epilogue_f32(const float* spec, const float* x, const float* skip_
                            int64_t points, int32_t skip_kind, int32_t act, void* stream);
 
 /*
+ * Fused channel MLP of an FNO layer: y = act(W2 gelu(W1 x + b1) + b2 + skip).
+ * Replaces ChannelMLP.forward with n_layers = 2 (neuralop/layers/channel_mlp.py
+ * :82-119: two 1x1 Conv1d with GELU between), the channel-MLP skip
+ * (SoftGating.forward, skip_connections.py:88-93, or identity) and the second
+ * activation of FNOBlocks.forward_with_postactivation (fno_block.py:363-379).
+ *   x       float32 [B, Ci, P] (16-byte aligned); y float32 [B, Co, P], may
+ *           alias x or skip_x
+ *   w1 [Ch, Ci], b1 [Ch] (may be NULL), w2 [Co, Ch], b2 [Co] (may be NULL)
+ *   skip_kind FNO_SKIP_NONE, FNO_SKIP_SOFT_GATING (skip_x [B, Co, P] scaled
+ *           by skip_weight [Co] plus skip_bias [Co] or NULL) or
+ *           FNO_SKIP_IDENTITY (skip_x added)
+ * Covered: (Ci, Ch, Co) in {(32,16,32), (64,32,64), (128,64,128)}, P % 4 == 0;
+ * otherwise FNO_ERR_UNSUPPORTED (fno_channel_mlp_is_supported tells which).
+ */
+int fno_channel_mlp_f32(const float* x, const float* w1, const float* b1, const float* w2,
+                        const float* b2, const float* skip_x, const float* skip_weight,
+                        const float* skip_bias, float* y, int64_t batch, int32_t in_channels,
+                        int32_t hidden_channels, int32_t out_channels, int64_t points,
+                        int32_t skip_kind, int32_t act, void* stream);
+int fno_channel_mlp_is_supported(int32_t in_channels, int32_t hidden_channels,
+                                 int32_t out_channels, int64_t points);
+
+/*
  * One call for the whole spectral block
  *     y = act(SpectralConv(x) + skip(x))
  * with a dense weight (w [Ci, Co, m_1..m_ndim] window, complex64) and bias

@@ -24,6 +24,10 @@ int axis_matmul(const float2* in, const float2* mat, float2* out, int64_t outer,
                 int64_t inner, hipStream_t st);
 int block_epilogue(const float* spec, const float* x, const float* ws, float* y, int B, int Ci,
                    int Co, int64_t P, int skip_kind, int act, hipStream_t st);
+bool channel_mlp_supported(int Ci, int Ch, int Co, int64_t P);
+int channel_mlp(const float* x, const float* w1, const float* b1, const float* w2, const float* b2,
+                const float* xs, const float* sw, const float* sb, float* y, int64_t B, int Ci,
+                int Ch, int Co, int64_t P, int skip_kind, int act, hipStream_t st);
 bool fast2d_supported(int B, int Ci, int Co, int ndim, const int32_t* sizes, const int32_t* modes,
                       int skip_kind);
 size_t fast2d_workspace(int B, int Ci, int Co, const int32_t* sizes, const int32_t* modes);
@@ -208,6 +212,43 @@ int fno_block_epilogue_f32(const float* spec, const float* x, const float* skip_
   if (rc) return rc;
   return block_epilogue(spec, x, skip_weight, y, batch, in_channels, out_channels, points,
                         skip_kind, act, reinterpret_cast<hipStream_t>(stream));
+}
+
+int fno_channel_mlp_is_supported(int32_t in_channels, int32_t hidden_channels,
+                                 int32_t out_channels, int64_t points) {
+  return channel_mlp_supported(in_channels, hidden_channels, out_channels, points) ? 1 : 0;
+}
+
+int fno_channel_mlp_f32(const float* x, const float* w1, const float* b1, const float* w2,
+                        const float* b2, const float* skip_x, const float* skip_weight,
+                        const float* skip_bias, float* y, int64_t batch, int32_t in_channels,
+                        int32_t hidden_channels, int32_t out_channels, int64_t points,
+                        int32_t skip_kind, int32_t act, void* stream) {
+  clear_error();
+  FNO_CHECK_ARG(x && w1 && w2 && y, "x/w1/w2/y must not be NULL");
+  FNO_CHECK_ARG(batch >= 1 && in_channels >= 1 && hidden_channels >= 1 && out_channels >= 1 &&
+                    points >= 1,
+                "bad batch/channels/points");
+  FNO_CHECK_ARG(skip_kind == FNO_SKIP_NONE || skip_kind == FNO_SKIP_SOFT_GATING ||
+                    skip_kind == FNO_SKIP_IDENTITY,
+                "channel MLP skip must be none, soft-gating or identity (got %d)", skip_kind);
+  FNO_CHECK_ARG(skip_kind == FNO_SKIP_NONE || skip_x, "skip_x must not be NULL with a skip");
+  FNO_CHECK_ARG(skip_kind != FNO_SKIP_SOFT_GATING || skip_weight,
+                "soft-gating needs a skip weight");
+  FNO_CHECK_ARG(act == FNO_ACT_NONE || act == FNO_ACT_GELU, "unknown activation %d", act);
+  if (!channel_mlp_supported(in_channels, hidden_channels, out_channels, points)) {
+    set_error("channel MLP %d -> %d -> %d over %lld points is not covered by the kernel",
+              in_channels, hidden_channels, out_channels, (long long)points);
+    return FNO_ERR_UNSUPPORTED;
+  }
+  const uintptr_t addr = reinterpret_cast<uintptr_t>(x);
+  if (addr % 16 != 0) {
+    set_error("channel MLP: x must be 16-byte aligned");
+    return FNO_ERR_UNSUPPORTED;
+  }
+  return channel_mlp(x, w1, b1, w2, b2, skip_x, skip_weight, skip_bias, y, batch, in_channels,
+                     hidden_channels, out_channels, points, skip_kind, act,
+                     reinterpret_cast<hipStream_t>(stream));
 }
 
 int fno_spectral_block_is_fused(int32_t batch, int32_t in_channels, int32_t out_channels,

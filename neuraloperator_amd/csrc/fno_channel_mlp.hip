@@ -1,0 +1,216 @@
+// Fused channel MLP of an FNO layer:
+//
+//   y = act( W2 gelu(W1 x + b1) + b2 + skip(xs) )
+//
+// the two pointwise 1x1 convolutions of ChannelMLP.forward
+// (neuralop/layers/channel_mlp.py:82-119, n_layers = 2, GELU between), the
+// channel-MLP skip (SoftGating.forward, neuralop/layers/skip_connections.py
+// :88-93, or identity) and the block's second activation
+// (neuralop/layers/fno_block.py:363-379), in one pass over the field: x and xs
+// are read once, y written once, the hidden activation never leaves the CU.
+//
+// k_channel_mlp<CI, CH, CO>: persistent workgroups of 4 waves stride over
+// tiles of TP = 128 points of one sample.  Per tile:
+//   * the [CI][TP] slab of x moves through LDS (the next tile's slab is in
+//     flight in registers while this one is computed);
+//   * GEMM 1 on v_mfma_f32_16x16x4f32: each wave owns 32 points (2 column
+//     tiles) and all CH hidden rows; A (W1) comes from LDS in lane order, B
+//     (x) from the slab;
+//   * bias + GELU in the accumulators;
+//   * GEMM 2 takes its B operand straight from GEMM 1's accumulators: lane
+//     group G holds hidden rows 16m + 4G + r (register r) of its point column,
+//     so k-step (m, r) contracts hidden row 16m + 4G + r in lane group G, and
+//     W2 is staged in that order;
+//   * bias, skip, activation and the store of y from GEMM 2's accumulators.
+// fp32 operands and accumulation throughout.
+#include "fno_common.h"
+
+namespace fno {
+
+namespace {
+constexpr int kMlpWaves = 4;
+constexpr int kMlpThreads = 64 * kMlpWaves;
+constexpr int kMlpTP = 32 * kMlpWaves;   // points per tile
+constexpr int kMlpXS = kMlpTP;           // slab row stride (floats)
+// slab column of point c in row `row`: XOR-swizzled by 16 (row % 4) so the
+// four lane groups of an MFMA operand read (rows 4k + G) hit distinct banks
+__device__ __forceinline__ int slab_col(int row, int c) { return c ^ ((row & 3) << 4); }
+typedef float v4f __attribute__((ext_vector_type(4)));
+}  // namespace
+
+template <int CI, int CH, int CO>
+__global__ void __launch_bounds__(kMlpThreads) __attribute__((amdgpu_waves_per_eu(CI <= 64 ? 3 : 1)))
+k_channel_mlp(const float* x, const float* __restrict__ w1, const float* __restrict__ b1,
+              const float* __restrict__ w2, const float* __restrict__ b2, const float* xs,
+              const float* __restrict__ sw, const float* __restrict__ sb, float* y, int64_t P,
+              int64_t tiles_per_sample, int64_t tiles, int skip_kind, int act) {
+  static_assert(CI % 4 == 0 && CH % 16 == 0 && CO % 16 == 0, "channel multiples");
+  constexpr int KS1 = CI / 4, MT1 = CH / 16, MT2 = CO / 16;
+  constexpr int LPT = CI * kMlpTP / 4 / kMlpThreads;   // float4 slab loads per thread
+  static_assert(LPT >= 1 && CI * kMlpTP / 4 % kMlpThreads == 0, "slab split");
+  extern __shared__ float4 smem4[];
+  float* w1s = reinterpret_cast<float*>(smem4);   // [MT1][KS1][64] lane order
+  float* w2s = w1s + CH * CI;                     // [MT2][MT1][4][64] lane order
+  float* slab = w2s + CO * CH;                    // [CI][kMlpXS]
+  float* bos = slab + CI * kMlpXS;                // [CO] output bias (+ gate bias)
+  float* gws = bos + CO;                          // [CO] gate weight
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int G = lane >> 4, t = lane & 15;
+
+  for (int e = tid; e < CH * CI; e += kMlpThreads) {
+    const int l = e & 63, ks = (e >> 6) % KS1, m = (e >> 6) / KS1;
+    w1s[e] = w1[(16 * m + (l & 15)) * CI + 4 * ks + (l >> 4)];
+  }
+  for (int e = tid; e < CO * CH; e += kMlpThreads) {
+    const int l = e & 63, r = (e >> 6) & 3, m = ((e >> 8) % MT1), mo = (e >> 8) / MT1;
+    w2s[e] = w2[(16 * mo + (l & 15)) * CH + 16 * m + 4 * (l >> 4) + r];
+  }
+  for (int o = tid; o < CO; o += kMlpThreads) {
+    bos[o] = (b2 ? b2[o] : 0.f) + (skip_kind == FNO_SKIP_SOFT_GATING && sb ? sb[o] : 0.f);
+    gws[o] = skip_kind == FNO_SKIP_SOFT_GATING ? sw[o] : 1.f;
+  }
+  float bh[MT1][4];
+#pragma unroll
+  for (int m = 0; m < MT1; ++m)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) bh[m][r] = b1 ? b1[16 * m + 4 * G + r] : 0.f;
+  const bool has_skip = skip_kind != FNO_SKIP_NONE;
+  const bool gelu_out = act == FNO_ACT_GELU;
+
+  // slab of tile `tile` into registers: float4 q = tid + kMlpThreads j is row
+  // q / (TP/4), points 4 (q % (TP/4)) .. +3; points past P read as zero
+  float4 pre[LPT];
+  auto load_slab = [&](int64_t tile) __attribute__((always_inline)) {
+    const int64_t b = tile / tiles_per_sample;
+    const int64_t p0 = (tile % tiles_per_sample) * kMlpTP;
+    const float* xb = x + b * CI * P;
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) {
+      const int q = tid + kMlpThreads * j;
+      const int c = q / (kMlpTP / 4);
+      const int64_t p = p0 + 4 * (q % (kMlpTP / 4));
+      pre[j] = p < P ? *reinterpret_cast<const float4*>(xb + c * P + p) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+
+  int64_t tile = blockIdx.x;
+  if (tile < tiles) load_slab(tile);
+  for (; tile < tiles; tile += gridDim.x) {
+    __syncthreads();   // previous tile's slab reads done (and the weights staged)
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) {
+      const int q = tid + kMlpThreads * j;
+      const int row = q / (kMlpTP / 4);
+      *reinterpret_cast<float4*>(slab + row * kMlpXS + slab_col(row, 4 * (q % (kMlpTP / 4)))) = pre[j];
+    }
+    __syncthreads();
+    const int64_t b = tile / tiles_per_sample;
+    const int64_t p0 = (tile % tiles_per_sample) * kMlpTP;
+    if (tile + gridDim.x < tiles) load_slab(tile + gridDim.x);
+
+    // GEMM 1: h[16m + row][point] over the wave's 2 column tiles
+    v4f h[MT1][2];
+#pragma unroll
+    for (int m = 0; m < MT1; ++m) h[m][0] = h[m][1] = (v4f)0.f;
+    // rows 4 ks + G: the swizzle is 16 G for every ks
+    const float* bcol0 = slab + G * kMlpXS + slab_col(G, 32 * wave + t);
+    const float* bcol1 = slab + G * kMlpXS + slab_col(G, 32 * wave + 16 + t);
+#pragma unroll
+    for (int ks = 0; ks < KS1; ++ks) {
+      const float xb0 = bcol0[4 * ks * kMlpXS], xb1 = bcol1[4 * ks * kMlpXS];
+#pragma unroll
+      for (int m = 0; m < MT1; ++m) {
+        const float a = w1s[(m * KS1 + ks) * 64 + lane];
+        h[m][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, xb0, h[m][0], 0, 0, 0);
+        h[m][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, xb1, h[m][1], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < MT1; ++m)
+#pragma unroll
+      for (int n = 0; n < 2; ++n)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) h[m][n][r] = gelu_erf(h[m][n][r] + bh[m][r]);
+
+    // GEMM 2: k-step (m, r) contracts hidden row 16m + 4G + r of lane group G
+    v4f o[MT2][2];
+#pragma unroll
+    for (int mo = 0; mo < MT2; ++mo) o[mo][0] = o[mo][1] = (v4f)0.f;
+#pragma unroll
+    for (int m = 0; m < MT1; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int mo = 0; mo < MT2; ++mo) {
+          const float a = w2s[((mo * MT1 + m) * 4 + r) * 64 + lane];
+          o[mo][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, h[m][0][r], o[mo][0], 0, 0, 0);
+          o[mo][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, h[m][1][r], o[mo][1], 0, 0, 0);
+        }
+
+    // epilogue: output channel 16 mo + 4G + r, point p0 + 32 wave + 16 n + t
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      const int64_t p = p0 + 32 * wave + 16 * n + t;
+      if (p >= P) continue;
+#pragma unroll
+      for (int mo = 0; mo < MT2; ++mo)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int oc = 16 * mo + 4 * G + r;
+          const int64_t idx = (b * CO + oc) * P + p;
+          float v = o[mo][n][r] + bos[oc];
+          if (has_skip) v = fmaf(gws[oc], xs[idx], v);
+          if (gelu_out) v = gelu_erf(v);
+          y[idx] = v;
+        }
+    }
+  }
+}
+
+// --------------------------------------------------------------------- host
+template <int CI, int CH, int CO>
+static size_t mlp_lds_bytes() {
+  return (size_t)(CH * CI + CO * CH + CI * kMlpXS + 2 * CO) * sizeof(float);
+}
+
+bool channel_mlp_supported(int Ci, int Ch, int Co, int64_t P) {
+  if (P % 4 != 0) return false;
+  return (Ci == 64 && Ch == 32 && Co == 64) || (Ci == 32 && Ch == 16 && Co == 32) ||
+         (Ci == 128 && Ch == 64 && Co == 128);
+}
+
+template <int CI, int CH, int CO>
+static int launch_mlp(const float* x, const float* w1, const float* b1, const float* w2,
+                      const float* b2, const float* xs, const float* sw, const float* sb, float* y,
+                      int64_t B, int64_t P, int skip_kind, int act, hipStream_t st) {
+  const size_t lds = mlp_lds_bytes<CI, CH, CO>();
+  if (lds > 48 * 1024) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_channel_mlp<CI, CH, CO>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) {
+      set_error("channel MLP: %s", hipGetErrorString(e));
+      return FNO_ERR_HIP;
+    }
+  }
+  const int64_t tps = (P + kMlpTP - 1) / kMlpTP;
+  const int64_t tiles = B * tps;
+  // persistent grid: as many workgroups as fit the CUs at once
+  const int per_cu = (int)(160 * 1024 / lds) < 4 ? (int)(160 * 1024 / lds) : 4;
+  int64_t grid = (int64_t)256 * (per_cu > 0 ? per_cu : 1);
+  if (grid > tiles) grid = tiles;
+  hipLaunchKernelGGL((k_channel_mlp<CI, CH, CO>), dim3((unsigned)grid), dim3(kMlpThreads), lds, st,
+                     x, w1, b1, w2, b2, xs, sw, sb, y, P, tps, tiles, skip_kind, act);
+  return launch_status("k_channel_mlp");
+}
+
+int channel_mlp(const float* x, const float* w1, const float* b1, const float* w2, const float* b2,
+                const float* xs, const float* sw, const float* sb, float* y, int64_t B, int Ci,
+                int Ch, int Co, int64_t P, int skip_kind, int act, hipStream_t st) {
+  if (Ci == 64)
+    return launch_mlp<64, 32, 64>(x, w1, b1, w2, b2, xs, sw, sb, y, B, P, skip_kind, act, st);
+  if (Ci == 32)
+    return launch_mlp<32, 16, 32>(x, w1, b1, w2, b2, xs, sw, sb, y, B, P, skip_kind, act, st);
+  return launch_mlp<128, 64, 128>(x, w1, b1, w2, b2, xs, sw, sb, y, B, P, skip_kind, act, st);
+}
+
+}  // namespace fno

@@ -4,9 +4,11 @@ Post-activation forward (fno_block.py:327-381).  When the layer is
   SpectralConv (this package's) + linear / soft-gating (no bias) / identity /
   no skip, no norm, no stabilizer, GELU non-linearity, output size == input
 the spectral conv, bias, skip, add and first GELU run as ONE library call
-(fno_spectral_block_f32: fused 2D path or generic kernels).  Everything after
-it (channel MLP, its skip, second GELU) and every other configuration runs as
-torch ops around the HIP SpectralConv.
+(fno_spectral_block_f32: fused 2D path or generic kernels).  When the channel
+MLP is the default two-layer GELU MLP (no dropout) with a soft-gating /
+identity / no skip and the kernel covers its widths, the MLP, its skip and the
+second GELU run as a second call (fno_channel_mlp_f32).  Every other
+configuration runs as torch ops around the HIP SpectralConv.
 """
 from __future__ import annotations
 
@@ -17,9 +19,10 @@ import torch.nn.functional as F
 from torch import nn
 
 from . import _native as nat
+from . import functional as Fh
 from .channel_mlp import ChannelMLP
 from .skip_connections import Flattened1dConv, SoftGating, skip_connection
-from .spectral_convolution import SpectralConv
+from .spectral_convolution import SpectralConv, _attach
 from .utils import get_active_profiler, maybe_profile, validate_scaling_factor
 
 Number = Union[int, float]
@@ -207,10 +210,41 @@ class FNOBlocks(nn.Module):
             return self.forward_with_preactivation(x, index, output_shape)
         return self.forward_with_postactivation(x, index, output_shape)
 
+    def _fused_mlp(self, x, index, output_shape):
+        """(skip_kind, gate) when the channel MLP, its skip and the second
+        activation of this layer can run as one fno_channel_mlp_f32 call, else
+        None."""
+        if not self.use_channel_mlp or not x.is_cuda or x.dtype != torch.float32:
+            return None
+        if self.norm is not None or self.non_linearity is not F.gelu:
+            return None
+        conv = self.convs[index]
+        if output_shape is not None or getattr(conv, "resolution_scaling_factor", None) is not None:
+            return None
+        mlp = self.channel_mlp[index]
+        if (mlp.n_layers != 2 or mlp.non_linearity is not F.gelu or mlp.dropout is not None
+                or mlp.in_channels != self.out_channels):
+            return None
+        P = 1
+        for s in x.shape[2:]:
+            P *= s
+        if not Fh.channel_mlp_is_supported(mlp.in_channels, mlp.hidden_channels, mlp.out_channels, P):
+            return None
+        if self.channel_mlp_skips is None:
+            return nat.SKIP_NONE, None
+        sk = self.channel_mlp_skips[index]
+        if isinstance(sk, SoftGating):
+            return nat.SKIP_SOFT_GATING, sk
+        if isinstance(sk, nn.Identity) and self.in_channels == self.out_channels:
+            return nat.SKIP_IDENTITY, None
+        return None
+
     def forward_with_postactivation(self, x, index=0, output_shape=None):
         profiler = get_active_profiler()
         prefix = f"fno_blocks/{index}"
-        if self.use_channel_mlp and self.channel_mlp_skips is not None:
+        fused_mlp = self._fused_mlp(x, index, output_shape)
+        x_in = x
+        if self.use_channel_mlp and self.channel_mlp_skips is not None and fused_mlp is None:
             with maybe_profile(profiler, f"{prefix}/channel_mlp_skip", x.device):
                 x_skip_channel_mlp = self.channel_mlp_skips[index](x)
                 x_skip_channel_mlp = self.convs[index].transform(x_skip_channel_mlp,
@@ -234,6 +268,23 @@ class FNOBlocks(nn.Module):
             x = x_fno + x_skip_fno if self.fno_skips is not None else x_fno
             if act0:
                 x = self.non_linearity(x)
+        if fused_mlp is not None:
+            # channel MLP + its skip + the second activation in one kernel
+            kind, gate = fused_mlp
+            mlp = self.channel_mlp[index]
+            fc0, fc1 = mlp.fcs
+            with maybe_profile(profiler, f"{prefix}/channel_mlp", x.device):
+                y = Fh.channel_mlp(
+                    x.detach(), fc0.weight.detach(), None if fc0.bias is None else fc0.bias.detach(),
+                    fc1.weight.detach(), None if fc1.bias is None else fc1.bias.detach(), kind,
+                    x_in.detach() if kind != nat.SKIP_NONE else None,
+                    gate.weight.detach() if gate is not None else None,
+                    gate.bias.detach() if gate is not None and gate.bias is not None else None,
+                    nat.ACT_GELU if index < (self.n_layers - 1) else nat.ACT_NONE)
+            params = [x, x_in] + list(mlp.parameters())
+            if gate is not None:
+                params += list(gate.parameters())
+            return _attach(y, *params)
         if self.use_channel_mlp:
             with maybe_profile(profiler, f"{prefix}/channel_mlp", x.device):
                 x = self.channel_mlp[index](x)

@@ -142,6 +142,38 @@ def block_epilogue(spec: torch.Tensor, x: Optional[torch.Tensor], skip_kind: int
     return y
 
 
+def channel_mlp_is_supported(Ci: int, Ch: int, Co: int, P: int) -> bool:
+    return bool(nat.load().fno_channel_mlp_is_supported(Ci, Ch, Co, P))
+
+
+def channel_mlp(x: torch.Tensor, w1: torch.Tensor, b1: Optional[torch.Tensor], w2: torch.Tensor,
+                b2: Optional[torch.Tensor], skip_kind: int = nat.SKIP_NONE,
+                skip_x: Optional[torch.Tensor] = None, skip_weight: Optional[torch.Tensor] = None,
+                skip_bias: Optional[torch.Tensor] = None, act: int = nat.ACT_NONE,
+                out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """act(W2 gelu(W1 x + b1) + b2 + skip(skip_x)) over x [B, Ci, *S]
+    (ChannelMLP.forward with two layers, channel_mlp.py:82-119, plus the
+    channel-MLP skip and second activation of fno_block.py:363-379)."""
+    _require_gpu(x, w1, w2, skip_x)
+    lib = nat.load()
+    B, Ci, *S = x.shape
+    P = 1
+    for s in S:
+        P *= s
+    Ch, Co = w1.shape[0], w2.shape[0]
+    xx = _f32(x)
+    y = torch.empty((B, Co, *S), dtype=torch.float32, device=x.device) if out is None else out
+    sx = _f32(skip_x) if skip_x is not None else None
+    # flattened operands held in locals until the launch is enqueued
+    w1f, b1f, w2f, b2f, swf, sbf = (_f32(t.reshape(-1)) if t is not None else None
+                                    for t in (w1, b1, w2, b2, skip_weight, skip_bias))
+    nat.check(lib.fno_channel_mlp_f32(_ptr(xx), _ptr(w1f), _ptr(b1f), _ptr(w2f), _ptr(b2f), _ptr(sx),
+                                      _ptr(swf), _ptr(sbf), _ptr(y), B, Ci, Ch, Co, P, skip_kind,
+                                      act, _stream(x.device)),
+              "fno_channel_mlp_f32")
+    return y
+
+
 def spectral_block_is_fused(B, Ci, Co, sizes, modes, skip_kind) -> bool:
     lib = nat.load()
     return bool(lib.fno_spectral_block_is_fused(B, Ci, Co, len(sizes), nat.i32_array(sizes),

@@ -435,6 +435,59 @@ def test_block_epilogue_unaligned_views(cuda_device):
     assert rel_err(y, ref) <= TOL
 
 
+@pytest.mark.parametrize("C,P", [(32, 64), (64, 132), (64, 4096), (128, 260)])
+@pytest.mark.parametrize("skip,act", [("soft-gating", "gelu"), ("soft-gating-bias", "none"),
+                                      ("identity", "gelu"), ("none", "none")])
+def test_channel_mlp(C, P, skip, act, cuda_device):
+    """Fused channel MLP (two 1x1 convs, GELU between) + skip + activation
+    against the float64 oracle; P = 132 and 260 end in a partial tile."""
+    print(f"channel mlp C{C} P{P} {skip} {act}", flush=True)
+    g = torch.Generator().manual_seed(23)
+    B, Ch = 3, C // 2
+    x = torch.randn(B, C, P, generator=g)
+    xs = torch.randn(B, C, P, generator=g)
+    w1, b1 = torch.randn(Ch, C, 1, generator=g) / C ** 0.5, torch.randn(Ch, generator=g) * 0.1
+    w2, b2 = torch.randn(C, Ch, 1, generator=g) / Ch ** 0.5, torch.randn(C, generator=g) * 0.1
+    gw, gb = torch.rand(1, C, 1, generator=g) + 0.5, torch.randn(1, C, 1, generator=g) * 0.1
+    ref = R.channel_mlp(x.double(), [w1.double(), w2.double()], [b1.double(), b2.double()])
+    kind = nat.SKIP_NONE
+    if skip.startswith("soft-gating"):
+        kind = nat.SKIP_SOFT_GATING
+        ref = ref + R.soft_gating(xs.double(), gw.double(), gb.double() if skip.endswith("bias") else None)
+    elif skip == "identity":
+        kind = nat.SKIP_IDENTITY
+        ref = ref + xs.double()
+    if act == "gelu":
+        ref = R.gelu(ref)
+    d = lambda t: t.to(cuda_device)
+    with torch.no_grad():
+        y = Fh.channel_mlp(d(x), d(w1), d(b1), d(w2), d(b2), kind,
+                           d(xs) if kind != nat.SKIP_NONE else None,
+                           d(gw) if kind == nat.SKIP_SOFT_GATING else None,
+                           d(gb) if skip.endswith("bias") else None,
+                           nat.ACT_GELU if act == "gelu" else nat.ACT_NONE)
+    torch.cuda.synchronize()
+    assert rel_err(y, ref) <= TOL
+
+
+def test_channel_mlp_in_place(cuda_device):
+    """y written over x (the layout FNOBlocks may use) matches the out-of-place result."""
+    g = torch.Generator().manual_seed(24)
+    B, C, P = 2, 64, 1024
+    x = torch.randn(B, C, P, generator=g).to(cuda_device)
+    xs = torch.randn(B, C, P, generator=g).to(cuda_device)
+    w1 = (torch.randn(32, C, generator=g) / 8).to(cuda_device)
+    w2 = (torch.randn(C, 32, generator=g) / 6).to(cuda_device)
+    gw = (torch.rand(C, generator=g) + 0.5).to(cuda_device)
+    with torch.no_grad():
+        a = Fh.channel_mlp(x, w1, None, w2, None, nat.SKIP_SOFT_GATING, xs, gw, None, nat.ACT_GELU)
+        xc = x.clone()
+        b = Fh.channel_mlp(xc, w1, None, w2, None, nat.SKIP_SOFT_GATING, xs, gw, None, nat.ACT_GELU,
+                           out=xc)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
 def test_kernel_gelu_matches_exact_erf(cuda_device):
     """The kernels' erf GELU (Abramowitz & Stegun 7.1.28 form) against exact
     erf GELU in float64 over [-12, 12], through the C-ABI epilogue with no
