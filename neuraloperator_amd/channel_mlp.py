@@ -1,8 +1,16 @@
-"""Pointwise channel MLP (neuralop/layers/channel_mlp.py:136-249), torch ops."""
+"""Pointwise channel MLP (neuralop/layers/channel_mlp.py:82-119).
+
+The default two-layer GELU MLP runs as one fno_channel_mlp_f32 call on the GPU
+when the library covers its widths (the lifting, projection and block MLPs of
+FNO); other configurations run as torch ops."""
 from __future__ import annotations
 
+import torch
 import torch.nn.functional as F
 from torch import nn
+
+from . import _native as nat
+from . import functional as Fh
 
 
 class ChannelMLP(nn.Module):
@@ -27,7 +35,26 @@ class ChannelMLP(nn.Module):
             else:
                 self.fcs.append(nn.Conv1d(self.hidden_channels, self.hidden_channels, 1))
 
+    def _fusable(self, x):
+        if not x.is_cuda or x.dtype != torch.float32 or x.ndim < 3:
+            return False
+        if self.n_layers != 2 or self.non_linearity is not F.gelu or self.dropout is not None:
+            return False
+        P = 1
+        for s in x.shape[2:]:
+            P *= s
+        return Fh.channel_mlp_is_supported(self.in_channels, self.hidden_channels,
+                                           self.out_channels, P)
+
     def forward(self, x):
+        if self._fusable(x):
+            from .spectral_convolution import _attach
+            fc0, fc1 = self.fcs
+            y = Fh.channel_mlp(x.detach(), fc0.weight.detach(),
+                               None if fc0.bias is None else fc0.bias.detach(), fc1.weight.detach(),
+                               None if fc1.bias is None else fc1.bias.detach(), nat.SKIP_NONE, None,
+                               None, None, nat.ACT_NONE)
+            return _attach(y, x, *self.parameters())
         reshaped = False
         size = list(x.shape)
         if x.ndim > 3:

@@ -39,15 +39,16 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 }  // namespace
 
 template <int CI, int CH, int CO>
-__global__ void __launch_bounds__(kMlpThreads) __attribute__((amdgpu_waves_per_eu(CI <= 64 ? 3 : 1)))
+__global__ void __launch_bounds__(kMlpThreads) __attribute__((amdgpu_waves_per_eu(CI <= 64 ? 2 : 1)))
 k_channel_mlp(const float* x, const float* __restrict__ w1, const float* __restrict__ b1,
               const float* __restrict__ w2, const float* __restrict__ b2, const float* xs,
               const float* __restrict__ sw, const float* __restrict__ sb, float* y, int64_t P,
-              int64_t tiles_per_sample, int64_t tiles, int skip_kind, int act) {
+              int64_t tiles_per_sample, int64_t tiles, int ci, int co, int skip_kind, int act) {
   static_assert(CI % 4 == 0 && CH % 16 == 0 && CO % 16 == 0, "channel multiples");
   constexpr int KS1 = CI / 4, MT1 = CH / 16, MT2 = CO / 16;
-  constexpr int LPT = CI * kMlpTP / 4 / kMlpThreads;   // float4 slab loads per thread
-  static_assert(LPT >= 1 && CI * kMlpTP / 4 % kMlpThreads == 0, "slab split");
+  constexpr int NQ = CI * kMlpTP / 4;                  // float4s per slab
+  constexpr int LPT = (NQ + kMlpThreads - 1) / kMlpThreads;   // ... per thread
+  static_assert(NQ % kMlpThreads == 0 || NQ < kMlpThreads, "slab split");
   extern __shared__ float4 smem4[];
   float* w1s = reinterpret_cast<float*>(smem4);   // [MT1][KS1][64] lane order
   float* w2s = w1s + CH * CI;                     // [MT2][MT1][4][64] lane order
@@ -59,15 +60,18 @@ k_channel_mlp(const float* x, const float* __restrict__ w1, const float* __restr
 
   for (int e = tid; e < CH * CI; e += kMlpThreads) {
     const int l = e & 63, ks = (e >> 6) % KS1, m = (e >> 6) / KS1;
-    w1s[e] = w1[(16 * m + (l & 15)) * CI + 4 * ks + (l >> 4)];
+    const int k = 4 * ks + (l >> 4);
+    w1s[e] = k < ci ? w1[(16 * m + (l & 15)) * ci + k] : 0.f;
   }
   for (int e = tid; e < CO * CH; e += kMlpThreads) {
     const int l = e & 63, r = (e >> 6) & 3, m = ((e >> 8) % MT1), mo = (e >> 8) / MT1;
-    w2s[e] = w2[(16 * mo + (l & 15)) * CH + 16 * m + 4 * (l >> 4) + r];
+    const int oc = 16 * mo + (l & 15);
+    w2s[e] = oc < co ? w2[oc * CH + 16 * m + 4 * (l >> 4) + r] : 0.f;
   }
   for (int o = tid; o < CO; o += kMlpThreads) {
-    bos[o] = (b2 ? b2[o] : 0.f) + (skip_kind == FNO_SKIP_SOFT_GATING && sb ? sb[o] : 0.f);
-    gws[o] = skip_kind == FNO_SKIP_SOFT_GATING ? sw[o] : 1.f;
+    bos[o] = o >= co ? 0.f
+                     : (b2 ? b2[o] : 0.f) + (skip_kind == FNO_SKIP_SOFT_GATING && sb ? sb[o] : 0.f);
+    gws[o] = o < co && skip_kind == FNO_SKIP_SOFT_GATING ? sw[o] : 1.f;
   }
   float bh[MT1][4];
 #pragma unroll
@@ -83,13 +87,30 @@ k_channel_mlp(const float* x, const float* __restrict__ w1, const float* __restr
   auto load_slab = [&](int64_t tile) __attribute__((always_inline)) {
     const int64_t b = tile / tiles_per_sample;
     const int64_t p0 = (tile % tiles_per_sample) * kMlpTP;
-    const float* xb = x + b * CI * P;
+    const float* xb = x + b * ci * P;
 #pragma unroll
     for (int j = 0; j < LPT; ++j) {
       const int q = tid + kMlpThreads * j;
       const int c = q / (kMlpTP / 4);
       const int64_t p = p0 + 4 * (q % (kMlpTP / 4));
-      pre[j] = p < P ? *reinterpret_cast<const float4*>(xb + c * P + p) : make_float4(0.f, 0.f, 0.f, 0.f);
+      pre[j] = q < NQ && p < P && c < ci ? *reinterpret_cast<const float4*>(xb + c * P + p)
+                                         : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+
+  // skip input of the outputs this lane stores for tile `tile`
+  auto load_skip = [&](int64_t tile, float (&dst)[2][MT2][4]) __attribute__((always_inline)) {
+    const int64_t b = tile / tiles_per_sample;
+    const int64_t p0 = (tile % tiles_per_sample) * kMlpTP;
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      const int64_t p = p0 + 32 * wave + 16 * n + t;
+#pragma unroll
+      for (int mo = 0; mo < MT2; ++mo)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          dst[n][mo][r] = has_skip && p < P && 16 * mo + 4 * G + r < co
+                              ? xs[(b * co + 16 * mo + 4 * G + r) * P + p] : 0.f;
     }
   };
 
@@ -101,12 +122,16 @@ k_channel_mlp(const float* x, const float* __restrict__ w1, const float* __restr
     for (int j = 0; j < LPT; ++j) {
       const int q = tid + kMlpThreads * j;
       const int row = q / (kMlpTP / 4);
-      *reinterpret_cast<float4*>(slab + row * kMlpXS + slab_col(row, 4 * (q % (kMlpTP / 4)))) = pre[j];
+      if (q < NQ)
+        *reinterpret_cast<float4*>(slab + row * kMlpXS + slab_col(row, 4 * (q % (kMlpTP / 4)))) = pre[j];
     }
     __syncthreads();
     const int64_t b = tile / tiles_per_sample;
     const int64_t p0 = (tile % tiles_per_sample) * kMlpTP;
     if (tile + gridDim.x < tiles) load_slab(tile + gridDim.x);
+    // the skip input of this tile's outputs, in flight during the GEMMs
+    float sv[2][MT2][4];
+    load_skip(tile, sv);
 
     // GEMM 1: h[16m + row][point] over the wave's 2 column tiles
     v4f h[MT1][2];
@@ -157,9 +182,10 @@ k_channel_mlp(const float* x, const float* __restrict__ w1, const float* __restr
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int oc = 16 * mo + 4 * G + r;
-          const int64_t idx = (b * CO + oc) * P + p;
+          if (oc >= co) continue;
+          const int64_t idx = (b * co + oc) * P + p;
           float v = o[mo][n][r] + bos[oc];
-          if (has_skip) v = fmaf(gws[oc], xs[idx], v);
+          if (has_skip) v = fmaf(gws[oc], sv[n][mo][r], v);
           if (gelu_out) v = gelu_erf(v);
           y[idx] = v;
         }
@@ -173,16 +199,28 @@ static size_t mlp_lds_bytes() {
   return (size_t)(CH * CI + CO * CH + CI * kMlpXS + 2 * CO) * sizeof(float);
 }
 
+// (Ci, Ch, Co) -> kernel widths: Ci <= 4 runs padded to 4 input channels and
+// Co <= 16 padded to 16 outputs (the lifting 3 -> 2H -> H and projection
+// H -> 2H -> 1 MLPs of FNO); the block MLPs C -> C/2 -> C run at their widths
+static int mlp_variant(int Ci, int Ch, int Co) {
+  if (Ci == 64 && Ch == 32 && Co == 64) return 0;
+  if (Ci == 32 && Ch == 16 && Co == 32) return 1;
+  if (Ci == 128 && Ch == 64 && Co == 128) return 2;
+  if (Ci <= 4 && Ch == 128 && Co == 64) return 3;
+  if (Ci <= 4 && Ch == 64 && Co == 32) return 4;
+  if (Ci == 64 && Ch == 128 && Co <= 16) return 5;
+  if (Ci == 32 && Ch == 64 && Co <= 16) return 6;
+  return -1;
+}
+
 bool channel_mlp_supported(int Ci, int Ch, int Co, int64_t P) {
-  if (P % 4 != 0) return false;
-  return (Ci == 64 && Ch == 32 && Co == 64) || (Ci == 32 && Ch == 16 && Co == 32) ||
-         (Ci == 128 && Ch == 64 && Co == 128);
+  return P % 4 == 0 && mlp_variant(Ci, Ch, Co) >= 0;
 }
 
 template <int CI, int CH, int CO>
 static int launch_mlp(const float* x, const float* w1, const float* b1, const float* w2,
                       const float* b2, const float* xs, const float* sw, const float* sb, float* y,
-                      int64_t B, int64_t P, int skip_kind, int act, hipStream_t st) {
+                      int64_t B, int64_t P, int ci, int co, int skip_kind, int act, hipStream_t st) {
   const size_t lds = mlp_lds_bytes<CI, CH, CO>();
   if (lds > 48 * 1024) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_channel_mlp<CI, CH, CO>),
@@ -194,23 +232,44 @@ static int launch_mlp(const float* x, const float* w1, const float* b1, const fl
   }
   const int64_t tps = (P + kMlpTP - 1) / kMlpTP;
   const int64_t tiles = B * tps;
-  // persistent grid: as many workgroups as fit the CUs at once
-  const int per_cu = (int)(160 * 1024 / lds) < 4 ? (int)(160 * 1024 / lds) : 4;
-  int64_t grid = (int64_t)256 * (per_cu > 0 ? per_cu : 1);
+  // persistent grid: exactly as many workgroups as are resident at once (a
+  // second round of workgroups would each carry a full share of the tiles)
+  static int per_cu = 0;
+  if (per_cu == 0) {
+    int n = 0;
+    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+        &n, reinterpret_cast<const void*>(&k_channel_mlp<CI, CH, CO>), kMlpThreads, lds);
+    per_cu = (e == hipSuccess && n > 0) ? n : 1;
+  }
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+    cus = 256;
+  int64_t grid = (int64_t)cus * per_cu;
   if (grid > tiles) grid = tiles;
   hipLaunchKernelGGL((k_channel_mlp<CI, CH, CO>), dim3((unsigned)grid), dim3(kMlpThreads), lds, st,
-                     x, w1, b1, w2, b2, xs, sw, sb, y, P, tps, tiles, skip_kind, act);
+                     x, w1, b1, w2, b2, xs, sw, sb, y, P, tps, tiles, ci, co, skip_kind, act);
   return launch_status("k_channel_mlp");
 }
 
 int channel_mlp(const float* x, const float* w1, const float* b1, const float* w2, const float* b2,
                 const float* xs, const float* sw, const float* sb, float* y, int64_t B, int Ci,
                 int Ch, int Co, int64_t P, int skip_kind, int act, hipStream_t st) {
-  if (Ci == 64)
-    return launch_mlp<64, 32, 64>(x, w1, b1, w2, b2, xs, sw, sb, y, B, P, skip_kind, act, st);
-  if (Ci == 32)
-    return launch_mlp<32, 16, 32>(x, w1, b1, w2, b2, xs, sw, sb, y, B, P, skip_kind, act, st);
-  return launch_mlp<128, 64, 128>(x, w1, b1, w2, b2, xs, sw, sb, y, B, P, skip_kind, act, st);
+#define FNO_MLP(ci_, ch_, co_)                                                                     \
+  launch_mlp<ci_, ch_, co_>(x, w1, b1, w2, b2, xs, sw, sb, y, B, P, Ci, Co, skip_kind, act, st)
+  switch (mlp_variant(Ci, Ch, Co)) {
+    case 0: return FNO_MLP(64, 32, 64);
+    case 1: return FNO_MLP(32, 16, 32);
+    case 2: return FNO_MLP(128, 64, 128);
+    case 3: return FNO_MLP(4, 128, 64);
+    case 4: return FNO_MLP(4, 64, 32);
+    case 5: return FNO_MLP(64, 128, 16);
+    case 6: return FNO_MLP(32, 64, 16);
+    default: break;
+  }
+#undef FNO_MLP
+  set_error("channel MLP %d -> %d -> %d is not covered by the kernel", Ci, Ch, Co);
+  return FNO_ERR_UNSUPPORTED;
 }
 
 }  // namespace fno

@@ -470,6 +470,27 @@ def test_channel_mlp(C, P, skip, act, cuda_device):
     assert rel_err(y, ref) <= TOL
 
 
+@pytest.mark.parametrize("Ci,Ch,Co,P", [(3, 128, 64, 512), (3, 64, 32, 132), (4, 128, 64, 64),
+                                        (64, 128, 1, 260), (32, 64, 1, 1024), (64, 128, 16, 128)])
+def test_channel_mlp_lifting_projection(Ci, Ch, Co, P, cuda_device):
+    """The FNO lifting (3 -> 2H -> H) and projection (H -> 2H -> 1) MLPs
+    through the kernel's padded input / output widths."""
+    print(f"channel mlp {Ci}->{Ch}->{Co} P{P}", flush=True)
+    g = torch.Generator().manual_seed(25)
+    B = 2
+    x = torch.randn(B, Ci, P, generator=g)
+    w1, b1 = torch.randn(Ch, Ci, 1, generator=g) / Ci ** 0.5, torch.randn(Ch, generator=g) * 0.1
+    w2, b2 = torch.randn(Co, Ch, 1, generator=g) / Ch ** 0.5, torch.randn(Co, generator=g) * 0.1
+    ref = R.channel_mlp(x.double(), [w1.double(), w2.double()], [b1.double(), b2.double()])
+    d = lambda t: t.to(cuda_device)
+    assert Fh.channel_mlp_is_supported(Ci, Ch, Co, P)
+    with torch.no_grad():
+        y = Fh.channel_mlp(d(x), d(w1), d(b1), d(w2), d(b2))
+    torch.cuda.synchronize()
+    assert list(y.shape) == [B, Co, P]
+    assert rel_err(y, ref) <= TOL
+
+
 def test_channel_mlp_in_place(cuda_device):
     """y written over x (the layout FNOBlocks may use) matches the out-of-place result."""
     g = torch.Generator().manual_seed(24)
