@@ -38,13 +38,16 @@ __device__ __forceinline__ int slab_col(int row, int c) { return c ^ ((row & 3) 
 typedef float v4f __attribute__((ext_vector_type(4)));
 }  // namespace
 
-template <int CI, int CH, int CO>
+// TWO = false: a single 1x1 layer y = act(W1 x + b2 + skip) (CH == CO), the
+// linear skip of the block epilogue with the spectral term as identity skip.
+template <int CI, int CH, int CO, bool TWO>
 __global__ void __launch_bounds__(kMlpThreads) __attribute__((amdgpu_waves_per_eu(CI <= 64 ? 2 : 1)))
 k_channel_mlp(const float* x, const float* __restrict__ w1, const float* __restrict__ b1,
               const float* __restrict__ w2, const float* __restrict__ b2, const float* xs,
               const float* __restrict__ sw, const float* __restrict__ sb, float* y, int64_t P,
               int64_t tiles_per_sample, int64_t tiles, int ci, int co, int skip_kind, int act) {
   static_assert(CI % 4 == 0 && CH % 16 == 0 && CO % 16 == 0, "channel multiples");
+  static_assert(TWO || CH == CO, "one layer: CH == CO");
   constexpr int KS1 = CI / 4, MT1 = CH / 16, MT2 = CO / 16;
   constexpr int NQ = CI * kMlpTP / 4;                  // float4s per slab
   constexpr int LPT = (NQ + kMlpThreads - 1) / kMlpThreads;   // ... per thread
@@ -52,7 +55,7 @@ k_channel_mlp(const float* x, const float* __restrict__ w1, const float* __restr
   extern __shared__ float4 smem4[];
   float* w1s = reinterpret_cast<float*>(smem4);   // [MT1][KS1][64] lane order
   float* w2s = w1s + CH * CI;                     // [MT2][MT1][4][64] lane order
-  float* slab = w2s + CO * CH;                    // [CI][kMlpXS]
+  float* slab = w2s + (TWO ? CO * CH : 0);        // [CI][kMlpXS]
   float* bos = slab + CI * kMlpXS;                // [CO] output bias (+ gate bias)
   float* gws = bos + CO;                          // [CO] gate weight
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -63,7 +66,7 @@ k_channel_mlp(const float* x, const float* __restrict__ w1, const float* __restr
     const int k = 4 * ks + (l >> 4);
     w1s[e] = k < ci ? w1[(16 * m + (l & 15)) * ci + k] : 0.f;
   }
-  for (int e = tid; e < CO * CH; e += kMlpThreads) {
+  for (int e = tid; TWO && e < CO * CH; e += kMlpThreads) {
     const int l = e & 63, r = (e >> 6) & 3, m = ((e >> 8) % MT1), mo = (e >> 8) / MT1;
     const int oc = 16 * mo + (l & 15);
     w2s[e] = oc < co ? w2[oc * CH + 16 * m + 4 * (l >> 4) + r] : 0.f;
@@ -150,27 +153,35 @@ k_channel_mlp(const float* x, const float* __restrict__ w1, const float* __restr
         h[m][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, xb1, h[m][1], 0, 0, 0);
       }
     }
-#pragma unroll
-    for (int m = 0; m < MT1; ++m)
-#pragma unroll
-      for (int n = 0; n < 2; ++n)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) h[m][n][r] = gelu_erf(h[m][n][r] + bh[m][r]);
-
-    // GEMM 2: k-step (m, r) contracts hidden row 16m + 4G + r of lane group G
     v4f o[MT2][2];
+    if constexpr (TWO) {
 #pragma unroll
-    for (int mo = 0; mo < MT2; ++mo) o[mo][0] = o[mo][1] = (v4f)0.f;
+      for (int m = 0; m < MT1; ++m)
 #pragma unroll
-    for (int m = 0; m < MT1; ++m)
+        for (int n = 0; n < 2; ++n)
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
+          for (int r = 0; r < 4; ++r) h[m][n][r] = gelu_erf(h[m][n][r] + bh[m][r]);
+
+      // GEMM 2: k-step (m, r) contracts hidden row 16m + 4G + r of lane group G
 #pragma unroll
-        for (int mo = 0; mo < MT2; ++mo) {
-          const float a = w2s[((mo * MT1 + m) * 4 + r) * 64 + lane];
-          o[mo][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, h[m][0][r], o[mo][0], 0, 0, 0);
-          o[mo][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, h[m][1][r], o[mo][1], 0, 0, 0);
-        }
+      for (int mo = 0; mo < MT2; ++mo) o[mo][0] = o[mo][1] = (v4f)0.f;
+#pragma unroll
+      for (int m = 0; m < MT1; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int mo = 0; mo < MT2; ++mo) {
+            const float a = w2s[((mo * MT1 + m) * 4 + r) * 64 + lane];
+            o[mo][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, h[m][0][r], o[mo][0], 0, 0, 0);
+            o[mo][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, h[m][1][r], o[mo][1], 0, 0, 0);
+          }
+    } else {
+#pragma unroll
+      for (int mo = 0; mo < MT2; ++mo) {
+        o[mo][0] = h[mo][0];
+        o[mo][1] = h[mo][1];
+      }
+    }
 
     // epilogue: output channel 16 mo + 4G + r, point p0 + 32 wave + 16 n + t
 #pragma unroll
@@ -194,9 +205,9 @@ k_channel_mlp(const float* x, const float* __restrict__ w1, const float* __restr
 }
 
 // --------------------------------------------------------------------- host
-template <int CI, int CH, int CO>
+template <int CI, int CH, int CO, bool TWO>
 static size_t mlp_lds_bytes() {
-  return (size_t)(CH * CI + CO * CH + CI * kMlpXS + 2 * CO) * sizeof(float);
+  return (size_t)(CH * CI + (TWO ? CO * CH : 0) + CI * kMlpXS + 2 * CO) * sizeof(float);
 }
 
 // (Ci, Ch, Co) -> kernel widths: Ci <= 4 runs padded to 4 input channels and
@@ -217,13 +228,13 @@ bool channel_mlp_supported(int Ci, int Ch, int Co, int64_t P) {
   return P % 4 == 0 && mlp_variant(Ci, Ch, Co) >= 0;
 }
 
-template <int CI, int CH, int CO>
+template <int CI, int CH, int CO, bool TWO = true>
 static int launch_mlp(const float* x, const float* w1, const float* b1, const float* w2,
                       const float* b2, const float* xs, const float* sw, const float* sb, float* y,
                       int64_t B, int64_t P, int ci, int co, int skip_kind, int act, hipStream_t st) {
-  const size_t lds = mlp_lds_bytes<CI, CH, CO>();
+  const size_t lds = mlp_lds_bytes<CI, CH, CO, TWO>();
   if (lds > 48 * 1024) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_channel_mlp<CI, CH, CO>),
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_channel_mlp<CI, CH, CO, TWO>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) {
       set_error("channel MLP: %s", hipGetErrorString(e));
@@ -238,7 +249,7 @@ static int launch_mlp(const float* x, const float* w1, const float* b1, const fl
   if (per_cu == 0) {
     int n = 0;
     const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-        &n, reinterpret_cast<const void*>(&k_channel_mlp<CI, CH, CO>), kMlpThreads, lds);
+        &n, reinterpret_cast<const void*>(&k_channel_mlp<CI, CH, CO, TWO>), kMlpThreads, lds);
     per_cu = (e == hipSuccess && n > 0) ? n : 1;
   }
   int dev = 0, cus = 0;
@@ -247,7 +258,7 @@ static int launch_mlp(const float* x, const float* w1, const float* b1, const fl
     cus = 256;
   int64_t grid = (int64_t)cus * per_cu;
   if (grid > tiles) grid = tiles;
-  hipLaunchKernelGGL((k_channel_mlp<CI, CH, CO>), dim3((unsigned)grid), dim3(kMlpThreads), lds, st,
+  hipLaunchKernelGGL((k_channel_mlp<CI, CH, CO, TWO>), dim3((unsigned)grid), dim3(kMlpThreads), lds, st,
                      x, w1, b1, w2, b2, xs, sw, sb, y, P, tps, tiles, ci, co, skip_kind, act);
   return launch_status("k_channel_mlp");
 }
@@ -270,6 +281,23 @@ int channel_mlp(const float* x, const float* w1, const float* b1, const float* w
 #undef FNO_MLP
   set_error("channel MLP %d -> %d -> %d is not covered by the kernel", Ci, Ch, Co);
   return FNO_ERR_UNSUPPORTED;
+}
+
+// Linear block skip on MFMA: y = act(Ws x + spec); spec may alias y
+bool skip_gemm_supported(int Ci, int Co, int64_t P, const void* x) {
+  return P % 4 == 0 && Ci == Co && (Ci == 32 || Ci == 64 || Ci == 128) &&
+         reinterpret_cast<uintptr_t>(x) % 16 == 0;
+}
+
+int skip_gemm(const float* x, const float* ws, const float* spec, float* y, int64_t B, int Ci,
+              int Co, int64_t P, int act, hipStream_t st) {
+#define FNO_SKIPG(c)                                                                               \
+  launch_mlp<c, c, c, false>(x, ws, nullptr, nullptr, nullptr, spec, nullptr, nullptr, y, B, P, Ci, \
+                             Co, FNO_SKIP_IDENTITY, act, st)
+  if (Ci == 32) return FNO_SKIPG(32);
+  if (Ci == 64) return FNO_SKIPG(64);
+  return FNO_SKIPG(128);
+#undef FNO_SKIPG
 }
 
 }  // namespace fno

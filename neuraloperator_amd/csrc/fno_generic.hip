@@ -76,6 +76,9 @@ static constexpr int kThreads = 256;
 __global__ void __launch_bounds__(kThreads)
 k_r2c_direct(const float* __restrict__ x, float2* __restrict__ out, int64_t rows, int N, int m,
              int rows_per_block, float scale) {
+  // a (row, bin) task is summed by 16 lanes over n = lane, lane + 16, ...
+  // and reduced across them
+  constexpr int L = 16;
   extern __shared__ float smem[];
   float2* tw = reinterpret_cast<float2*>(smem);
   float* xs = reinterpret_cast<float*>(tw + N);
@@ -85,20 +88,33 @@ k_r2c_direct(const float* __restrict__ x, float2* __restrict__ out, int64_t rows
   const float* xg = x + r0 * N;
   for (int t = threadIdx.x; t < nr * N; t += blockDim.x) xs[t] = xg[t];
   __syncthreads();
-  for (int task = threadIdx.x; task < nr * m; task += blockDim.x) {
-    const int rr = task / m, j = task - (task / m) * m;
+  const int sub = threadIdx.x % L;
+  // every lane runs the same number of passes so the shuffles stay converged
+  const int passes = (nr * m + kThreads / L - 1) / (kThreads / L);
+  for (int pass = 0; pass < passes; ++pass) {
+    const int task = pass * (kThreads / L) + threadIdx.x / L;
+    const bool live = task < nr * m;
+    const int rr = live ? task / m : 0, j = live ? task % m : 0;
     const float* xr = xs + rr * N;
     float re = 0.f, im = 0.f;
-    int idx = 0;
-    for (int n = 0; n < N; ++n) {
-      const float2 w = tw[idx];
-      const float v = xr[n];
-      re = fmaf(v, w.x, re);
-      im = fmaf(-v, w.y, im);
-      idx += j;
-      if (idx >= N) idx -= N;
+    if (live) {
+      int idx = (int)(((int64_t)j * sub) % N);
+      const int step = (int)(((int64_t)j * L) % N);
+      for (int n = sub; n < N; n += L) {
+        const float2 w = tw[idx];
+        const float v = xr[n];
+        re = fmaf(v, w.x, re);
+        im = fmaf(-v, w.y, im);
+        idx += step;
+        if (idx >= N) idx -= N;
+      }
     }
-    out[(r0 + rr) * m + j] = make_float2(re * scale, im * scale);
+#pragma unroll
+    for (int off = L / 2; off > 0; off >>= 1) {
+      re += __shfl_xor(re, off, L);
+      im += __shfl_xor(im, off, L);
+    }
+    if (live && sub == 0) out[(r0 + rr) * m + j] = make_float2(re * scale, im * scale);
   }
 }
 
@@ -293,10 +309,13 @@ k_epilogue(const float* spec, const float* __restrict__ x, const float* __restri
   const int b = blockIdx.z;
   const int on = min(OT, Co - o0);
   const bool linear = skip_kind == FNO_SKIP_LINEAR;
+  constexpr int KB = 8;   // input channels per batch of x loads
+  const int CiP = (Ci + KB - 1) / KB * KB;
   if (linear) {
-    for (int e = threadIdx.x; e < Ci * OT; e += kThreads) {
+    // rows Ci .. CiP-1 are zero so whole batches need no guard
+    for (int e = threadIdx.x; e < CiP * OT; e += kThreads) {
       const int i = e / OT, c = e % OT;
-      wT[e] = c < on ? ws[(int64_t)(o0 + c) * Ci + i] : 0.f;
+      wT[e] = (c < on && i < Ci) ? ws[(int64_t)(o0 + c) * Ci + i] : 0.f;
     }
     __syncthreads();
   }
@@ -307,21 +326,31 @@ k_epilogue(const float* spec, const float* __restrict__ x, const float* __restri
   for (int c = 0; c < OT; ++c) acc[c] = (vpp)0.f;
   if (linear) {
     const float* xb = x + (int64_t)b * Ci * P + p;
-    // x of the next input channel is in flight while this one is used
-    vpp vn = *reinterpret_cast<const vpp*>(xb);
-#pragma unroll 2
-    for (int i = 0; i < Ci; ++i) {
-      const vpp v = vn;
-      if (i + 1 < Ci) vn = *reinterpret_cast<const vpp*>(xb + (int64_t)(i + 1) * P);
-      const float4* w4 = reinterpret_cast<const float4*>(wT + i * OT);
+    // batches of KB input channels; the next batch is in flight while this
+    // one is used
+    vpp cur[KB], nxt[KB];
+    auto load = [&](int i0, vpp (&d)[KB]) __attribute__((always_inline)) {
 #pragma unroll
-      for (int c4 = 0; c4 < OT / 4; ++c4) {
-        const float4 w = w4[c4];
-        acc[4 * c4 + 0] += w.x * v;
-        acc[4 * c4 + 1] += w.y * v;
-        acc[4 * c4 + 2] += w.z * v;
-        acc[4 * c4 + 3] += w.w * v;
+      for (int k = 0; k < KB; ++k)
+        d[k] = i0 + k < Ci ? *reinterpret_cast<const vpp*>(xb + (int64_t)(i0 + k) * P) : (vpp)0.f;
+    };
+    load(0, cur);
+    for (int i0 = 0; i0 < Ci; i0 += KB) {
+      if (i0 + KB < Ci) load(i0 + KB, nxt);
+#pragma unroll
+      for (int k = 0; k < KB; ++k) {
+        const float4* w4 = reinterpret_cast<const float4*>(wT + (i0 + k) * OT);
+#pragma unroll
+        for (int c4 = 0; c4 < OT / 4; ++c4) {
+          const float4 w = w4[c4];
+          acc[4 * c4 + 0] += w.x * cur[k];
+          acc[4 * c4 + 1] += w.y * cur[k];
+          acc[4 * c4 + 2] += w.z * cur[k];
+          acc[4 * c4 + 3] += w.w * cur[k];
+        }
       }
+#pragma unroll
+      for (int k = 0; k < KB; ++k) cur[k] = nxt[k];
     }
   } else if (skip_kind == FNO_SKIP_SOFT_GATING || skip_kind == FNO_SKIP_IDENTITY) {
 #pragma unroll
@@ -420,6 +449,9 @@ int rfft_window(const float* x, float2* xhat, int64_t planes, int32_t ndim, cons
       int rpb = (int)((48 * 1024 - 8 * N) / (4 * N));
       if (rpb < 1) rpb = 1;
       if (rpb > 64) rpb = 64;
+      // one pass of 16 tasks per workgroup: more workgroups for few bins
+      const int rfill = (16 + m - 1) / m;
+      if (rpb > rfill) rpb = rfill;
       const size_t lds = (size_t)N * 8 + (size_t)rpb * N * 4;
       const int64_t blocks = (rows + rpb - 1) / rpb;
       hipLaunchKernelGGL(k_r2c_direct, dim3((unsigned)blocks), dim3(kThreads), lds, st, x, dst,
@@ -556,7 +588,7 @@ static int launch_epilogue(const float* spec, const float* x, const float* ws, f
                            int Ci, int Co, int64_t P, int skip_kind, int act, hipStream_t st) {
   const int64_t per = (int64_t)kThreads * PP;
   dim3 grid((unsigned)((P + per - 1) / per), (unsigned)((Co + OT - 1) / OT), (unsigned)B);
-  const size_t lds = skip_kind == FNO_SKIP_LINEAR ? (size_t)Ci * OT * sizeof(float) : 0;
+  const size_t lds = skip_kind == FNO_SKIP_LINEAR ? (size_t)((Ci + 7) / 8 * 8) * OT * sizeof(float) : 0;
   if (lds > 160 * 1024) {
     set_error("block epilogue: %d input channels exceed the staged skip weights", Ci);
     return FNO_ERR_UNSUPPORTED;
@@ -574,22 +606,29 @@ static int launch_epilogue(const float* spec, const float* x, const float* ws, f
   return launch_status("k_epilogue");
 }
 
+bool skip_gemm_supported(int Ci, int Co, int64_t P, const void* x);
+int skip_gemm(const float* x, const float* ws, const float* spec, float* y, int64_t B, int Ci,
+              int Co, int64_t P, int act, hipStream_t st);
+
 int block_epilogue(const float* spec, const float* x, const float* ws, float* y, int B, int Ci,
                    int Co, int64_t P, int skip_kind, int act, hipStream_t st) {
+  // the linear skip as an MFMA GEMM with the spectral term added in its epilogue
+  if (skip_kind == FNO_SKIP_LINEAR && skip_gemm_supported(Ci, Co, P, x))
+    return skip_gemm(x, ws, spec, y, B, Ci, Co, P, act, st);
   // vector access needs every (b, c) row to start on the vector boundary
   const uintptr_t addr = reinterpret_cast<uintptr_t>(spec) | reinterpret_cast<uintptr_t>(x) |
                          reinterpret_cast<uintptr_t>(y);
   const bool v4 = P % 4 == 0 && addr % 16 == 0, v2 = P % 2 == 0 && addr % 8 == 0;
   // wide output blocks while their staged weights stay small
   const bool wide_ok = skip_kind != FNO_SKIP_LINEAR || (size_t)Ci * 64 * sizeof(float) <= 64 * 1024;
+  // OT x PP = 64 accumulators per thread
   if (Co <= 16 || !wide_ok)
     return v4 ? launch_epilogue<16, 4>(spec, x, ws, y, B, Ci, Co, P, skip_kind, act, st)
               : launch_epilogue<16, 1>(spec, x, ws, y, B, Ci, Co, P, skip_kind, act, st);
   if (Co <= 32)
-    return v4 ? launch_epilogue<32, 4>(spec, x, ws, y, B, Ci, Co, P, skip_kind, act, st)
+    return v2 ? launch_epilogue<32, 2>(spec, x, ws, y, B, Ci, Co, P, skip_kind, act, st)
               : launch_epilogue<32, 1>(spec, x, ws, y, B, Ci, Co, P, skip_kind, act, st);
-  return v2 ? launch_epilogue<64, 2>(spec, x, ws, y, B, Ci, Co, P, skip_kind, act, st)
-            : launch_epilogue<64, 1>(spec, x, ws, y, B, Ci, Co, P, skip_kind, act, st);
+  return launch_epilogue<64, 1>(spec, x, ws, y, B, Ci, Co, P, skip_kind, act, st);
 }
 
 int validate_window(int32_t ndim, const int32_t* sizes, const int32_t* modes) {

@@ -387,12 +387,15 @@ def test_errors_raise(cuda_device):
 
 @pytest.mark.parametrize("Ci,Co,S", [(3, 4, (8, 9)), (32, 32, (16, 16, 16)), (20, 24, (37,)),
                                       (64, 48, (10, 12)), (64, 64, (33, 7)), (32, 96, (64,)),
-                                      (300, 40, (16,))])
+                                      (300, 40, (16,)), (64, 64, (12, 12)), (128, 128, (10, 10)),
+                                      (32, 32, (6, 10))])
 @pytest.mark.parametrize("skip", ["linear", "soft-gating", "identity", "none"])
 def test_block_epilogue(Ci, Co, S, skip, cuda_device):
     """Generic epilogue act(spec + skip(x)) against float64 torch: channel
     counts on and off the 16/32/64 output blocks, point counts with and without
-    4- and 2-point vectors, more input channels than the wide blocks stage."""
+    4- and 2-point vectors, more input channels than the wide blocks stage;
+    square 32/64/128-channel linear skips over P % 4 == 0 points take the MFMA
+    skip GEMM (P = 144, 100 and 60 end in a partial tile)."""
     if skip in ("soft-gating", "identity") and Ci != Co:
         Ci = Co
     g = torch.Generator().manual_seed(21)
