@@ -1100,7 +1100,9 @@ static int launch_epi_r(const float* x, const float2* z, const float* skip_w, co
   const size_t lds = epi_r_lds_bytes(CO);
   int rc = allow_lds(k_row_epilogue_r<W, CO, CI, NB>, lds);
   if (rc) return rc;
-  const int TR = 16;
+  // 16 rows per workgroup, or 8 when that leaves fewer than two workgroups
+  // per CU (two share a CU by LDS and registers)
+  const int TR = ((int64_t)B * (H / 16) >= 512) ? 16 : 8;
   const int64_t grid = (int64_t)B * (H / TR);
   hipLaunchKernelGGL((k_row_epilogue_r<W, CO, CI, NB>), dim3((unsigned)grid), dim3(CO * 4), lds,
                      st, x, z, skip_w, bias, y, H, TR, m2h, skip_kind, act, inv_scale);
