@@ -61,9 +61,11 @@ k_contract_mfma(const float2* __restrict__ X, const float2* __restrict__ W, floa
   auto Wbuf = [&](int d) __attribute__((always_inline)) { return smem + d * BUF; };
   auto Xbuf = [&](int d) __attribute__((always_inline)) { return smem + d * BUF + IC * KB * MS; };
   // pair (mode block, channel half) placement: the halves of block p run on
-  // one XCD (workgroup id mod 8), 8 ids apart
+  // one XCD (workgroup id mod 8), 8 ids apart, and each XCD takes a
+  // contiguous range of mode blocks, so the 128-byte lines that two adjacent
+  // blocks' mode runs share are fetched into one L2
   const int bid = blockIdx.x;
-  const int p = (bid / 16) * 8 + (bid % 8);
+  const int p = (bid % 8) * ((nblocks + 7) / 8) + bid / 16;
   const int half = (bid / 8) % 2;
   if (p >= nblocks) return;
   const int64_t k0 = (int64_t)p * KB;
