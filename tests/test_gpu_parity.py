@@ -362,6 +362,29 @@ def test_fno_forward_matches_oracle(hidden, H, W, nm, cuda_device):
     assert rel_err(y, ref) <= TOL
 
 
+def test_fno_c3_shape_bf16_input(cuda_device):
+    """The 4-layer FNO of the bf16 configuration (hidden 64, n_modes (64,64),
+    256^2, lifting 3 -> 128 -> 64, channel MLP + soft-gating, projection
+    64 -> 128 -> 1) on bf16 inputs, two samples, against the float64 oracle
+    on the same bf16-rounded input: within the configuration's 2e-2, and
+    within the fp32 bound since every stage computes in fp32."""
+    print("fno c3 shape B2 bf16 input", flush=True)
+    torch.manual_seed(16)
+    model = na.FNO((64, 64), in_channels=1, out_channels=1, hidden_channels=64, n_layers=4).to(cuda_device)
+    with torch.no_grad():
+        for sk in model.fno_blocks.channel_mlp_skips:
+            sk.weight.uniform_(0.5, 1.5)
+    x = gaussian_random_field((2, 1, 256, 256), seed=17).to(torch.bfloat16)
+    with torch.no_grad():
+        y = model(x.to(cuda_device).float())
+    params = {"lifting": _mlp(model.lifting), "projection": _mlp(model.projection),
+              "layers": [_layer_params(model.fno_blocks, i) for i in range(4)]}
+    ref = R.fno_forward(x.double(), params)
+    err = rel_err(y, ref)
+    assert err <= 2e-2
+    assert err <= TOL
+
+
 def test_deterministic(cuda_device):
     torch.manual_seed(11)
     conv = na.SpectralConv(64, 64, (64, 64)).to(cuda_device)
