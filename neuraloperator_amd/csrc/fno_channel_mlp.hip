@@ -35,6 +35,9 @@ constexpr int kMlpXS = kMlpTP;           // slab row stride (floats)
 // slab column of point c in row `row`: XOR-swizzled by 16 (row % 4) so the
 // four lane groups of an MFMA operand read (rows 4k + G) hit distinct banks
 __device__ __forceinline__ int slab_col(int row, int c) { return c ^ ((row & 3) << 4); }
+// output tile column: rows 16 mo + 4 G + r are written by lane group G, so
+// the swizzle follows G = (row / 4) % 4
+__device__ __forceinline__ int out_col(int row, int c) { return c ^ (((row >> 2) & 3) << 4); }
 typedef float v4f __attribute__((ext_vector_type(4)));
 }  // namespace
 
@@ -48,6 +51,11 @@ k_channel_mlp(const float* x, const float* __restrict__ w1, const float* __restr
               int64_t tiles_per_sample, int64_t tiles, int ci, int co, int skip_kind, int act) {
   static_assert(CI % 4 == 0 && CH % 16 == 0 && CO % 16 == 0, "channel multiples");
   static_assert(TWO || CH == CO, "one layer: CH == CO");
+  // outputs go back through the slab (as [CO][TP]) for 16-byte stores when
+  // they fit in it
+  constexpr bool STAGE = CO <= CI;
+  constexpr int NQO = CO * kMlpTP / 4;                // float4s per output tile
+  constexpr int LPO = (NQO + kMlpThreads - 1) / kMlpThreads;
   constexpr int KS1 = CI / 4, MT1 = CH / 16, MT2 = CO / 16;
   constexpr int NQ = CI * kMlpTP / 4;                  // float4s per slab
   constexpr int LPT = (NQ + kMlpThreads - 1) / kMlpThreads;   // ... per thread
@@ -134,7 +142,20 @@ k_channel_mlp(const float* x, const float* __restrict__ w1, const float* __restr
     if (tile + gridDim.x < tiles) load_slab(tile + gridDim.x);
     // the skip input of this tile's outputs, in flight during the GEMMs
     float sv[2][MT2][4];
-    load_skip(tile, sv);
+    float4 svq[LPO];
+    if constexpr (STAGE) {
+#pragma unroll
+      for (int j = 0; j < LPO; ++j) {
+        const int q = tid + kMlpThreads * j;
+        const int c = q / (kMlpTP / 4);
+        const int64_t p = p0 + 4 * (q % (kMlpTP / 4));
+        svq[j] = has_skip && q < NQO && c < co && p < P
+                     ? *reinterpret_cast<const float4*>(xs + (b * co + c) * P + p)
+                     : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    } else {
+      load_skip(tile, sv);
+    }
 
     // GEMM 1: h[16m + row][point] over the wave's 2 column tiles
     v4f h[MT1][2];
@@ -183,6 +204,44 @@ k_channel_mlp(const float* x, const float* __restrict__ w1, const float* __restr
       }
     }
 
+    if constexpr (STAGE) {
+      // every wave is past GEMM 1: the slab becomes the [CO][TP] output tile
+      __syncthreads();
+#pragma unroll
+      for (int n = 0; n < 2; ++n)
+#pragma unroll
+        for (int mo = 0; mo < MT2; ++mo)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = 16 * mo + 4 * G + r;
+            slab[row * kMlpXS + out_col(row, 32 * wave + 16 * n + t)] = o[mo][n][r];
+          }
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < LPO; ++j) {
+        const int q = tid + kMlpThreads * j;
+        const int c = q / (kMlpTP / 4);
+        const int64_t p = p0 + 4 * (q % (kMlpTP / 4));
+        if (q >= NQO || c >= co || p >= P) continue;
+        float4 v = *reinterpret_cast<const float4*>(slab + c * kMlpXS + out_col(c, 4 * (q % (kMlpTP / 4))));
+        const float bb = bos[c], gg = gws[c];
+        v.x += bb; v.y += bb; v.z += bb; v.w += bb;
+        if (has_skip) {
+          v.x = fmaf(gg, svq[j].x, v.x);
+          v.y = fmaf(gg, svq[j].y, v.y);
+          v.z = fmaf(gg, svq[j].z, v.z);
+          v.w = fmaf(gg, svq[j].w, v.w);
+        }
+        if (gelu_out) {
+          v.x = gelu_erf(v.x);
+          v.y = gelu_erf(v.y);
+          v.z = gelu_erf(v.z);
+          v.w = gelu_erf(v.w);
+        }
+        *reinterpret_cast<float4*>(y + (b * co + c) * P + p) = v;
+      }
+      continue;
+    }
     // epilogue: output channel 16 mo + 4G + r, point p0 + 32 wave + 16 n + t
 #pragma unroll
     for (int n = 0; n < 2; ++n) {
