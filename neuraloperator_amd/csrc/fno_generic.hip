@@ -265,6 +265,32 @@ k_contract_dense(const float2* __restrict__ X, const float2* __restrict__ W, flo
       if (b0 + a < B && o0 + c < Co) Y[((int64_t)(b0 + a) * Co + o0 + c) * M + k] = acc[a][c];
 }
 
+// Small contractions (few modes): 16 lanes per output y[b, o, k], each
+// summing every 16th input channel, reduced across the lanes; outputs are
+// ordered k fastest, then o, then b.
+__global__ void __launch_bounds__(kThreads)
+k_contract_small(const float2* __restrict__ X, const float2* __restrict__ W, float2* __restrict__ Y,
+                 int B, int Ci, int Co, int64_t M, int64_t sWi, int64_t sWo, int64_t sWk) {
+  constexpr int L = 16;
+  const int64_t out = ((int64_t)blockIdx.x * kThreads + threadIdx.x) / L;
+  const int sub = threadIdx.x % L;
+  const bool live = out < (int64_t)B * Co * M;
+  const int64_t k = live ? out % M : 0;
+  const int o = live ? (int)((out / M) % Co) : 0;
+  const int b = live ? (int)(out / (M * Co)) : 0;
+  float2 acc = make_float2(0.f, 0.f);
+  if (live) {
+    for (int i = sub; i < Ci; i += L)
+      cfma(acc, X[((int64_t)b * Ci + i) * M + k], W[(int64_t)i * sWi + (int64_t)o * sWo + k * sWk]);
+  }
+#pragma unroll
+  for (int off = L / 2; off > 0; off >>= 1) {
+    acc.x += __shfl_xor(acc.x, off, L);
+    acc.y += __shfl_xor(acc.y, off, L);
+  }
+  if (live && sub == 0) Y[((int64_t)b * Co + o) * M + k] = acc;
+}
+
 // y[b, i, k] = x[b, i, k] * w[i, k]
 __global__ void __launch_bounds__(kThreads)
 k_contract_separable(const float2* __restrict__ X, const float2* __restrict__ W,
@@ -557,6 +583,15 @@ int contract_mfma(const float2* X, const float2* W, float2* Y, int B, int Ci, in
 
 int contract_dense(const float2* X, const float2* W, float2* Y, int B, int Ci, int Co, int64_t M,
                    int64_t sWi, int64_t sWo, int64_t sWk, hipStream_t st) {
+  // few modes: the MFMA kernel's grid (a workgroup per 8+ modes and 32
+  // output channels) would leave most CUs idle; spread the outputs instead
+  const int64_t outs = (int64_t)B * Co * M;
+  if (M <= 64 && outs <= (int64_t(1) << 20)) {
+    const int64_t blocks = (outs * 16 + kThreads - 1) / kThreads;
+    hipLaunchKernelGGL(k_contract_small, dim3((unsigned)blocks), dim3(kThreads), 0, st, X, W, Y, B,
+                       Ci, Co, M, sWi, sWo, sWk);
+    return launch_status("k_contract_small");
+  }
   if (contract_mfma_supported(B, Ci, Co, M, sWi, sWo, sWk))
     return contract_mfma(X, W, Y, B, Ci, Co, M, st);
   constexpr int TB = 4, TO = 8;
