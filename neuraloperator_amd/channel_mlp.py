@@ -38,6 +38,9 @@ class ChannelMLP(nn.Module):
     def _fusable(self, x):
         if not x.is_cuda or x.dtype != torch.float32 or x.ndim < 3:
             return False
+        if torch.is_grad_enabled() and (x.requires_grad or
+                                        any(p.requires_grad for p in self.parameters())):
+            return False   # torch ops carry the gradients
         if self.n_layers != 2 or self.non_linearity is not F.gelu or self.dropout is not None:
             return False
         P = 1

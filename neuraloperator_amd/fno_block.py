@@ -28,6 +28,11 @@ from .utils import get_active_profiler, maybe_profile, validate_scaling_factor
 Number = Union[int, float]
 
 
+def _needs_grad(module: nn.Module, x: torch.Tensor) -> bool:
+    return torch.is_grad_enabled() and (x.requires_grad or
+                                        any(p.requires_grad for p in module.parameters()))
+
+
 class InstanceNorm(nn.Module):
     """Instance norm over all spatial dims (neuralop normalization_layers)."""
 
@@ -196,6 +201,8 @@ class FNOBlocks(nn.Module):
         conv = self.convs[index]
         if not isinstance(conv, SpectralConv) or not x.is_cuda:
             return False
+        if _needs_grad(self, x):
+            return False   # the composed path carries the gradients
         if self.norm is not None or self.stabilizer is not None or self.preactivation:
             return False
         if self.non_linearity is not F.gelu:
@@ -215,6 +222,8 @@ class FNOBlocks(nn.Module):
         activation of this layer can run as one fno_channel_mlp_f32 call, else
         None."""
         if not self.use_channel_mlp or not x.is_cuda or x.dtype != torch.float32:
+            return None
+        if _needs_grad(self, x):
             return None
         if self.norm is not None or self.non_linearity is not F.gelu:
             return None

@@ -13,7 +13,12 @@ CP / TT weights are reconstructed (torch ops on the weight only) and then
 contracted densely; the result is the same mathematics as the reference's
 factor-wise einsums (spectral_convolution.py:55-73, :106-132).
 
-Autograd: the HIP path is forward-only.  Calling backward through it raises.
+Autograd: when gradients are required (training), the forward runs as
+_SpectralConvFn, whose backward is built from the same library calls (window
+transforms under the dual norm and the dense contraction) for output size ==
+input size and non-separable weights; a factorized weight gets its gradient
+through the torch reconstruction of its dense window.  Other configurations
+raise on backward.
 """
 from __future__ import annotations
 
@@ -79,6 +84,67 @@ class _NoGradThroughHip(torch.autograd.Function):
     def backward(ctx, *grads):
         raise NotImplementedError(
             "backward of the HIP spectral path is not implemented (forward-only build)")
+
+
+_DUAL_NORM = {"forward": "backward", "backward": "forward", "ortho": "ortho"}
+
+
+def _hermitian_weights(m_last: int, n_last: int, ndim: int, device) -> torch.Tensor:
+    """c_k of the real inverse transform along the last axis: 1 for bin 0 and
+    the Nyquist bin, 2 for the bins that stand for a conjugate pair."""
+    c = torch.full((m_last,), 2.0, device=device)
+    c[0] = 1.0
+    if n_last % 2 == 0 and n_last // 2 < m_last:
+        c[n_last // 2] = 1.0
+    return c.view(*([1] * (ndim + 1)), m_last)
+
+
+class _SpectralConvFn(torch.autograd.Function):
+    """Dense spectral convolution y = s_i I(W . s_f F(x)) + bias with the
+    gradients of SpectralConv.forward (spectral_convolution.py:417-570), for
+    output size == input size.  With F the window of the forward transform
+    (bins e^{-i phi_k(n)}) and I the real inverse (y = sum_k c_k Re(Y_k
+    e^{i phi_k(n)}), c_k = 2 for bins that stand for a conjugate pair):
+
+        gY = s_i c_k . F_unscaled(gy)      gX = gY . conj(W)^T
+        gW = conj(X)^T . gY               gx = s_f Re(sum_k gX_k e^{i phi_k})
+                                              = s_f I_unscaled(gX / c_k)
+
+    so both transforms are the library's own window transforms under the dual
+    norm (forward <-> backward scaling), and both contractions its dense
+    mode-wise contraction."""
+
+    @staticmethod
+    def forward(ctx, x, w, bias, kept, fft_norm):
+        sizes = list(x.shape[2:])
+        b = bias.reshape(-1) if bias is not None else None
+        y = Fh.spectral_block(x, w, b, kept, nat.SKIP_NONE, None, nat.ACT_NONE, fft_norm)
+        ctx.save_for_backward(x, w)
+        ctx.kept, ctx.fft_norm, ctx.sizes = list(kept), fft_norm, sizes
+        ctx.bias_shape = None if bias is None else bias.shape
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        x, w = ctx.saved_tensors
+        kept, norm, sizes = ctx.kept, ctx.fft_norm, ctx.sizes
+        gy = gy.contiguous().float()
+        dual = _DUAL_NORM[norm]
+        c = _hermitian_weights(kept[-1], sizes[-1], len(sizes), gy.device)
+        gY = Fh.rfft_window(gy, kept, dual) * c
+        gx = gw = gb = None
+        if ctx.needs_input_grad[0]:
+            wt = w.conj().transpose(0, 1).contiguous()              # [Co, Ci, *m]
+            gX = Fh.contract_dense(gY, wt)                          # [B, Ci, *m]
+            gx = Fh.irfft_window(gX / c, sizes, sizes, None, dual, False)
+        if ctx.needs_input_grad[1]:
+            X = Fh.rfft_window(x, kept, norm)                       # [B, Ci, *m]
+            xt = X.conj().transpose(0, 1).contiguous()              # [Ci, B, *m]
+            gw = Fh.contract_dense(xt, gY.contiguous())             # [Ci, Co, *m]
+        if ctx.bias_shape is not None and ctx.needs_input_grad[2]:
+            dims = [0] + list(range(2, gy.ndim))
+            gb = gy.sum(dim=dims).reshape(ctx.bias_shape)
+        return gx, gw, gb, None, None
 
 
 def _attach(y, *params):
@@ -232,7 +298,24 @@ class SpectralConv(BaseSpectralConv):
         profiler = get_active_profiler()
         name = getattr(self, "profile_prefix", "spectral_conv")
         with maybe_profile(profiler, name, x.device):
+            if torch.is_grad_enabled() and (x.requires_grad or
+                                            any(p.requires_grad for p in self.parameters())):
+                return self._forward_autograd(x, output_shape)
             return self._forward_hip(x, output_shape)
+
+    def _forward_autograd(self, x, output_shape=None):
+        """Forward with gradients for x, the weight (through its dense window,
+        so factorized weights get theirs through the reconstruction) and the
+        bias; output size == input size, non-separable."""
+        sizes = list(x.shape[2:])
+        out_sizes = self.output_sizes(sizes, output_shape)
+        if out_sizes != sizes or self.separable:
+            raise NotImplementedError(
+                "gradients of the HIP spectral path cover output size == input size, "
+                "non-separable weights")
+        kept, sl = self.window(sizes)
+        w = self.dense_window_weight(sl)
+        return _SpectralConvFn.apply(x, w, self.bias, kept, self.fft_norm)
 
     def _forward_hip(self, x, output_shape=None, skip_kind=nat.SKIP_NONE, skip_weight=None,
                      act=nat.ACT_NONE):

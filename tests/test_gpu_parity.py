@@ -385,6 +385,102 @@ def test_fno_c3_shape_bf16_input(cuda_device):
     assert err <= TOL
 
 
+@pytest.mark.parametrize("dim,sizes,nm,norm", [
+    (2, (16, 20), (8, 10), "forward"),
+    (2, (64, 128), (16, 16), "backward"),     # fused forward path
+    (2, (12, 9), (6, 5), "ortho"),            # odd last axis (no Nyquist bin)
+    (2, (16, 16), (16, 16), "forward"),       # every bin, Nyquist kept
+    (1, (64,), (20,), "forward"),
+    (3, (8, 12, 16), (4, 6, 8), "backward"),
+])
+def test_spectral_conv_gradients(dim, sizes, nm, norm, cuda_device):
+    """x, weight and bias gradients of SpectralConv against torch autograd
+    through the float64 oracle, for a random output cotangent."""
+    print(f"grad dim{dim} {sizes} {nm} {norm}", flush=True)
+    torch.manual_seed(18)
+    Ci, Co, B = 3, 4, 2
+    conv = na.SpectralConv(Ci, Co, nm, fft_norm=norm).to(cuda_device)
+    with torch.no_grad():
+        conv.bias.normal_()
+    x = torch.randn(B, Ci, *sizes)
+    g = torch.randn(B, Co, *sizes)
+    xg = x.to(cuda_device).requires_grad_(True)
+    (conv(xg) * g.to(cuda_device)).sum().backward()
+    xd = x.double().requires_grad_(True)
+    wd = conv.weight.to_tensor().detach().cpu().to(torch.complex128).requires_grad_(True)
+    bd = conv.bias.detach().cpu().double().requires_grad_(True)
+    yd = R.spectral_conv_forward(xd, wd, bd, conv.n_modes, conv.max_n_modes, fft_norm=norm)
+    (yd * g.double()).sum().backward()
+    assert rel_err(xg.grad, xd.grad) <= TOL
+    assert rel_err(torch.view_as_real(conv.weight.to_tensor().grad), torch.view_as_real(wd.grad)) <= TOL
+    assert rel_err(conv.bias.grad, bd.grad) <= TOL
+
+
+def test_tucker_spectral_conv_gradients(cuda_device):
+    """A Tucker weight gets its gradients through the reconstruction of its
+    dense window: compare the reconstructed-weight gradient path against the
+    oracle for x and against a dense module carrying the same weight."""
+    torch.manual_seed(19)
+    conv = na.SpectralConv(4, 4, (8, 8), factorization="Tucker", rank=0.5,
+                           implementation="factorized").to(cuda_device)
+    x = torch.randn(2, 4, 16, 16)
+    g = torch.randn(2, 4, 16, 16)
+    xg = x.to(cuda_device).requires_grad_(True)
+    (conv(xg) * g.to(cuda_device)).sum().backward()
+    for p in conv.weight.parameters():
+        assert p.grad is not None and torch.isfinite(p.grad).all()
+    xd = x.double().requires_grad_(True)
+    wd = conv.weight.to_tensor().detach().cpu().to(torch.complex128)
+    yd = R.spectral_conv_forward(xd, wd, conv.bias.detach().cpu().double(), conv.n_modes,
+                                 conv.max_n_modes)
+    (yd * g.double()).sum().backward()
+    assert rel_err(xg.grad, xd.grad) <= TOL
+
+
+def test_fno_backward_gradients(cuda_device):
+    """FNO training step: every parameter gets a gradient (reference
+    test_fno.py:73-84), and the lifting, spectral, skip and channel-MLP
+    gradients match torch autograd through the float64 oracle."""
+    torch.manual_seed(20)
+    model = na.FNO((8, 8), in_channels=1, out_channels=1, hidden_channels=8, n_layers=2).to(cuda_device)
+    with torch.no_grad():
+        for sk in model.fno_blocks.channel_mlp_skips:
+            sk.weight.uniform_(0.5, 1.5)
+        for conv in model.fno_blocks.convs:
+            conv.bias.normal_()
+    x = gaussian_random_field((2, 1, 16, 16), seed=21)
+    out = model(x.to(cuda_device))
+    out.pow(2).sum().backward()
+    for name, p in model.named_parameters():
+        assert p.grad is not None, name
+    blocks = model.fno_blocks
+    d = lambda t: t.detach().cpu().double().requires_grad_(True)
+    lift = {"weights": [d(f.weight) for f in model.lifting.fcs], "biases": [d(f.bias) for f in model.lifting.fcs]}
+    proj = {"weights": [d(f.weight) for f in model.projection.fcs],
+            "biases": [d(f.bias) for f in model.projection.fcs]}
+    layers = []
+    for i in range(2):
+        conv = blocks.convs[i]
+        layers.append({
+            "conv": dict(weight=conv.weight.to_tensor().detach().cpu().to(torch.complex128).requires_grad_(True),
+                         bias=d(conv.bias), n_modes=conv.n_modes, max_n_modes=conv.max_n_modes),
+            "fno_skip": {"type": "linear", "w": d(blocks.fno_skips[i].conv.weight[:, :, 0])},
+            "mlp": {"weights": [d(f.weight) for f in blocks.channel_mlp[i].fcs],
+                    "biases": [d(f.bias) for f in blocks.channel_mlp[i].fcs]},
+            "mlp_skip": {"type": "soft-gating", "w": d(blocks.channel_mlp_skips[i].weight)}})
+    ref = R.fno_forward(x.double(), {"lifting": lift, "projection": proj, "layers": layers})
+    ref.pow(2).sum().backward()
+    assert rel_err(model.lifting.fcs[0].weight.grad, lift["weights"][0].grad) <= TOL
+    assert rel_err(model.projection.fcs[1].weight.grad, proj["weights"][1].grad) <= TOL
+    for i in range(2):
+        assert rel_err(torch.view_as_real(blocks.convs[i].weight.to_tensor().grad),
+                       torch.view_as_real(layers[i]["conv"]["weight"].grad)) <= TOL
+        assert rel_err(blocks.convs[i].bias.grad, layers[i]["conv"]["bias"].grad) <= TOL
+        assert rel_err(blocks.fno_skips[i].conv.weight.grad[:, :, 0], layers[i]["fno_skip"]["w"].grad) <= TOL
+        assert rel_err(blocks.channel_mlp[i].fcs[0].weight.grad, layers[i]["mlp"]["weights"][0].grad) <= TOL
+        assert rel_err(blocks.channel_mlp_skips[i].weight.grad, layers[i]["mlp_skip"]["w"].grad) <= TOL
+
+
 def test_deterministic(cuda_device):
     torch.manual_seed(11)
     conv = na.SpectralConv(64, 64, (64, 64)).to(cuda_device)
@@ -403,9 +499,12 @@ def test_errors_raise(cuda_device):
         conv(torch.randn(1, 3, 8, 8))            # CPU input
     with pytest.raises(RuntimeError, match="4096"):
         conv(torch.randn(1, 3, 8, 8200, device=cuda_device))
+    # gradients cover output size == input size, non-separable weights
+    x = torch.randn(1, 3, 8, 8, device=cuda_device, requires_grad=True)
     with pytest.raises(NotImplementedError):
-        x = torch.randn(1, 3, 8, 8, device=cuda_device, requires_grad=True)
-        conv(x).sum().backward()
+        conv(x, output_shape=(16, 16))
+    with pytest.raises(NotImplementedError):
+        na.SpectralConv(3, 3, (4, 4), separable=True).to(cuda_device)(x)
 
 
 @pytest.mark.parametrize("Ci,Co,S", [(3, 4, (8, 9)), (32, 32, (16, 16, 16)), (20, 24, (37,)),
