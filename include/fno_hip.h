@@ -121,6 +121,31 @@ size_t fno_irfft_window_workspace_bytes(int64_t planes, int32_t ndim, const int3
                                         const int32_t* modes);
 
 /*
+ * Complex-data window transforms (SpectralConv(complex_data=True)).  Replace
+ * torch.fft.fftn + fftshift + window slice and the inverse scatter +
+ * ifftshift + ifftn of spectral_convolution.py:436-449, :500-538.
+ *   x     complex64 [planes, N_1..N_ndim]
+ *   xhat  complex64 [planes, m_1..m_ndim], m_d <= N_d: on every axis but the
+ *         last, window index j holds frequency j - m/2; on the last axis it
+ *         holds frequency j - N/2 (j of the fftshift-ed order) when ndim > 1
+ *         and frequency j when ndim == 1
+ *   fno_ifft_window_c64: window -> complex64 y [batch, channels, out sizes];
+ *         on the last axis window entry j is frequency j (no ifftshift
+ *         there); bias (float32 [channels] or NULL) is added to the real part
+ */
+int fno_fft_window_c64(const void* x, void* xhat, int64_t planes, int32_t ndim,
+                       const int32_t* sizes, const int32_t* modes, int32_t norm, void* workspace,
+                       size_t workspace_bytes, void* stream);
+size_t fno_fft_window_workspace_bytes(int64_t planes, int32_t ndim, const int32_t* sizes,
+                                      const int32_t* modes);
+int fno_ifft_window_c64(const void* yhat, const float* bias, void* y, int64_t batch,
+                        int32_t channels, int32_t ndim, const int32_t* in_sizes,
+                        const int32_t* out_sizes, const int32_t* modes, int32_t norm,
+                        void* workspace, size_t workspace_bytes, void* stream);
+size_t fno_ifft_window_workspace_bytes(int64_t planes, int32_t ndim, const int32_t* out_sizes,
+                                       const int32_t* modes);
+
+/*
  * Block epilogue: y = act(spec + skip(x)).  Replaces the skip, add and first
  * activation of FNOBlocks.forward_with_postactivation, fno_block.py:331-361,
  * with the skips of skip_connections.py:88-130.  spec may alias y.

@@ -52,6 +52,12 @@ _SIGNATURES = {
     "fno_channel_mlp_f32": (_c_i32, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                                      _c_i64, _c_i32, _c_i32, _c_i32, _c_i64, _c_i32, _c_i32, _c_vp]),
     "fno_channel_mlp_is_supported": (_c_i32, [_c_i32, _c_i32, _c_i32, _c_i64]),
+    "fno_fft_window_c64": (_c_i32, [_c_vp, _c_vp, _c_i64, _c_i32, _c_i32p, _c_i32p, _c_i32, _c_vp,
+                                    _c_size, _c_vp]),
+    "fno_fft_window_workspace_bytes": (_c_size, [_c_i64, _c_i32, _c_i32p, _c_i32p]),
+    "fno_ifft_window_c64": (_c_i32, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i32, _c_i32, _c_i32p, _c_i32p,
+                                     _c_i32p, _c_i32, _c_vp, _c_size, _c_vp]),
+    "fno_ifft_window_workspace_bytes": (_c_size, [_c_i64, _c_i32, _c_i32p, _c_i32p]),
 }
 
 _lib = None

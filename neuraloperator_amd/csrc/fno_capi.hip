@@ -10,6 +10,16 @@ int validate_window(int32_t ndim, const int32_t* sizes, const int32_t* modes);
 size_t rfft_window_ws(int64_t planes, int32_t ndim, const int32_t* sizes, const int32_t* modes);
 size_t irfft_window_ws(int64_t planes, int32_t ndim, const int32_t* out_sizes,
                        const int32_t* modes);
+int fft_window_c2c(const float2* x, float2* xhat, int64_t planes, int32_t ndim,
+                   const int32_t* sizes, const int32_t* modes, int32_t norm, void* ws,
+                   size_t ws_bytes, hipStream_t st);
+size_t fft_window_c2c_ws(int64_t planes, int32_t ndim, const int32_t* sizes, const int32_t* modes);
+int ifft_window_c2c(const float2* yhat, const float* bias, float2* y, int64_t batch,
+                    int32_t channels, int32_t ndim, const int32_t* in_sizes,
+                    const int32_t* out_sizes, const int32_t* modes, int32_t norm, void* ws,
+                    size_t ws_bytes, hipStream_t st);
+size_t ifft_window_c2c_ws(int64_t planes, int32_t ndim, const int32_t* out_sizes,
+                          const int32_t* modes);
 int rfft_window(const float* x, float2* xhat, int64_t planes, int32_t ndim, const int32_t* sizes,
                 const int32_t* modes, int32_t norm, void* ws, size_t ws_bytes, hipStream_t st);
 int irfft_window(const float2* yhat, const float* bias, float* y, int64_t batch, int32_t channels,
@@ -198,6 +208,66 @@ int fno_irfft_window_f32(const void* yhat, const float* bias, float* y, int64_t 
   return irfft_window(reinterpret_cast<const float2*>(yhat), bias, y, batch, channels, ndim,
                       in_sizes, out_sizes, modes, norm, enforce_hermitian, workspace,
                       workspace_bytes, reinterpret_cast<hipStream_t>(stream));
+}
+
+// complex data: every axis keeps at most its own length in modes
+static int validate_complex_window(int32_t ndim, const int32_t* sizes, const int32_t* modes) {
+  FNO_CHECK_ARG(ndim >= 1 && ndim <= 3, "ndim must be 1..3 (got %d)", ndim);
+  FNO_CHECK_ARG(sizes && modes, "sizes/modes must not be NULL");
+  for (int d = 0; d < ndim; ++d) {
+    FNO_CHECK_ARG(sizes[d] >= 1 && sizes[d] <= 4096, "size[%d]=%d outside [1, 4096]", d, sizes[d]);
+    FNO_CHECK_ARG(modes[d] >= 1 && modes[d] <= sizes[d], "modes[%d]=%d outside [1, %d]", d,
+                  modes[d], sizes[d]);
+  }
+  return FNO_OK;
+}
+
+size_t fno_fft_window_workspace_bytes(int64_t planes, int32_t ndim, const int32_t* sizes,
+                                      const int32_t* modes) {
+  if (!sizes || !modes || ndim < 1 || ndim > 3) return 0;
+  return fft_window_c2c_ws(planes, ndim, sizes, modes);
+}
+
+int fno_fft_window_c64(const void* x, void* xhat, int64_t planes, int32_t ndim,
+                       const int32_t* sizes, const int32_t* modes, int32_t norm, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  clear_error();
+  FNO_CHECK_ARG(x && xhat, "x/xhat must not be NULL");
+  FNO_CHECK_ARG(planes >= 1, "planes must be positive");
+  int rc = validate_complex_window(ndim, sizes, modes);
+  if (rc) return rc;
+  rc = check_norm(norm);
+  if (rc) return rc;
+  return fft_window_c2c(reinterpret_cast<const float2*>(x), reinterpret_cast<float2*>(xhat), planes,
+                        ndim, sizes, modes, norm, workspace, workspace_bytes,
+                        reinterpret_cast<hipStream_t>(stream));
+}
+
+size_t fno_ifft_window_workspace_bytes(int64_t planes, int32_t ndim, const int32_t* out_sizes,
+                                       const int32_t* modes) {
+  if (!out_sizes || !modes || ndim < 1 || ndim > 3) return 0;
+  return ifft_window_c2c_ws(planes, ndim, out_sizes, modes);
+}
+
+int fno_ifft_window_c64(const void* yhat, const float* bias, void* y, int64_t batch,
+                        int32_t channels, int32_t ndim, const int32_t* in_sizes,
+                        const int32_t* out_sizes, const int32_t* modes, int32_t norm,
+                        void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  FNO_CHECK_ARG(yhat && y, "yhat/y must not be NULL");
+  FNO_CHECK_ARG(batch >= 1 && channels >= 1, "batch/channels must be positive");
+  int rc = validate_complex_window(ndim, in_sizes, modes);
+  if (rc) return rc;
+  FNO_CHECK_ARG(out_sizes, "out_sizes must not be NULL");
+  for (int d = 0; d < ndim; ++d) {
+    FNO_CHECK_ARG(out_sizes[d] >= 1 && out_sizes[d] <= 4096, "out size %d outside [1, 4096]",
+                  out_sizes[d]);
+  }
+  rc = check_norm(norm);
+  if (rc) return rc;
+  return ifft_window_c2c(reinterpret_cast<const float2*>(yhat), bias, reinterpret_cast<float2*>(y),
+                         batch, channels, ndim, in_sizes, out_sizes, modes, norm, workspace,
+                         workspace_bytes, reinterpret_cast<hipStream_t>(stream));
 }
 
 int fno_block_epilogue_f32(const float* spec, const float* x, const float* skip_weight, float* y,

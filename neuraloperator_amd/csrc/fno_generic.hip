@@ -118,11 +118,12 @@ k_r2c_direct(const float* __restrict__ x, float2* __restrict__ out, int64_t rows
   }
 }
 
-// Middle axis, complex -> complex, centred window:
-//   out[o, j, q] = s * sum_n in[o, n, q] exp(-2 pi i (j - m/2) n / N)
+// Non-last axis (or the last axis of complex data), complex -> complex: window
+// entry j is frequency j + off (off = -m/2: the centred window):
+//   out[o, j, q] = s * sum_n in[o, n, q] exp(-2 pi i (j + off) n / N)
 __global__ void __launch_bounds__(kThreads)
 k_c2c_fwd_direct(const float2* __restrict__ in, float2* __restrict__ out, int64_t outer, int N,
-                 int64_t inner, int m, float scale) {
+                 int64_t inner, int m, int off, float scale) {
   extern __shared__ float smem[];
   float2* tw = reinterpret_cast<float2*>(smem);
   for (int t = threadIdx.x; t < N; t += blockDim.x) tw[t] = twiddle_any(t, N);
@@ -134,7 +135,7 @@ k_c2c_fwd_direct(const float2* __restrict__ in, float2* __restrict__ out, int64_
     const int64_t t2 = task / inner;
     const int j = (int)(t2 % m);
     const int64_t o = t2 / m;
-    int step = (j - m / 2) % N;
+    int step = (j + off) % N;
     if (step < 0) step += N;
     const float2* src = in + o * (int64_t)N * inner + q;
     float2 acc = make_float2(0.f, 0.f);
@@ -152,12 +153,12 @@ k_c2c_fwd_direct(const float2* __restrict__ in, float2* __restrict__ out, int64_
 }
 
 // ---------------------------------------------------------------- inverse axes
-// Middle axis, window -> length N' (ifftshift + ifftn(s = N') semantics):
+// Window -> length N' (ifftshift + ifftn(s = N') semantics):
 //   out[o, n, q] = s * sum_{j : t_j < N'} in[o, j, q] exp(+2 pi i t_j n / N'),
-//   t_j = (j - m/2) mod N
+//   t_j = (j + off) mod N (off = -m/2: the centred window)
 __global__ void __launch_bounds__(kThreads)
 k_c2c_inv_direct(const float2* __restrict__ in, float2* __restrict__ out, int64_t outer, int N,
-                 int Np, int64_t inner, int m, float scale) {
+                 int Np, int64_t inner, int m, int off, float scale) {
   extern __shared__ float smem[];
   float2* tw = reinterpret_cast<float2*>(smem);
   for (int t = threadIdx.x; t < Np; t += blockDim.x) tw[t] = twiddle_any(t, Np);
@@ -172,7 +173,7 @@ k_c2c_inv_direct(const float2* __restrict__ in, float2* __restrict__ out, int64_
     const float2* src = in + o * (int64_t)m * inner + q;
     float2 acc = make_float2(0.f, 0.f);
     for (int j = 0; j < m; ++j) {
-      int t = (j - m / 2) % N;
+      int t = (j + off) % N;
       if (t < 0) t += N;
       if (t >= Np) continue;
       const int idx = (int)(((int64_t)t * n) % Np);
@@ -441,10 +442,10 @@ bool c2r_fft_supported(int Np, int64_t rows);
 int c2r_fft(const float2* in, float* out, const float* bias, int64_t rows, int64_t rows_per_plane,
             int channels, int N, int Np, int m, int enforce, float scale, hipStream_t st);
 bool c2c_fft_supported(int L, int64_t outer, int64_t inner);
-int c2c_fft_fwd(const float2* in, float2* out, int64_t outer, int64_t inner, int N, int m,
+int c2c_fft_fwd(const float2* in, float2* out, int64_t outer, int64_t inner, int N, int m, int off,
                 float scale, hipStream_t st);
 int c2c_fft_inv(const float2* in, float2* out, int64_t outer, int64_t inner, int N, int Np, int m,
-                float scale, hipStream_t st);
+                int off, float scale, hipStream_t st);
 
 int rfft_window(const float* x, float2* xhat, int64_t planes, int32_t ndim, const int32_t* sizes,
                 const int32_t* modes, int32_t norm, void* ws, size_t ws_bytes, hipStream_t st) {
@@ -498,16 +499,143 @@ int rfft_window(const float* x, float2* xhat, int64_t planes, int32_t ndim, cons
     const float sc = (d == 0) ? (float)scale : 1.f;
     int rc;
     if (c2c_fft_supported(N, outer, inner)) {
-      rc = c2c_fft_fwd(src, dst, outer, inner, N, m, sc, st);
+      rc = c2c_fft_fwd(src, dst, outer, inner, N, m, -(m / 2), sc, st);
     } else {
       hipLaunchKernelGGL(k_c2c_fwd_direct, dim3(grid_for(outer * m * inner)), dim3(kThreads),
-                         (size_t)N * 8, st, src, dst, outer, N, inner, m, sc);
+                         (size_t)N * 8, st, src, dst, outer, N, inner, m, -(m / 2), sc);
       rc = launch_status("k_c2c_fwd_direct");
     }
     if (rc) return rc;
     src = dst;
   }
   return FNO_OK;
+}
+
+// ------------------------------------------------- complex-data windows
+// One axis of a complex window transform: line FFTs for 64/128/256 points,
+// direct sums otherwise.  Window entry j is frequency j + off.
+static int c2c_axis_fwd(const float2* src, float2* dst, int64_t outer, int N, int64_t inner, int m,
+                        int off, float sc, hipStream_t st) {
+  if (c2c_fft_supported(N, outer, inner)) return c2c_fft_fwd(src, dst, outer, inner, N, m, off, sc, st);
+  hipLaunchKernelGGL(k_c2c_fwd_direct, dim3(grid_for(outer * m * inner)), dim3(kThreads),
+                     (size_t)N * 8, st, src, dst, outer, N, inner, m, off, sc);
+  return launch_status("k_c2c_fwd_direct");
+}
+
+static int c2c_axis_inv(const float2* src, float2* dst, int64_t outer, int N, int Np, int64_t inner,
+                        int m, int off, float sc, hipStream_t st) {
+  if (c2c_fft_supported(Np, outer, inner))
+    return c2c_fft_inv(src, dst, outer, inner, N, Np, m, off, sc, st);
+  hipLaunchKernelGGL(k_c2c_inv_direct, dim3(grid_for(outer * Np * inner)), dim3(kThreads),
+                     (size_t)Np * 8, st, src, dst, outer, N, Np, inner, m, off, sc);
+  return launch_status("k_c2c_inv_direct");
+}
+
+// y[plane, p] += bias[plane % channels] on the real part
+__global__ void __launch_bounds__(kThreads)
+k_add_bias_re(float2* __restrict__ y, const float* __restrict__ bias, int64_t per_plane,
+              int channels, int64_t total) {
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x)
+    y[t].x += bias[(t / per_plane) % channels];
+}
+
+// Window offsets of complex data (spectral_convolution.py:436-449, :500-517,
+// :531-538): the non-last axes are fftshift-ed and keep the centred window;
+// the last axis keeps the first m entries of its fftshift-ed order (the
+// first m frequencies when the field is 1D, which is not shifted), and the
+// inverse places window entry j at index j of that axis (no ifftshift there).
+static int complex_fwd_off(int d, int ndim, int N, int m) {
+  if (d < ndim - 1) return -(m / 2);
+  return ndim > 1 ? -(N / 2) : 0;
+}
+
+int fft_window_c2c(const float2* x, float2* xhat, int64_t planes, int32_t ndim,
+                   const int32_t* sizes, const int32_t* modes, int32_t norm, void* ws,
+                   size_t ws_bytes, hipStream_t st) {
+  const double scale = forward_scale(norm, sizes, ndim);
+  const int64_t e0 = fwd_stage_elems(planes, ndim, sizes, modes, ndim - 1);
+  const int64_t e1 = ndim == 3 ? fwd_stage_elems(planes, ndim, sizes, modes, ndim - 2) : 0;
+  const size_t need = (ndim > 1 ? (size_t)e0 * sizeof(float2) : 0) + (size_t)e1 * sizeof(float2);
+  if (ws_bytes < need) {
+    set_error("fft_window: workspace %zu < %zu bytes", ws_bytes, need);
+    return FNO_ERR_WORKSPACE;
+  }
+  float2* bufs[2] = {reinterpret_cast<float2*>(ws), reinterpret_cast<float2*>(ws) + e0};
+  const float2* src = x;
+  for (int d = ndim - 1, stage = 0; d >= 0; --d, ++stage) {
+    int64_t outer = planes;
+    for (int a = 0; a < d; ++a) outer *= sizes[a];
+    int64_t inner = 1;
+    for (int a = d + 1; a < ndim; ++a) inner *= modes[a];
+    float2* dst = (d == 0) ? xhat : bufs[stage];
+    const int rc = c2c_axis_fwd(src, dst, outer, sizes[d], inner, modes[d],
+                                complex_fwd_off(d, ndim, sizes[d], modes[d]),
+                                d == 0 ? (float)scale : 1.f, st);
+    if (rc) return rc;
+    src = dst;
+  }
+  return FNO_OK;
+}
+
+size_t fft_window_c2c_ws(int64_t planes, int32_t ndim, const int32_t* sizes, const int32_t* modes) {
+  if (ndim <= 1) return 0;
+  size_t e = (size_t)fwd_stage_elems(planes, ndim, sizes, modes, ndim - 1);
+  if (ndim == 3) e += (size_t)fwd_stage_elems(planes, ndim, sizes, modes, ndim - 2);
+  return e * sizeof(float2);
+}
+
+int ifft_window_c2c(const float2* yhat, const float* bias, float2* y, int64_t batch,
+                    int32_t channels, int32_t ndim, const int32_t* in_sizes,
+                    const int32_t* out_sizes, const int32_t* modes, int32_t norm, void* ws,
+                    size_t ws_bytes, hipStream_t st) {
+  const int64_t planes = batch * channels;
+  const double scale = inverse_scale(norm, out_sizes, ndim);
+  int64_t eA = 0, eB = 0;
+  if (ndim >= 2) {
+    eA = planes * out_sizes[0];
+    for (int a = 1; a < ndim; ++a) eA *= modes[a];
+  }
+  if (ndim == 3) eB = planes * out_sizes[0] * out_sizes[1] * modes[2];
+  const size_t need = (size_t)(eA + eB) * sizeof(float2);
+  if (ws_bytes < need) {
+    set_error("ifft_window: workspace %zu < %zu bytes", ws_bytes, need);
+    return FNO_ERR_WORKSPACE;
+  }
+  float2* bufs[2] = {reinterpret_cast<float2*>(ws), reinterpret_cast<float2*>(ws) + eA};
+  const float2* src = yhat;
+  for (int d = 0; d < ndim; ++d) {
+    int64_t outer = planes;
+    for (int a = 0; a < d; ++a) outer *= out_sizes[a];
+    int64_t inner = 1;
+    for (int a = d + 1; a < ndim; ++a) inner *= modes[a];
+    const bool last = d == ndim - 1;
+    float2* dst = last ? y : bufs[d];
+    const int off = last ? 0 : -(modes[d] / 2);
+    const int rc = c2c_axis_inv(src, dst, outer, in_sizes[d], out_sizes[d], inner, modes[d], off,
+                                last ? (float)scale : 1.f, st);
+    if (rc) return rc;
+    src = dst;
+  }
+  if (bias) {
+    int64_t per_plane = 1;
+    for (int a = 0; a < ndim; ++a) per_plane *= out_sizes[a];
+    hipLaunchKernelGGL(k_add_bias_re, dim3(grid_for(planes * per_plane)), dim3(kThreads), 0, st, y,
+                       bias, per_plane, channels, planes * per_plane);
+    return launch_status("k_add_bias_re");
+  }
+  return FNO_OK;
+}
+
+size_t ifft_window_c2c_ws(int64_t planes, int32_t ndim, const int32_t* out_sizes,
+                          const int32_t* modes) {
+  int64_t eA = 0, eB = 0;
+  if (ndim >= 2) {
+    eA = planes * out_sizes[0];
+    for (int a = 1; a < ndim; ++a) eA *= modes[a];
+  }
+  if (ndim == 3) eB = planes * out_sizes[0] * out_sizes[1] * modes[2];
+  return (size_t)(eA + eB) * sizeof(float2);
 }
 
 int irfft_window(const float2* yhat, const float* bias, float* y, int64_t batch, int32_t channels,
@@ -540,10 +668,10 @@ int irfft_window(const float2* yhat, const float* bias, float* y, int64_t batch,
     const int N = in_sizes[d], Np = out_sizes[d], m = modes[d];
     int rc;
     if (c2c_fft_supported(Np, outer, inner)) {
-      rc = c2c_fft_inv(src, dst, outer, inner, N, Np, m, 1.f, st);
+      rc = c2c_fft_inv(src, dst, outer, inner, N, Np, m, -(m / 2), 1.f, st);
     } else {
       hipLaunchKernelGGL(k_c2c_inv_direct, dim3(grid_for(outer * Np * inner)), dim3(kThreads),
-                         (size_t)Np * 8, st, src, dst, outer, N, Np, inner, m, 1.f);
+                         (size_t)Np * 8, st, src, dst, outer, N, Np, inner, m, -(m / 2), 1.f);
       rc = launch_status("k_c2c_inv_direct");
     }
     if (rc) return rc;

@@ -147,14 +147,15 @@ k_c2r_fft(const float2* __restrict__ in, float* __restrict__ out, const float* _
 // stride of `inner` entries.  A workgroup takes QB consecutive q of one o:
 // the [L][QB] tile moves through LDS with coalesced row accesses (stride TS >
 // QB against bank conflicts) and each line FFTs in its own tile column.
-//   forward (SIGN -1): L = N input points; out[o][j][q] = s X[(j - m/2) mod N]
-//   inverse (SIGN +1): L = Np; window entry j goes to index (j - m/2) mod N
+//   forward (SIGN -1): L = N input points; out[o][j][q] = s X[(j + off) mod N]
+//   inverse (SIGN +1): L = Np; window entry j goes to index (j + off) mod N
 //                      when that is < Np (zero-padding / truncation of the
 //                      length-N spectrum), out[o][n][q] for n < Np
+// (off = -m/2 for the centred window of fftshift-ed axes)
 template <int L, int SIGN>
 __global__ void __launch_bounds__(kFftThreads)
 k_c2c_fft_axis(const float2* __restrict__ in, float2* __restrict__ out, int64_t inner, int N,
-               int m, float scale) {
+               int m, int off, float scale) {
   using PL = LinePlan<L>;
   constexpr int T = PL::T, R = PL::R, Q = PL::Q;
   constexpr int QB = kFftThreads / T;
@@ -182,7 +183,7 @@ k_c2c_fft_axis(const float2* __restrict__ in, float2* __restrict__ out, int64_t 
     __syncthreads();
     for (int i = threadIdx.x; i < m * QB; i += kFftThreads) {
       const int j = i / QB, g = i % QB;
-      int t = (j - m / 2) % N;
+      int t = (j + off) % N;
       if (t < 0) t += N;
       if (t < L && g < qn) tile[t * TS + g] = src[(int64_t)j * inner + g];
     }
@@ -207,7 +208,7 @@ k_c2c_fft_axis(const float2* __restrict__ in, float2* __restrict__ out, int64_t 
     const int j = i / QB, g = i % QB;
     int k = j;
     if (SIGN < 0) {
-      k = (j - m / 2) % L;
+      k = (j + off) % L;
       if (k < 0) k += L;
     }
     if (g < qn) dst[(int64_t)j * inner + g] = cscale(tile[k * TS + g], scale);
@@ -271,30 +272,30 @@ bool c2c_fft_supported(int L, int64_t outer, int64_t inner) {
 
 template <int L, int SIGN>
 static int launch_c2c(const float2* in, float2* out, int64_t outer, int64_t inner, int N, int m,
-                      float scale, hipStream_t st) {
+                      int off, float scale, hipStream_t st) {
   constexpr int QB = kFftThreads / LinePlan<L>::T;
   constexpr int TS = (QB == 32) ? 40 : QB + 1;
   const size_t lds = (size_t)(L + L * TS) * sizeof(float2);
   const int64_t blocks = outer * ((inner + QB - 1) / QB);
   hipLaunchKernelGGL((k_c2c_fft_axis<L, SIGN>), dim3((unsigned)blocks), dim3(kFftThreads), lds,
-                     st, in, out, inner, N, m, scale);
+                     st, in, out, inner, N, m, off, scale);
   return launch_status("k_c2c_fft_axis");
 }
 
-// forward: lines of N points -> m centred modes
-int c2c_fft_fwd(const float2* in, float2* out, int64_t outer, int64_t inner, int N, int m,
+// forward: lines of N points -> m window modes (entry j = frequency j + off)
+int c2c_fft_fwd(const float2* in, float2* out, int64_t outer, int64_t inner, int N, int m, int off,
                 float scale, hipStream_t st) {
-  if (N == 64) return launch_c2c<64, -1>(in, out, outer, inner, N, m, scale, st);
-  if (N == 128) return launch_c2c<128, -1>(in, out, outer, inner, N, m, scale, st);
-  return launch_c2c<256, -1>(in, out, outer, inner, N, m, scale, st);
+  if (N == 64) return launch_c2c<64, -1>(in, out, outer, inner, N, m, off, scale, st);
+  if (N == 128) return launch_c2c<128, -1>(in, out, outer, inner, N, m, off, scale, st);
+  return launch_c2c<256, -1>(in, out, outer, inner, N, m, off, scale, st);
 }
 
-// inverse: m centred modes of a length-N spectrum -> lines of Np points
+// inverse: m window modes of a length-N spectrum -> lines of Np points
 int c2c_fft_inv(const float2* in, float2* out, int64_t outer, int64_t inner, int N, int Np, int m,
-                float scale, hipStream_t st) {
-  if (Np == 64) return launch_c2c<64, +1>(in, out, outer, inner, N, m, scale, st);
-  if (Np == 128) return launch_c2c<128, +1>(in, out, outer, inner, N, m, scale, st);
-  return launch_c2c<256, +1>(in, out, outer, inner, N, m, scale, st);
+                int off, float scale, hipStream_t st) {
+  if (Np == 64) return launch_c2c<64, +1>(in, out, outer, inner, N, m, off, scale, st);
+  if (Np == 128) return launch_c2c<128, +1>(in, out, outer, inner, N, m, off, scale, st);
+  return launch_c2c<256, +1>(in, out, outer, inner, N, m, off, scale, st);
 }
 
 }  // namespace fno

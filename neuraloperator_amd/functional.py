@@ -122,6 +122,43 @@ def irfft_window(yhat: torch.Tensor, in_sizes: Sequence[int], out_sizes: Sequenc
     return y
 
 
+def fft_window(x: torch.Tensor, modes: Sequence[int], fft_norm: str = "forward") -> torch.Tensor:
+    """Kept-mode window of fftn(x) for complex data (see fno_fft_window_c64).
+    x complex [B, C, *S] -> complex64 [B, C, *modes]."""
+    _require_gpu(x)
+    lib = nat.load()
+    x = _c64(x)
+    B, C, *S = x.shape
+    nd = len(S)
+    out = torch.empty((B, C, *modes), dtype=torch.complex64, device=x.device)
+    sz, md = nat.i32_array(S), nat.i32_array(modes)
+    wsb = lib.fno_fft_window_workspace_bytes(B * C, nd, sz, md)
+    ws = _workspace(wsb, x.device)
+    nat.check(lib.fno_fft_window_c64(_ptr(x), _ptr(out), B * C, nd, sz, md, nat.NORMS[fft_norm],
+                                     _ptr(ws), wsb, _stream(x.device)), "fno_fft_window_c64")
+    return out
+
+
+def ifft_window(yhat: torch.Tensor, in_sizes: Sequence[int], out_sizes: Sequence[int],
+                bias: Optional[torch.Tensor] = None, fft_norm: str = "forward") -> torch.Tensor:
+    """Complex field of size out_sizes from a complex-data window (+ bias on
+    the real part)."""
+    _require_gpu(yhat, bias)
+    lib = nat.load()
+    yhat = _c64(yhat)
+    B, C, *modes = yhat.shape
+    nd = len(modes)
+    y = torch.empty((B, C, *out_sizes), dtype=torch.complex64, device=yhat.device)
+    b = _f32(bias.reshape(-1)) if bias is not None else None
+    isz, osz, md = nat.i32_array(in_sizes), nat.i32_array(out_sizes), nat.i32_array(modes)
+    wsb = lib.fno_ifft_window_workspace_bytes(B * C, nd, osz, md)
+    ws = _workspace(wsb, yhat.device)
+    nat.check(lib.fno_ifft_window_c64(_ptr(yhat), _ptr(b), _ptr(y), B, C, nd, isz, osz, md,
+                                      nat.NORMS[fft_norm], _ptr(ws), wsb, _stream(yhat.device)),
+              "fno_ifft_window_c64")
+    return y
+
+
 def block_epilogue(spec: torch.Tensor, x: Optional[torch.Tensor], skip_kind: int,
                    skip_weight: Optional[torch.Tensor], act: int, out: Optional[torch.Tensor] = None):
     """act(spec + skip(x)); writes into ``out`` (default: spec itself)."""

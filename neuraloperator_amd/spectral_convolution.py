@@ -13,6 +13,8 @@ CP / TT weights are reconstructed (torch ops on the weight only) and then
 contracted densely; the result is the same mathematics as the reference's
 factor-wise einsums (spectral_convolution.py:55-73, :106-132).
 
+complex_data=True runs fno_fft_window_c64 -> contraction -> fno_ifft_window_c64.
+
 Autograd: when gradients are required (training), the forward runs as
 _SpectralConvFn, whose backward is built from the same library calls (window
 transforms under the dual norm and the dense contraction) for output size ==
@@ -267,8 +269,11 @@ class SpectralConv(BaseSpectralConv):
             fft_size[-1] = fft_size[-1] // 2 + 1
         starts = [mx - min(s, n) for s, n, mx in zip(fft_size, self.n_modes, self.max_n_modes)]
         sl = [slice(None)] if self.separable else [slice(None), slice(None)]
-        sl += [slice(s // 2, -s // 2) if s else slice(s, None) for s in starts[:-1]]
-        sl += [slice(None, -starts[-1]) if starts[-1] else slice(None)]
+        if self.complex_data:   # every axis centred (:475-479)
+            sl += [slice(s // 2, -s // 2) if s else slice(s, None) for s in starts]
+        else:
+            sl += [slice(s // 2, -s // 2) if s else slice(s, None) for s in starts[:-1]]
+            sl += [slice(None, -starts[-1]) if starts[-1] else slice(None)]
         kept = [mx - s for mx, s in zip(self.max_n_modes, starts)]
         return kept, tuple(sl)
 
@@ -293,15 +298,32 @@ class SpectralConv(BaseSpectralConv):
             raise RuntimeError(
                 "SpectralConv (neuraloperator_amd) runs on the GPU only; move the module and "
                 "input to a HIP device")
-        if self.complex_data:
-            raise NotImplementedError("complex_data=True spectral path is not built")
         profiler = get_active_profiler()
         name = getattr(self, "profile_prefix", "spectral_conv")
         with maybe_profile(profiler, name, x.device):
+            if self.complex_data:
+                return self._forward_complex(x, output_shape)
             if torch.is_grad_enabled() and (x.requires_grad or
                                             any(p.requires_grad for p in self.parameters())):
                 return self._forward_autograd(x, output_shape)
             return self._forward_hip(x, output_shape)
+
+    def _forward_complex(self, x, output_shape=None):
+        """complex_data=True: fftn / window / contraction / ifftn on complex
+        fields (spectral_convolution.py:436-449, :500-538), output complex."""
+        sizes = list(x.shape[2:])
+        kept, sl = self.window(sizes)
+        out_sizes = self.output_sizes(sizes, output_shape)
+        xhat = Fh.fft_window(x.detach(), kept, self.fft_norm)
+        if self._contract == "tucker" and not self.separable:
+            wv = self.weight[sl]
+            yhat = Fh.contract_tucker(xhat, wv.core.detach(), [f.detach() for f in wv.factors])
+        else:
+            yhat = Fh.contract_dense(xhat, self.dense_window_weight(sl).detach(),
+                                     separable=self.separable)
+        bias = self.bias.reshape(-1).detach() if self.bias is not None else None
+        y = Fh.ifft_window(yhat, sizes, out_sizes, bias, self.fft_norm)
+        return _attach(y, x, self.bias, *self.weight.parameters())
 
     def _forward_autograd(self, x, output_shape=None):
         """Forward with gradients for x, the weight (through its dense window,

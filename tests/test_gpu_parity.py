@@ -481,6 +481,51 @@ def test_fno_backward_gradients(cuda_device):
         assert rel_err(blocks.channel_mlp_skips[i].weight.grad, layers[i]["mlp_skip"]["w"].grad) <= TOL
 
 
+@pytest.mark.parametrize("sizes,nm,out", [
+    ((64,), (20,), None),                    # 1D, line FFT
+    ((37,), (12,), None),                    # 1D, direct
+    ((16, 64), (8, 20), None),
+    ((12, 9), (6, 5), None),                 # odd last axis
+    ((64, 128), (16, 32), None),             # line FFTs on both axes
+    ((8, 12, 16), (4, 6, 8), None),
+    ((16, 64), (8, 20), (32, 128)),          # onto a larger grid
+    ((16, 64), (8, 20), (8, 32)),            # onto a smaller one
+])
+@pytest.mark.parametrize("norm", ["forward", "ortho"])
+def test_complex_data_spectral_conv(sizes, nm, out, norm, cuda_device):
+    """SpectralConv(complex_data=True) on complex fields against the float64
+    oracle (fftn / window / ifftn, with the reference's last-axis window)."""
+    print(f"complex {sizes} {nm} {out} {norm}", flush=True)
+    torch.manual_seed(22)
+    conv = na.SpectralConv(3, 4, nm, complex_data=True, fft_norm=norm).to(cuda_device)
+    with torch.no_grad():
+        conv.bias.normal_()
+    x = torch.randn(2, 3, *sizes, dtype=torch.complex64)
+    with torch.no_grad():
+        y = conv(x.to(cuda_device), output_shape=out)
+    assert y.dtype == torch.complex64 and list(y.shape) == [2, 4, *(out or sizes)]
+    ref = R.spectral_conv_forward(x.to(torch.complex128),
+                                  conv.weight.to_tensor().detach().cpu().to(torch.complex128),
+                                  conv.bias.detach().cpu().double(), conv.n_modes, conv.max_n_modes,
+                                  fft_norm=norm, complex_data=True, output_shape=out)
+    assert rel_err(torch.view_as_real(y), torch.view_as_real(ref)) <= TOL
+
+
+def test_complex_data_tucker(cuda_device):
+    torch.manual_seed(23)
+    conv = na.SpectralConv(4, 4, (8, 8, 8), complex_data=True, factorization="Tucker", rank=0.5,
+                           implementation="factorized").to(cuda_device)
+    x = torch.randn(2, 4, 16, 16, 16, dtype=torch.complex64)
+    with torch.no_grad():
+        y = conv(x.to(cuda_device))
+    core = conv.weight.core.detach().cpu().to(torch.complex128)
+    factors = [f.detach().cpu().to(torch.complex128) for f in conv.weight.factors]
+    ref = R.spectral_conv_forward(x.to(torch.complex128), {"tucker": (core, factors)},
+                                  conv.bias.detach().cpu().double(), conv.n_modes, conv.max_n_modes,
+                                  implementation="factorized", complex_data=True)
+    assert rel_err(torch.view_as_real(y), torch.view_as_real(ref)) <= TOL
+
+
 def test_deterministic(cuda_device):
     torch.manual_seed(11)
     conv = na.SpectralConv(64, 64, (64, 64)).to(cuda_device)

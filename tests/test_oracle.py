@@ -91,6 +91,32 @@ def test_plane_wave_known_answer(kh, kw):
     assert torch.allclose(y, expected, atol=1e-12)
 
 
+@pytest.mark.parametrize("sizes,nm,f_in,j,f_out", [
+    # 2D: axis 0 keeps the centred window (j = f + m/2); the last axis keeps
+    # the first m entries of its fftshift-ed order (frequency j - N/2) and
+    # the inverse puts entry j at frequency j (no ifftshift on the last axis,
+    # spectral_convolution.py:448-449, :510-517, :531-538)
+    ((8, 8), (4, 4), (1, -3), (3, 1), (1, 1)),
+    ((8, 9), (4, 5), (-2, -4), (0, 0), (-2, 0)),
+    # 1D: no shift at all, the first m frequencies
+    ((10,), (4,), (3,), (3,), (3,)),
+])
+def test_complex_data_plane_wave(sizes, nm, f_in, j, f_out):
+    """complex_data=True: a plane wave through a weight that is non-zero at
+    one window entry comes out as the plane wave of the frequency the
+    reference's shifts and slices map that entry to."""
+    grids = torch.meshgrid(*[torch.arange(n, dtype=torch.float64) for n in sizes], indexing="ij")
+    phase = sum(f * g / n for f, g, n in zip(f_in, grids, sizes))
+    x = torch.exp(2j * math.pi * phase).reshape(1, 1, *sizes)
+    w = torch.zeros(1, 1, *nm, dtype=torch.complex128)
+    a = 0.7 - 0.4j
+    w[(0, 0, *j)] = a
+    y = R.spectral_conv_forward(x, w, None, list(nm), list(nm), complex_data=True)
+    out_phase = sum(f * g / n for f, g, n in zip(f_out, grids, sizes))
+    expect = a * torch.exp(2j * math.pi * out_phase).reshape(1, 1, *sizes)
+    assert torch.allclose(y, expect, atol=1e-12)
+
+
 def test_circular_shift_equivariance():
     torch.manual_seed(2)
     nms = R.stored_n_modes((6, 6))
