@@ -305,8 +305,15 @@ class SpectralConv(BaseSpectralConv):
                 return self._forward_complex(x, output_shape)
             if torch.is_grad_enabled() and (x.requires_grad or
                                             any(p.requires_grad for p in self.parameters())):
-                return self._forward_autograd(x, output_shape)
-            return self._forward_hip(x, output_shape)
+                y = self._forward_autograd(x, output_shape)
+            else:
+                y = self._forward_hip(x, output_shape)
+            # fno_block_precision 'half' / 'mixed' (:436-459): the reference's
+            # inverse returns float16, promoted to float32 by the float32 bias
+            # when there is one; the kernels compute in fp32 either way
+            if self.fno_block_precision in ("half", "mixed") and self.bias is None:
+                y = y.half()
+            return y
 
     def _forward_complex(self, x, output_shape=None):
         """complex_data=True: fftn / window / contraction / ifftn on complex

@@ -526,6 +526,24 @@ def test_complex_data_tucker(cuda_device):
     assert rel_err(torch.view_as_real(y), torch.view_as_real(ref)) <= TOL
 
 
+@pytest.mark.parametrize("precision", ["half", "mixed"])
+@pytest.mark.parametrize("bias", [True, False])
+def test_block_precision_output_dtype(precision, bias, cuda_device):
+    """fno_block_precision 'half' / 'mixed': output dtype as the reference's
+    (float16 from the inverse, float32 once the float32 bias is added); the
+    values are the fp32 computation."""
+    torch.manual_seed(24)
+    conv = na.SpectralConv(3, 4, (6, 6), bias=bias, fno_block_precision=precision).to(cuda_device)
+    x = torch.randn(2, 3, 12, 12)
+    with torch.no_grad():
+        y = conv(x.to(cuda_device))
+    assert y.dtype == (torch.float32 if bias else torch.float16)
+    ref = R.spectral_conv_forward(x.double(), conv.weight.to_tensor().detach().cpu().to(torch.complex128),
+                                  conv.bias.detach().cpu().double() if bias else None, conv.n_modes,
+                                  conv.max_n_modes)
+    assert rel_err(y, ref) <= (TOL if bias else 2e-3)
+
+
 def test_deterministic(cuda_device):
     torch.manual_seed(11)
     conv = na.SpectralConv(64, 64, (64, 64)).to(cuda_device)
