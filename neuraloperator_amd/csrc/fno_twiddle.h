@@ -5,7 +5,7 @@
 
 namespace fno {
 
-// exp(+2 pi i k / 256), k < 256, evaluated at compile time in double
+// exp(+2 pi i k / 1024), k < 1024, evaluated at compile time in double
 // precision (octant reduction + Taylor series to x^23, error << 1e-16) and
 // rounded once to float, so every twiddle is within half an ulp.
 namespace twd {
@@ -26,20 +26,21 @@ constexpr double cos_series(double x) {
   }
   return sum;
 }
-struct Table256 {
-  float re[256], im[256];
+constexpr int kN = 1024;
+struct Table {
+  float re[kN], im[kN];
 };
-constexpr Table256 make_table() {
-  Table256 t{};
-  for (int k = 0; k < 256; ++k) {
-    const int q = k / 64, m = k % 64;   // quadrant, position in it
+constexpr Table make_table() {
+  Table t{};
+  for (int k = 0; k < kN; ++k) {
+    const int q = k / (kN / 4), m = k % (kN / 4);   // quadrant, position in it
     double c = 0, sn = 0;
-    if (m <= 32) {
-      c = cos_series(2.0 * kPi * m / 256.0);
-      sn = sin_series(2.0 * kPi * m / 256.0);
+    if (m <= kN / 8) {
+      c = cos_series(2.0 * kPi * m / kN);
+      sn = sin_series(2.0 * kPi * m / kN);
     } else {
-      c = sin_series(2.0 * kPi * (64 - m) / 256.0);
-      sn = cos_series(2.0 * kPi * (64 - m) / 256.0);
+      c = sin_series(2.0 * kPi * (kN / 4 - m) / kN);
+      sn = cos_series(2.0 * kPi * (kN / 4 - m) / kN);
     }
     double cr = c, sr = sn;
     if (q == 1) { cr = -sn; sr = c; }
@@ -53,22 +54,22 @@ constexpr Table256 make_table() {
 }  // namespace twd
 // one copy per translation unit (internal linkage): device code is not
 // relocatable across units
-static __constant__ const twd::Table256 kTw256 = twd::make_table();
+static __constant__ const twd::Table kTw = twd::make_table();
 
-// LDS table of exp(+2 pi i t / N), t < N, for N dividing 256
+// LDS table of exp(+2 pi i t / N), t < N, for N dividing 1024
 template <int N>
 __device__ __forceinline__ void fill_twiddles(float2* tw) {
-  static_assert(256 % N == 0, "N must divide 256");
+  static_assert(twd::kN % N == 0, "N must divide 1024");
   for (int i = threadIdx.x; i < N; i += blockDim.x)
-    tw[i] = make_float2(kTw256.re[i * (256 / N)], kTw256.im[i * (256 / N)]);
+    tw[i] = make_float2(kTw.re[i * (twd::kN / N)], kTw.im[i * (twd::kN / N)]);
 }
 
-// exp(+2 pi i t / n) for 0 <= t < n: the table entry when n divides 256 (the
+// exp(+2 pi i t / n) for 0 <= t < n: the table entry when n divides 1024 (the
 // same correctly rounded value), else evaluated in double precision.
 __device__ __forceinline__ float2 twiddle_any(int t, int n) {
-  if (256 % n == 0) {
-    const int i = t * (256 / n);
-    return make_float2(kTw256.re[i], kTw256.im[i]);
+  if (twd::kN % n == 0) {
+    const int i = t * (twd::kN / n);
+    return make_float2(kTw.re[i], kTw.im[i]);
   }
   return twiddle_pos(t, n);
 }
