@@ -47,7 +47,7 @@ class ChannelMLP(nn.Module):
         for s in x.shape[2:]:
             P *= s
         return Fh.channel_mlp_is_supported(self.in_channels, self.hidden_channels,
-                                           self.out_channels, P)
+                                           self.out_channels, P, x)
 
     def forward(self, x):
         if self._fusable(x):

@@ -311,9 +311,11 @@ int fno_channel_mlp_f32(const float* x, const float* w1, const float* b1, const 
               in_channels, hidden_channels, out_channels, (long long)points);
     return FNO_ERR_UNSUPPORTED;
   }
-  const uintptr_t addr = reinterpret_cast<uintptr_t>(x);
+  // 16-byte slab loads of x, staged 16-byte rows of skip_x and y
+  const uintptr_t addr = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(skip_x) |
+                         reinterpret_cast<uintptr_t>(y);
   if (addr % 16 != 0) {
-    set_error("channel MLP: x must be 16-byte aligned");
+    set_error("channel MLP: x, skip_x and y must be 16-byte aligned");
     return FNO_ERR_UNSUPPORTED;
   }
   return channel_mlp(x, w1, b1, w2, b2, skip_x, skip_weight, skip_bias, y, batch, in_channels,

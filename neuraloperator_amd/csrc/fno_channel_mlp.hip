@@ -342,10 +342,13 @@ int channel_mlp(const float* x, const float* w1, const float* b1, const float* w
   return FNO_ERR_UNSUPPORTED;
 }
 
-// Linear block skip on MFMA: y = act(Ws x + spec); spec may alias y
-bool skip_gemm_supported(int Ci, int Co, int64_t P, const void* x) {
-  return P % 4 == 0 && Ci == Co && (Ci == 32 || Ci == 64 || Ci == 128) &&
-         reinterpret_cast<uintptr_t>(x) % 16 == 0;
+// Linear block skip on MFMA: y = act(Ws x + spec); spec may alias y.  The
+// slab loads of x and the staged rows of spec and y are 16-byte accesses.
+bool skip_gemm_supported(int Ci, int Co, int64_t P, const void* x, const void* spec,
+                         const void* y) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(spec) |
+                      reinterpret_cast<uintptr_t>(y);
+  return P % 4 == 0 && Ci == Co && (Ci == 32 || Ci == 64 || Ci == 128) && a % 16 == 0;
 }
 
 int skip_gemm(const float* x, const float* ws, const float* spec, float* y, int64_t B, int Ci,

@@ -769,14 +769,15 @@ static int launch_epilogue(const float* spec, const float* x, const float* ws, f
   return launch_status("k_epilogue");
 }
 
-bool skip_gemm_supported(int Ci, int Co, int64_t P, const void* x);
+bool skip_gemm_supported(int Ci, int Co, int64_t P, const void* x, const void* spec,
+                         const void* y);
 int skip_gemm(const float* x, const float* ws, const float* spec, float* y, int64_t B, int Ci,
               int Co, int64_t P, int act, hipStream_t st);
 
 int block_epilogue(const float* spec, const float* x, const float* ws, float* y, int B, int Ci,
                    int Co, int64_t P, int skip_kind, int act, hipStream_t st) {
   // the linear skip as an MFMA GEMM with the spectral term added in its epilogue
-  if (skip_kind == FNO_SKIP_LINEAR && skip_gemm_supported(Ci, Co, P, x))
+  if (skip_kind == FNO_SKIP_LINEAR && skip_gemm_supported(Ci, Co, P, x, spec, y))
     return skip_gemm(x, ws, spec, y, B, Ci, Co, P, act, st);
   // vector access needs every (b, c) row to start on the vector boundary
   const uintptr_t addr = reinterpret_cast<uintptr_t>(spec) | reinterpret_cast<uintptr_t>(x) |

@@ -237,7 +237,10 @@ class FNOBlocks(nn.Module):
         P = 1
         for s in x.shape[2:]:
             P *= s
-        if not Fh.channel_mlp_is_supported(mlp.in_channels, mlp.hidden_channels, mlp.out_channels, P):
+        # x here is the block input (the skip input); the MLP input is the
+        # spectral block's fresh output, allocated aligned
+        if not Fh.channel_mlp_is_supported(mlp.in_channels, mlp.hidden_channels, mlp.out_channels, P,
+                                           x):
             return None
         if self.channel_mlp_skips is None:
             return nat.SKIP_NONE, None

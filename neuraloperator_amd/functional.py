@@ -179,7 +179,11 @@ def block_epilogue(spec: torch.Tensor, x: Optional[torch.Tensor], skip_kind: int
     return y
 
 
-def channel_mlp_is_supported(Ci: int, Ch: int, Co: int, P: int) -> bool:
+def channel_mlp_is_supported(Ci: int, Ch: int, Co: int, P: int, *tensors) -> bool:
+    """Widths and point count the kernel covers; tensors passed here must
+    also start on a 16-byte boundary (its vector accesses)."""
+    if any(t is not None and t.data_ptr() % 16 for t in tensors):
+        return False
     return bool(nat.load().fno_channel_mlp_is_supported(Ci, Ch, Co, P))
 
 

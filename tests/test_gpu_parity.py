@@ -697,6 +697,24 @@ def test_channel_mlp_in_place(cuda_device):
     assert torch.equal(a, b)
 
 
+def test_block_epilogue_unaligned_spec(cuda_device):
+    """An aligned x with the spectral term (and output) one float off a
+    16-byte boundary: the square linear skip leaves the MFMA GEMM (its staged
+    rows are 16-byte accesses) for the scalar path and still matches."""
+    g = torch.Generator().manual_seed(26)
+    B, C, P = 2, 32, 256
+    sbuf = torch.randn(B * C * P + 1, generator=g)
+    x = torch.randn(B, C, P, generator=g)
+    ws = torch.randn(C, C, generator=g) / C ** 0.5
+    spec = sbuf[1:].view(B, C, P)
+    ref = R.gelu(spec.double() + torch.einsum("oi,bip->bop", ws.double(), x.double()))
+    sd = sbuf.to(cuda_device)[1:].view(B, C, P)
+    with torch.no_grad():
+        y = Fh.block_epilogue(sd, x.to(cuda_device), nat.SKIP_LINEAR, ws.to(cuda_device), nat.ACT_GELU)
+    torch.cuda.synchronize()
+    assert rel_err(y, ref) <= TOL
+
+
 def test_kernel_gelu_matches_exact_erf(cuda_device):
     """The kernels' erf GELU (Abramowitz & Stegun 7.1.28 form) against exact
     erf GELU in float64 over [-12, 12], through the C-ABI epilogue with no
