@@ -232,7 +232,7 @@ class FNOBlocks(nn.Module):
             return None
         mlp = self.channel_mlp[index]
         if (mlp.n_layers != 2 or mlp.non_linearity is not F.gelu or mlp.dropout is not None
-                or mlp.in_channels != self.out_channels):
+                or mlp.in_channels != conv.out_channels):
             return None
         P = 1
         for s in x.shape[2:]:
@@ -247,7 +247,7 @@ class FNOBlocks(nn.Module):
         sk = self.channel_mlp_skips[index]
         if isinstance(sk, SoftGating):
             return nat.SKIP_SOFT_GATING, sk
-        if isinstance(sk, nn.Identity) and self.in_channels == self.out_channels:
+        if isinstance(sk, nn.Identity) and conv.in_channels == conv.out_channels:
             return nat.SKIP_IDENTITY, None
         return None
 

@@ -1,0 +1,187 @@
+"""FNOStaged: FNO with per-layer Fourier mode counts
+(neuralop/models/fno_staged.py:24-502), on the MI355X FNOBlocks.
+
+The layers are FNOBlocks' own (so the fused spectral block and channel-MLP
+calls apply per layer), with each layer's SpectralConv built at that layer's
+n_modes / max_n_modes.  The module keeps the reference's top-level attribute
+names (convs, fno_skips, channel_mlp, channel_mlp_skips, norm, lifting,
+projection, positional_embedding).  The fork's bit-reversed butterfly path
+(no_br=True) is not built.
+"""
+from __future__ import annotations
+
+import warnings
+from typing import List, Literal, Optional, Tuple, Union
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from .channel_mlp import ChannelMLP
+from .embeddings import GridEmbeddingND
+from .fno_block import FNOBlocks
+from .spectral_convolution import SpectralConv
+from .utils import get_active_profiler, maybe_profile
+
+Number = Union[float, int]
+
+
+class FNOStaged(FNOBlocks):
+    def __init__(
+        self,
+        n_modes_per_layer: List[Tuple[int, ...]],
+        in_channels: int,
+        out_channels: int,
+        hidden_channels: int,
+        n_layers: Optional[int] = None,
+        max_n_modes_per_layer: Optional[List[Tuple[int, ...]]] = None,
+        lifting_channel_ratio: Number = 2,
+        projection_channel_ratio: Number = 2,
+        positional_embedding: Union[str, nn.Module] = "grid",
+        non_linearity: nn.Module = F.gelu,
+        norm: Literal["ada_in", "group_norm", "instance_norm", "batch_norm"] = None,
+        norm_groups: int = 1,
+        complex_data: bool = False,
+        use_channel_mlp: bool = True,
+        channel_mlp_dropout: float = 0,
+        channel_mlp_expansion: float = 0.5,
+        channel_mlp_skip: Literal["linear", "identity", "soft-gating", None] = "soft-gating",
+        fno_skip: Literal["linear", "identity", "soft-gating", None] = "linear",
+        resolution_scaling_factor: Union[Number, List[Number]] = None,
+        domain_padding: Union[Number, List[Number]] = None,
+        fno_block_precision: str = "full",
+        stabilizer: str = None,
+        factorization: str = None,
+        rank: float = 1.0,
+        fixed_rank_modes: bool = False,
+        implementation: str = "factorized",
+        decomposition_kwargs: dict = None,
+        separable: bool = False,
+        preactivation: bool = False,
+        conv_module: nn.Module = SpectralConv,
+        enforce_hermitian_symmetry: bool = True,
+        no_br: bool = False,
+    ):
+        if decomposition_kwargs is None:
+            decomposition_kwargs = {}
+        # argument checks of fno_staged.py:70-86
+        if n_layers is not None and n_layers != len(n_modes_per_layer):
+            raise ValueError(
+                f"Got n_layers={n_layers} but n_modes_per_layer has length {len(n_modes_per_layer)}")
+        n_modes_per_layer = [list(m) for m in n_modes_per_layer]
+        L = len(n_modes_per_layer)
+        if max_n_modes_per_layer is None:
+            max_n_modes_per_layer = n_modes_per_layer
+        if len(max_n_modes_per_layer) != L:
+            raise ValueError(
+                "max_n_modes_per_layer must be None or have the same length as n_modes_per_layer")
+        max_n_modes_per_layer = [list(m) for m in max_n_modes_per_layer]
+        if no_br:
+            raise NotImplementedError("no_br=True (bit-reversed butterfly spectral path) is not built")
+        if domain_padding is not None and (
+                (isinstance(domain_padding, list) and sum(domain_padding) > 0)
+                or (isinstance(domain_padding, (float, int)) and domain_padding > 0)):
+            raise NotImplementedError("domain_padding is not built")
+        if resolution_scaling_factor is not None and isinstance(resolution_scaling_factor,
+                                                                (float, int)):
+            resolution_scaling_factor = [resolution_scaling_factor] * L
+
+        super().__init__(
+            in_channels=hidden_channels, out_channels=hidden_channels,
+            n_modes=n_modes_per_layer[0], resolution_scaling_factor=resolution_scaling_factor,
+            n_layers=L, max_n_modes=max_n_modes_per_layer[0],
+            fno_block_precision=fno_block_precision, use_channel_mlp=use_channel_mlp,
+            channel_mlp_dropout=channel_mlp_dropout, channel_mlp_expansion=channel_mlp_expansion,
+            non_linearity=non_linearity, stabilizer=stabilizer, norm=norm, norm_groups=norm_groups,
+            preactivation=preactivation, fno_skip=fno_skip, channel_mlp_skip=channel_mlp_skip,
+            complex_data=complex_data, separable=separable, factorization=factorization, rank=rank,
+            conv_module=conv_module, fixed_rank_modes=fixed_rank_modes,
+            implementation=implementation, decomposition_kwargs=decomposition_kwargs,
+            enforce_hermitian_symmetry=enforce_hermitian_symmetry)
+
+        self.n_dim = len(n_modes_per_layer[0])
+        self.n_modes_per_layer = n_modes_per_layer
+        self.max_n_modes_per_layer = max_n_modes_per_layer
+        self.hidden_channels = hidden_channels
+        self.in_channels = in_channels
+        self.out_channels = out_channels
+        self.lifting_channel_ratio = lifting_channel_ratio
+        self.lifting_channels = int(lifting_channel_ratio * hidden_channels)
+        self.projection_channel_ratio = projection_channel_ratio
+        self.projection_channels = int(projection_channel_ratio * hidden_channels)
+        self.no_br = no_br
+
+        # per-layer spectral convolutions (fno_staged.py:162-190)
+        self.convs = nn.ModuleList([
+            conv_module(
+                hidden_channels, hidden_channels, n_modes=n_modes_per_layer[i],
+                max_n_modes=max_n_modes_per_layer[i],
+                resolution_scaling_factor=(resolution_scaling_factor[i]
+                                           if resolution_scaling_factor is not None else None),
+                rank=rank, fixed_rank_modes=fixed_rank_modes, implementation=implementation,
+                separable=separable, factorization=factorization,
+                fno_block_precision=fno_block_precision, decomposition_kwargs=decomposition_kwargs,
+                complex_data=complex_data,
+                **({"enforce_hermitian_symmetry": enforce_hermitian_symmetry}
+                   if issubclass(conv_module, SpectralConv) else {}))
+            for i in range(L)])
+        for i, conv in enumerate(self.convs):
+            setattr(conv, "profile_prefix", f"fno_blocks/{i}/spectral_conv")
+
+        if positional_embedding == "grid":
+            self.positional_embedding = GridEmbeddingND(
+                in_channels=in_channels, dim=self.n_dim, grid_boundaries=[[0.0, 1.0]] * self.n_dim)
+        elif isinstance(positional_embedding, GridEmbeddingND):
+            self.positional_embedding = positional_embedding
+        elif positional_embedding is None:
+            self.positional_embedding = None
+        else:
+            raise ValueError(
+                f"Error: tried to instantiate FNO positional embedding with {positional_embedding}, "
+                "expected one of 'grid', GridEmbeddingND")
+        self.domain_padding = None
+
+        lifting_in = in_channels + (self.n_dim if self.positional_embedding is not None else 0)
+        self.lifting = ChannelMLP(in_channels=lifting_in, out_channels=hidden_channels,
+                                  hidden_channels=self.lifting_channels, n_layers=2, n_dim=self.n_dim,
+                                  non_linearity=non_linearity)
+        self.projection = ChannelMLP(in_channels=hidden_channels, out_channels=out_channels,
+                                     hidden_channels=self.projection_channels, n_layers=2,
+                                     n_dim=self.n_dim, non_linearity=non_linearity)
+
+    @staticmethod
+    def _bitrev_spatial(x: torch.Tensor) -> torch.Tensor:
+        """Each power-of-two spatial dimension permuted into bit-reversed order
+        (an involution); other dimensions unchanged (fno_staged.py:325-341)."""
+        for dim in range(2, x.ndim):
+            n = x.shape[dim]
+            if n > 1 and (n & (n - 1)) == 0:
+                bits = n.bit_length() - 1
+                idx = torch.arange(n, device=x.device)
+                rev = torch.zeros_like(idx)
+                for i in range(bits):
+                    rev = (rev << 1) | ((idx >> i) & 1)
+                x = torch.index_select(x, dim, rev)
+        return x
+
+    def forward(self, x, output_shape=None, **kwargs):
+        """fno_staged.py:460-502 (without domain padding and the no_br path)."""
+        if kwargs:
+            warnings.warn(
+                f"FNOStaged.forward() received unexpected keyword arguments: {list(kwargs.keys())}. "
+                "These arguments will be ignored.", UserWarning, stacklevel=2)
+        if output_shape is None:
+            output_shape = [None] * self.n_layers
+        elif isinstance(output_shape, tuple):
+            output_shape = [None] * (self.n_layers - 1) + [output_shape]
+        profiler = get_active_profiler()
+        if self.positional_embedding is not None:
+            with maybe_profile(profiler, "fno/positional_embedding", x.device):
+                x = self.positional_embedding(x)
+        with maybe_profile(profiler, "fno/lifting", x.device):
+            x = self.lifting(x)
+        for layer_idx in range(self.n_layers):
+            x = super().forward(x, layer_idx, output_shape=output_shape[layer_idx])
+        with maybe_profile(profiler, "fno/projection", x.device):
+            x = self.projection(x)
+        return x

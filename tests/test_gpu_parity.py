@@ -544,6 +544,24 @@ def test_block_precision_output_dtype(precision, bias, cuda_device):
     assert rel_err(y, ref) <= (TOL if bias else 2e-3)
 
 
+def test_fno_staged_matches_oracle(cuda_device):
+    """FNOStaged with per-layer mode counts against the oracle's FNO forward
+    built from each layer's own parameters."""
+    torch.manual_seed(27)
+    model = na.FNOStaged([(16, 16), (12, 12), (8, 8)], in_channels=1, out_channels=1,
+                         hidden_channels=32).to(cuda_device)
+    with torch.no_grad():
+        for sk in model.channel_mlp_skips:
+            sk.weight.uniform_(0.5, 1.5)
+    x = gaussian_random_field((2, 1, 64, 64), seed=28)
+    with torch.no_grad():
+        y = model(x.to(cuda_device))
+    params = {"lifting": _mlp(model.lifting), "projection": _mlp(model.projection),
+              "layers": [_layer_params(model, i) for i in range(3)]}
+    ref = R.fno_forward(x.double(), params)
+    assert rel_err(y, ref) <= TOL
+
+
 def test_deterministic(cuda_device):
     torch.manual_seed(11)
     conv = na.SpectralConv(64, 64, (64, 64)).to(cuda_device)

@@ -118,3 +118,35 @@ def test_validate_scaling_factor():
     assert na.validate_scaling_factor(2, 2) == [2.0, 2.0]
     assert na.validate_scaling_factor(0.5, 2, 3) == [[0.5, 0.5]] * 3
     assert na.validate_scaling_factor([1, 2], 2) == [1.0, 2.0]
+
+
+def test_fno_staged_construction():
+    """FNOStaged (fno_staged.py:24-190): per-layer mode counts, the
+    reference's argument checks and top-level attribute names."""
+    m = na.FNOStaged([(8, 8), (6, 6), (4, 4)], in_channels=1, out_channels=2, hidden_channels=16)
+    assert m.n_layers == 3
+    assert [c.n_modes for c in m.convs] == [[8, 5], [6, 4], [4, 3]]
+    # max_n_modes_per_layer defaults to the raw per-layer tuples, which
+    # SpectralConv takes as given (not halved): the weights keep those shapes
+    assert [tuple(c.weight.shape[2:]) for c in m.convs] == [(8, 8), (6, 6), (4, 4)]
+    assert {"convs", "fno_skips", "channel_mlp", "channel_mlp_skips", "lifting", "projection"} <= \
+        {k.split(".")[0] for k in m.state_dict()}
+    assert m.lifting.in_channels == 3 and m.projection.out_channels == 2
+    with pytest.raises(ValueError):
+        na.FNOStaged([(8, 8), (6, 6)], in_channels=1, out_channels=1, hidden_channels=8, n_layers=3)
+    with pytest.raises(ValueError):
+        na.FNOStaged([(8, 8), (6, 6)], 1, 1, 8, max_n_modes_per_layer=[(8, 8)])
+    with pytest.raises(NotImplementedError):
+        na.FNOStaged([(8, 8)], 1, 1, 8, no_br=True)
+
+
+def test_fno_staged_bitrev():
+    """_bitrev_spatial is an involution on power-of-two dims and leaves other
+    sizes alone (reference test_fno_staged_no_br.py:32-62)."""
+    x = torch.randn(2, 3, 16, 12)
+    y = na.FNOStaged._bitrev_spatial(x)
+    assert torch.equal(x, na.FNOStaged._bitrev_spatial(y))
+    assert not torch.equal(x, y)
+    assert torch.equal(y[:, :, :, :], x[:, :, [0, 8, 4, 12, 2, 10, 6, 14, 1, 9, 5, 13, 3, 11, 7, 15], :])
+    z = torch.randn(1, 1, 9, 10)
+    assert torch.equal(z, na.FNOStaged._bitrev_spatial(z))
