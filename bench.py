@@ -305,8 +305,8 @@ def main():
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; multi-GPU runs are not part of it "
-                                   "(the block shards by batch with no communication)",
+        print(json.dumps({"error": "this benchmark runs on one GPU only; multi-GPU runs are not part "
+                                   "of it (the block shards by batch with no communication)",
                           "n_gpus": args.gpus}))
         sys.exit(2)
 

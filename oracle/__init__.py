@@ -1,8 +1,8 @@
 """Oracle for the FNO spectral path -- TEST INFRASTRUCTURE ONLY.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
-``bench.py`` may import this package, and only as the checker (or, for the
-CPU baseline, as the thing timed on the host).  The product path in
+``bench.py`` may import this package, and only as the reference results are
+compared against (or, for the CPU baseline, as the thing timed on the host).  The product path in
 ``neuraloperator_amd`` never imports it: the GPU modules fail loudly when the
 HIP library is missing instead of falling back to anything in here.
 

@@ -1,4 +1,4 @@
-"""Pins the oracle (oracle/spectral_ref.py) before it is trusted as the checker.
+"""Pins the oracle (oracle/spectral_ref.py) before the parity tests compare against it.
 
 Each check is chosen so that a plausible mistake fails it:
   * closed-form float64 DFT (oracle/dft64.py)  -> sign, index, shift, window,
