@@ -12,6 +12,7 @@ import torch.nn.functional as F
 from .channel_mlp import ChannelMLP
 from .embeddings import GridEmbeddingND
 from .fno_block import FNOBlocks
+from .padding import DomainPadding
 from .spectral_convolution import SpectralConv
 from .utils import get_active_profiler, maybe_profile
 
@@ -95,8 +96,10 @@ class FNO(nn.Module):
         if domain_padding is not None and (
                 (isinstance(domain_padding, list) and sum(domain_padding) > 0)
                 or (isinstance(domain_padding, (float, int)) and domain_padding > 0)):
-            raise NotImplementedError("domain_padding is not built")
-        self.domain_padding = None
+            self.domain_padding = DomainPadding(domain_padding=domain_padding,
+                                                resolution_scaling_factor=resolution_scaling_factor)
+        else:
+            self.domain_padding = None
 
         if resolution_scaling_factor is not None and isinstance(resolution_scaling_factor, (float, int)):
             resolution_scaling_factor = [resolution_scaling_factor] * self.n_layers
@@ -137,8 +140,14 @@ class FNO(nn.Module):
                 x = self.positional_embedding(x)
         with maybe_profile(profiler, "fno/lifting", x.device):
             x = self.lifting(x)
+        if self.domain_padding is not None:
+            with maybe_profile(profiler, "fno/domain_padding/pad", x.device):
+                x = self.domain_padding.pad(x)
         for layer_idx in range(self.n_layers):
             x = self.fno_blocks(x, layer_idx, output_shape=output_shape[layer_idx])
+        if self.domain_padding is not None:
+            with maybe_profile(profiler, "fno/domain_padding/unpad", x.device):
+                x = self.domain_padding.unpad(x)
         with maybe_profile(profiler, "fno/projection", x.device):
             x = self.projection(x)
         return x

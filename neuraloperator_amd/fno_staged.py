@@ -20,6 +20,7 @@ from torch import nn
 from .channel_mlp import ChannelMLP
 from .embeddings import GridEmbeddingND
 from .fno_block import FNOBlocks
+from .padding import DomainPadding
 from .spectral_convolution import SpectralConv
 from .utils import get_active_profiler, maybe_profile
 
@@ -78,10 +79,11 @@ class FNOStaged(FNOBlocks):
         max_n_modes_per_layer = [list(m) for m in max_n_modes_per_layer]
         if no_br:
             raise NotImplementedError("no_br=True (bit-reversed butterfly spectral path) is not built")
-        if domain_padding is not None and (
-                (isinstance(domain_padding, list) and sum(domain_padding) > 0)
-                or (isinstance(domain_padding, (float, int)) and domain_padding > 0)):
-            raise NotImplementedError("domain_padding is not built")
+        pad_on = domain_padding is not None and (
+            (isinstance(domain_padding, list) and sum(domain_padding) > 0)
+            or (isinstance(domain_padding, (float, int)) and domain_padding > 0))
+        # the padding takes the factor as given (fno_staged.py:143-157)
+        raw_scaling = resolution_scaling_factor
         if resolution_scaling_factor is not None and isinstance(resolution_scaling_factor,
                                                                 (float, int)):
             resolution_scaling_factor = [resolution_scaling_factor] * L
@@ -139,7 +141,9 @@ class FNOStaged(FNOBlocks):
             raise ValueError(
                 f"Error: tried to instantiate FNO positional embedding with {positional_embedding}, "
                 "expected one of 'grid', GridEmbeddingND")
-        self.domain_padding = None
+        self.domain_padding = (DomainPadding(domain_padding=domain_padding,
+                                             resolution_scaling_factor=raw_scaling)
+                               if pad_on else None)
 
         lifting_in = in_channels + (self.n_dim if self.positional_embedding is not None else 0)
         self.lifting = ChannelMLP(in_channels=lifting_in, out_channels=hidden_channels,
@@ -165,7 +169,7 @@ class FNOStaged(FNOBlocks):
         return x
 
     def forward(self, x, output_shape=None, **kwargs):
-        """fno_staged.py:460-502 (without domain padding and the no_br path)."""
+        """fno_staged.py:460-502 (without the no_br path)."""
         if kwargs:
             warnings.warn(
                 f"FNOStaged.forward() received unexpected keyword arguments: {list(kwargs.keys())}. "
@@ -180,8 +184,14 @@ class FNOStaged(FNOBlocks):
                 x = self.positional_embedding(x)
         with maybe_profile(profiler, "fno/lifting", x.device):
             x = self.lifting(x)
+        if self.domain_padding is not None:
+            with maybe_profile(profiler, "fno/domain_padding/pad", x.device):
+                x = self.domain_padding.pad(x)
         for layer_idx in range(self.n_layers):
             x = super().forward(x, layer_idx, output_shape=output_shape[layer_idx])
+        if self.domain_padding is not None:
+            with maybe_profile(profiler, "fno/domain_padding/unpad", x.device):
+                x = self.domain_padding.unpad(x)
         with maybe_profile(profiler, "fno/projection", x.device):
             x = self.projection(x)
         return x

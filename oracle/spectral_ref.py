@@ -489,18 +489,40 @@ def fno_block_forward(x, index, n_layers, conv: dict, fno_skip: Optional[dict], 
     return x
 
 
+def domain_pad(x, fractions):
+    """DomainPadding.pad without resolution scaling (padding.py:54-138):
+    round(p * n) zeros on both sides of every spatial axis."""
+    pads = [round(p * n) for p, n in zip(fractions, x.shape[2:])]
+    flat = []
+    for p in reversed(pads):
+        flat += [p, p]
+    return F.pad(x, flat, mode="constant"), pads
+
+
+def domain_unpad(x, pads):
+    """DomainPadding.unpad (padding.py:140-150)."""
+    return x[(Ellipsis,) + tuple(slice(p, -p) if p else slice(None) for p in pads)]
+
+
 def fno_forward(x, params: dict):
-    """FNO.forward (fno.py:342-408): grid embedding, lifting, blocks, projection.
+    """FNO.forward (fno.py:342-408): grid embedding, lifting, domain padding,
+    blocks, unpadding, projection.
 
     ``params`` = {"lifting": {"weights", "biases"}, "projection": {...},
-    "layers": [ {conv, fno_skip, mlp, mlp_skip}, ...], "positional_embedding": bool}
+    "layers": [ {conv, fno_skip, mlp, mlp_skip}, ...], "positional_embedding": bool,
+    "domain_padding": per-axis fractions or None}
     """
     if params.get("positional_embedding", True):
         x = grid_embedding_nd(x)
     x = channel_mlp(x, params["lifting"]["weights"], params["lifting"]["biases"])
+    pads = None
+    if params.get("domain_padding") is not None:
+        x, pads = domain_pad(x, params["domain_padding"])
     n_layers = len(params["layers"])
     for i, layer in enumerate(params["layers"]):
         x = fno_block_forward(x, i, n_layers, layer["conv"], layer.get("fno_skip"),
                               layer.get("mlp"), layer.get("mlp_skip"))
+    if pads is not None:
+        x = domain_unpad(x, pads)
     x = channel_mlp(x, params["projection"]["weights"], params["projection"]["biases"])
     return x

@@ -562,6 +562,28 @@ def test_fno_staged_matches_oracle(cuda_device):
     assert rel_err(y, ref) <= TOL
 
 
+@pytest.mark.parametrize("domain_padding", [0.1, [0.1, 0.2]])
+def test_fno_domain_padding(domain_padding, cuda_device):
+    """FNO with domain padding (reference test_fno.py:219-253): output size kept,
+    values against the oracle (pad after lifting, unpad before projection)."""
+    torch.manual_seed(29)
+    model = na.FNO((5, 5), in_channels=3, out_channels=1, hidden_channels=9, n_layers=2,
+                   domain_padding=domain_padding).to(cuda_device)
+    with torch.no_grad():
+        for sk in model.fno_blocks.channel_mlp_skips:
+            sk.weight.uniform_(0.5, 1.5)
+    x = torch.randn(3, 3, 12, 12)
+    with torch.no_grad():
+        y = model(x.to(cuda_device))
+    assert list(y.shape) == [3, 1, 12, 12]
+    fr = domain_padding if isinstance(domain_padding, list) else [domain_padding] * 2
+    params = {"lifting": _mlp(model.lifting), "projection": _mlp(model.projection),
+              "layers": [_layer_params(model.fno_blocks, i) for i in range(2)],
+              "domain_padding": fr}
+    ref = R.fno_forward(x.double(), params)
+    assert rel_err(y, ref) <= TOL
+
+
 def test_deterministic(cuda_device):
     torch.manual_seed(11)
     conv = na.SpectralConv(64, 64, (64, 64)).to(cuda_device)

@@ -117,6 +117,18 @@ def test_complex_data_plane_wave(sizes, nm, f_in, j, f_out):
     assert torch.allclose(y, expect, atol=1e-12)
 
 
+def test_domain_padding_restatement():
+    """Padding puts round(p * n) zeros on both sides and unpadding returns the
+    original field (padding.py:54-150); the reference's FNO test keeps the
+    output size (test_fno.py:219-253)."""
+    x = torch.randn(2, 3, 12, 10, dtype=torch.float64)
+    y, pads = R.domain_pad(x, [0.1, 0.2])
+    assert pads == [1, 2] and list(y.shape) == [2, 3, 14, 14]
+    assert torch.equal(y[:, :, :1], torch.zeros_like(y[:, :, :1]))
+    assert torch.equal(y[:, :, :, -2:], torch.zeros_like(y[:, :, :, -2:]))
+    assert torch.equal(R.domain_unpad(y, pads), x)
+
+
 def test_circular_shift_equivariance():
     torch.manual_seed(2)
     nms = R.stored_n_modes((6, 6))
