@@ -80,7 +80,7 @@ const char* fno_last_error(void) { return last_error_cstr(); }
 
 size_t fno_rfft_window_workspace_bytes(int64_t planes, int32_t ndim, const int32_t* sizes,
                                        const int32_t* modes) {
-  if (!sizes || !modes || ndim < 1 || ndim > 3) return 0;
+  if (!sizes || !modes || ndim < 1 || ndim > 4) return 0;
   return rfft_window_ws(planes, ndim, sizes, modes);
 }
 
@@ -119,7 +119,7 @@ int fno_contract_dense_c64(const void* xhat, const void* w, void* yhat, int32_t 
 
 size_t fno_contract_tucker_workspace_bytes(int32_t batch, int32_t ndim, const int32_t* modes,
                                            const int32_t* ranks) {
-  if (!modes || !ranks || ndim < 1 || ndim > 3) return 0;
+  if (!modes || !ranks || ndim < 1 || ndim > 4) return 0;
   const int64_t M = mode_count(ndim, modes);
   int64_t big = (int64_t)ranks[0] * ranks[1];
   for (int d = 0; d < ndim; ++d) big *= (modes[d] > ranks[2 + d] ? modes[d] : ranks[2 + d]);
@@ -134,7 +134,7 @@ int fno_contract_tucker_c64(const void* xhat, const void* core, const void* cons
                             void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
   FNO_CHECK_ARG(xhat && core && factors && ranks && yhat && modes, "NULL argument");
-  FNO_CHECK_ARG(ndim >= 1 && ndim <= 3, "ndim must be 1..3");
+  FNO_CHECK_ARG(ndim >= 1 && ndim <= 4, "ndim must be 1..4");
   for (int d = 0; d < ndim + 2; ++d) {
     FNO_CHECK_ARG(factors[d], "factor %d is NULL", d);
     FNO_CHECK_ARG(ranks[d] >= 1, "rank %d must be positive", d);
@@ -184,7 +184,7 @@ int fno_contract_tucker_c64(const void* xhat, const void* core, const void* cons
 
 size_t fno_irfft_window_workspace_bytes(int64_t planes, int32_t ndim, const int32_t* out_sizes,
                                         const int32_t* modes) {
-  if (!out_sizes || !modes || ndim < 1 || ndim > 3) return 0;
+  if (!out_sizes || !modes || ndim < 1 || ndim > 4) return 0;
   return irfft_window_ws(planes, ndim, out_sizes, modes);
 }
 
@@ -212,7 +212,7 @@ int fno_irfft_window_f32(const void* yhat, const float* bias, float* y, int64_t 
 
 // complex data: every axis keeps at most its own length in modes
 static int validate_complex_window(int32_t ndim, const int32_t* sizes, const int32_t* modes) {
-  FNO_CHECK_ARG(ndim >= 1 && ndim <= 3, "ndim must be 1..3 (got %d)", ndim);
+  FNO_CHECK_ARG(ndim >= 1 && ndim <= 4, "ndim must be 1..4 (got %d)", ndim);
   FNO_CHECK_ARG(sizes && modes, "sizes/modes must not be NULL");
   for (int d = 0; d < ndim; ++d) {
     FNO_CHECK_ARG(sizes[d] >= 1 && sizes[d] <= 4096, "size[%d]=%d outside [1, 4096]", d, sizes[d]);
@@ -224,7 +224,7 @@ static int validate_complex_window(int32_t ndim, const int32_t* sizes, const int
 
 size_t fno_fft_window_workspace_bytes(int64_t planes, int32_t ndim, const int32_t* sizes,
                                       const int32_t* modes) {
-  if (!sizes || !modes || ndim < 1 || ndim > 3) return 0;
+  if (!sizes || !modes || ndim < 1 || ndim > 4) return 0;
   return fft_window_c2c_ws(planes, ndim, sizes, modes);
 }
 
@@ -245,7 +245,7 @@ int fno_fft_window_c64(const void* x, void* xhat, int64_t planes, int32_t ndim,
 
 size_t fno_ifft_window_workspace_bytes(int64_t planes, int32_t ndim, const int32_t* out_sizes,
                                        const int32_t* modes) {
-  if (!out_sizes || !modes || ndim < 1 || ndim > 3) return 0;
+  if (!out_sizes || !modes || ndim < 1 || ndim > 4) return 0;
   return ifft_window_c2c_ws(planes, ndim, out_sizes, modes);
 }
 
@@ -333,7 +333,7 @@ int fno_spectral_block_is_fused(int32_t batch, int32_t in_channels, int32_t out_
 size_t fno_spectral_block_workspace_bytes(int32_t batch, int32_t in_channels,
                                           int32_t out_channels, int32_t ndim,
                                           const int32_t* sizes, const int32_t* modes) {
-  if (!sizes || !modes || ndim < 1 || ndim > 3) return 0;
+  if (!sizes || !modes || ndim < 1 || ndim > 4) return 0;
   size_t fused = 0;
   if (ndim == 2) fused = fast2d_workspace(batch, in_channels, out_channels, sizes, modes);
   const int64_t M = mode_count(ndim, modes);

@@ -409,7 +409,7 @@ static int grid_for(int64_t total) {
 }
 
 static int validate_axes(int32_t ndim, const int32_t* sizes, const int32_t* modes) {
-  FNO_CHECK_ARG(ndim >= 1 && ndim <= 3, "ndim must be 1..3 (got %d)", ndim);
+  FNO_CHECK_ARG(ndim >= 1 && ndim <= 4, "ndim must be 1..4 (got %d)", ndim);
   FNO_CHECK_ARG(sizes && modes, "sizes/modes must not be NULL");
   for (int d = 0; d < ndim; ++d) {
     FNO_CHECK_ARG(sizes[d] >= 1, "size[%d]=%d must be positive", d, sizes[d]);
@@ -435,6 +435,38 @@ static int64_t fwd_stage_elems(int64_t planes, int32_t ndim, const int32_t* size
   return e;
 }
 
+// Intermediate stages of a window transform alternate between two workspace
+// buffers (one for 2 axes, none for 1), each as large as the largest of them.
+static int stage_buffers(int32_t ndim) { return ndim >= 3 ? 2 : ndim - 1; }
+
+static int64_t fwd_buffer_elems(int64_t planes, int32_t ndim, const int32_t* sizes,
+                                const int32_t* modes) {
+  int64_t e = 0;
+  for (int d = 1; d < ndim; ++d) {   // axis d done (stages before the last)
+    const int64_t s = fwd_stage_elems(planes, ndim, sizes, modes, d);
+    if (s > e) e = s;
+  }
+  return e;
+}
+
+// the inverse stage that has expanded axes 0..d to their output lengths
+static int64_t inv_stage_elems(int64_t planes, int32_t ndim, const int32_t* out_sizes,
+                               const int32_t* modes, int d) {
+  int64_t e = planes;
+  for (int a = 0; a < ndim; ++a) e *= (a <= d) ? out_sizes[a] : modes[a];
+  return e;
+}
+
+static int64_t inv_buffer_elems(int64_t planes, int32_t ndim, const int32_t* out_sizes,
+                                const int32_t* modes) {
+  int64_t e = 0;
+  for (int d = 0; d + 1 < ndim; ++d) {
+    const int64_t s = inv_stage_elems(planes, ndim, out_sizes, modes, d);
+    if (s > e) e = s;
+  }
+  return e;
+}
+
 // line-FFT last-axis transforms (fno_generic_fft.hip)
 bool r2c_fft_supported(int N, int m, int64_t rows);
 int r2c_fft(const float* x, float2* out, int64_t rows, int N, int m, float scale, hipStream_t st);
@@ -452,15 +484,14 @@ int rfft_window(const float* x, float2* xhat, int64_t planes, int32_t ndim, cons
   // stage s transforms axis (ndim-1-s); stage outputs go to the workspace
   // (two alternating buffers), the last one to xhat.
   const double scale = forward_scale(norm, sizes, ndim);
-  const int64_t e0 = fwd_stage_elems(planes, ndim, sizes, modes, ndim - 1);
-  const int64_t e1 = ndim == 3 ? fwd_stage_elems(planes, ndim, sizes, modes, ndim - 2) : 0;
-  const size_t need = (ndim > 1 ? (size_t)e0 * sizeof(float2) : 0) + (size_t)e1 * sizeof(float2);
+  const int64_t eb = fwd_buffer_elems(planes, ndim, sizes, modes);
+  const size_t need = (size_t)stage_buffers(ndim) * eb * sizeof(float2);
   if (ws_bytes < need) {
     set_error("rfft_window: workspace %zu < %zu bytes", ws_bytes, need);
     return FNO_ERR_WORKSPACE;
   }
-  float2* bufA = reinterpret_cast<float2*>(ws);
-  float2* bufB = bufA + e0;
+  float2* bufs[2] = {reinterpret_cast<float2*>(ws), reinterpret_cast<float2*>(ws) + eb};
+  float2* bufA = bufs[0];
   // last axis
   {
     const int N = sizes[ndim - 1], m = modes[ndim - 1];
@@ -487,7 +518,7 @@ int rfft_window(const float* x, float2* xhat, int64_t planes, int32_t ndim, cons
       if (rc) return rc;
     }
   }
-  // middle axes, innermost first
+  // the other axes, innermost first; stage s = ndim - 1 - d writes bufs[s % 2]
   const float2* src = bufA;
   for (int d = ndim - 2; d >= 0; --d) {
     int64_t outer = planes;
@@ -495,7 +526,7 @@ int rfft_window(const float* x, float2* xhat, int64_t planes, int32_t ndim, cons
     int64_t inner = 1;
     for (int a = d + 1; a < ndim; ++a) inner *= modes[a];
     const int N = sizes[d], m = modes[d];
-    float2* dst = (d == 0) ? xhat : bufB;
+    float2* dst = (d == 0) ? xhat : bufs[(ndim - 1 - d) % 2];
     const float sc = (d == 0) ? (float)scale : 1.f;
     int rc;
     if (c2c_fft_supported(N, outer, inner)) {
@@ -554,21 +585,20 @@ int fft_window_c2c(const float2* x, float2* xhat, int64_t planes, int32_t ndim,
                    const int32_t* sizes, const int32_t* modes, int32_t norm, void* ws,
                    size_t ws_bytes, hipStream_t st) {
   const double scale = forward_scale(norm, sizes, ndim);
-  const int64_t e0 = fwd_stage_elems(planes, ndim, sizes, modes, ndim - 1);
-  const int64_t e1 = ndim == 3 ? fwd_stage_elems(planes, ndim, sizes, modes, ndim - 2) : 0;
-  const size_t need = (ndim > 1 ? (size_t)e0 * sizeof(float2) : 0) + (size_t)e1 * sizeof(float2);
+  const int64_t eb = fwd_buffer_elems(planes, ndim, sizes, modes);
+  const size_t need = (size_t)stage_buffers(ndim) * eb * sizeof(float2);
   if (ws_bytes < need) {
     set_error("fft_window: workspace %zu < %zu bytes", ws_bytes, need);
     return FNO_ERR_WORKSPACE;
   }
-  float2* bufs[2] = {reinterpret_cast<float2*>(ws), reinterpret_cast<float2*>(ws) + e0};
+  float2* bufs[2] = {reinterpret_cast<float2*>(ws), reinterpret_cast<float2*>(ws) + eb};
   const float2* src = x;
   for (int d = ndim - 1, stage = 0; d >= 0; --d, ++stage) {
     int64_t outer = planes;
     for (int a = 0; a < d; ++a) outer *= sizes[a];
     int64_t inner = 1;
     for (int a = d + 1; a < ndim; ++a) inner *= modes[a];
-    float2* dst = (d == 0) ? xhat : bufs[stage];
+    float2* dst = (d == 0) ? xhat : bufs[stage % 2];
     const int rc = c2c_axis_fwd(src, dst, outer, sizes[d], inner, modes[d],
                                 complex_fwd_off(d, ndim, sizes[d], modes[d]),
                                 d == 0 ? (float)scale : 1.f, st);
@@ -579,10 +609,7 @@ int fft_window_c2c(const float2* x, float2* xhat, int64_t planes, int32_t ndim,
 }
 
 size_t fft_window_c2c_ws(int64_t planes, int32_t ndim, const int32_t* sizes, const int32_t* modes) {
-  if (ndim <= 1) return 0;
-  size_t e = (size_t)fwd_stage_elems(planes, ndim, sizes, modes, ndim - 1);
-  if (ndim == 3) e += (size_t)fwd_stage_elems(planes, ndim, sizes, modes, ndim - 2);
-  return e * sizeof(float2);
+  return (size_t)stage_buffers(ndim) * fwd_buffer_elems(planes, ndim, sizes, modes) * sizeof(float2);
 }
 
 int ifft_window_c2c(const float2* yhat, const float* bias, float2* y, int64_t batch,
@@ -591,18 +618,13 @@ int ifft_window_c2c(const float2* yhat, const float* bias, float2* y, int64_t ba
                     size_t ws_bytes, hipStream_t st) {
   const int64_t planes = batch * channels;
   const double scale = inverse_scale(norm, out_sizes, ndim);
-  int64_t eA = 0, eB = 0;
-  if (ndim >= 2) {
-    eA = planes * out_sizes[0];
-    for (int a = 1; a < ndim; ++a) eA *= modes[a];
-  }
-  if (ndim == 3) eB = planes * out_sizes[0] * out_sizes[1] * modes[2];
-  const size_t need = (size_t)(eA + eB) * sizeof(float2);
+  const int64_t eb = inv_buffer_elems(planes, ndim, out_sizes, modes);
+  const size_t need = (size_t)stage_buffers(ndim) * eb * sizeof(float2);
   if (ws_bytes < need) {
     set_error("ifft_window: workspace %zu < %zu bytes", ws_bytes, need);
     return FNO_ERR_WORKSPACE;
   }
-  float2* bufs[2] = {reinterpret_cast<float2*>(ws), reinterpret_cast<float2*>(ws) + eA};
+  float2* bufs[2] = {reinterpret_cast<float2*>(ws), reinterpret_cast<float2*>(ws) + eb};
   const float2* src = yhat;
   for (int d = 0; d < ndim; ++d) {
     int64_t outer = planes;
@@ -610,7 +632,7 @@ int ifft_window_c2c(const float2* yhat, const float* bias, float2* y, int64_t ba
     int64_t inner = 1;
     for (int a = d + 1; a < ndim; ++a) inner *= modes[a];
     const bool last = d == ndim - 1;
-    float2* dst = last ? y : bufs[d];
+    float2* dst = last ? y : bufs[d % 2];
     const int off = last ? 0 : -(modes[d] / 2);
     const int rc = c2c_axis_inv(src, dst, outer, in_sizes[d], out_sizes[d], inner, modes[d], off,
                                 last ? (float)scale : 1.f, st);
@@ -629,13 +651,8 @@ int ifft_window_c2c(const float2* yhat, const float* bias, float2* y, int64_t ba
 
 size_t ifft_window_c2c_ws(int64_t planes, int32_t ndim, const int32_t* out_sizes,
                           const int32_t* modes) {
-  int64_t eA = 0, eB = 0;
-  if (ndim >= 2) {
-    eA = planes * out_sizes[0];
-    for (int a = 1; a < ndim; ++a) eA *= modes[a];
-  }
-  if (ndim == 3) eB = planes * out_sizes[0] * out_sizes[1] * modes[2];
-  return (size_t)(eA + eB) * sizeof(float2);
+  return (size_t)stage_buffers(ndim) * inv_buffer_elems(planes, ndim, out_sizes, modes) *
+         sizeof(float2);
 }
 
 int irfft_window(const float2* yhat, const float* bias, float* y, int64_t batch, int32_t channels,
@@ -644,27 +661,21 @@ int irfft_window(const float2* yhat, const float* bias, float* y, int64_t batch,
                  hipStream_t st) {
   const int64_t planes = batch * channels;
   const double scale = inverse_scale(norm, out_sizes, ndim);
-  // stage d (d < ndim-1) expands axis d to out_sizes[d]
-  int64_t eA = 0, eB = 0;
-  if (ndim >= 2) {
-    eA = planes * out_sizes[0];
-    for (int a = 1; a < ndim; ++a) eA *= modes[a];
-  }
-  if (ndim == 3) eB = planes * out_sizes[0] * out_sizes[1] * modes[2];
-  const size_t need = (size_t)(eA + eB) * sizeof(float2);
+  // stage d (d < ndim-1) expands axis d to out_sizes[d] into bufs[d % 2]
+  const int64_t eb = inv_buffer_elems(planes, ndim, out_sizes, modes);
+  const size_t need = (size_t)stage_buffers(ndim) * eb * sizeof(float2);
   if (ws_bytes < need) {
     set_error("irfft_window: workspace %zu < %zu bytes", ws_bytes, need);
     return FNO_ERR_WORKSPACE;
   }
-  float2* bufA = reinterpret_cast<float2*>(ws);
-  float2* bufB = bufA + eA;
+  float2* bufs[2] = {reinterpret_cast<float2*>(ws), reinterpret_cast<float2*>(ws) + eb};
   const float2* src = yhat;
   for (int d = 0; d < ndim - 1; ++d) {
     int64_t outer = planes;
     for (int a = 0; a < d; ++a) outer *= out_sizes[a];
     int64_t inner = 1;
     for (int a = d + 1; a < ndim; ++a) inner *= modes[a];
-    float2* dst = (d == 0) ? bufA : bufB;
+    float2* dst = bufs[d % 2];
     const int N = in_sizes[d], Np = out_sizes[d], m = modes[d];
     int rc;
     if (c2c_fft_supported(Np, outer, inner)) {
@@ -800,21 +811,13 @@ int validate_window(int32_t ndim, const int32_t* sizes, const int32_t* modes) {
 }
 
 size_t rfft_window_ws(int64_t planes, int32_t ndim, const int32_t* sizes, const int32_t* modes) {
-  if (ndim <= 1) return 0;
-  size_t e = (size_t)fwd_stage_elems(planes, ndim, sizes, modes, ndim - 1);
-  if (ndim == 3) e += (size_t)fwd_stage_elems(planes, ndim, sizes, modes, ndim - 2);
-  return e * sizeof(float2);
+  return (size_t)stage_buffers(ndim) * fwd_buffer_elems(planes, ndim, sizes, modes) * sizeof(float2);
 }
 
 size_t irfft_window_ws(int64_t planes, int32_t ndim, const int32_t* out_sizes,
                        const int32_t* modes) {
-  int64_t eA = 0, eB = 0;
-  if (ndim >= 2) {
-    eA = planes * out_sizes[0];
-    for (int a = 1; a < ndim; ++a) eA *= modes[a];
-  }
-  if (ndim == 3) eB = planes * out_sizes[0] * out_sizes[1] * modes[2];
-  return (size_t)(eA + eB) * sizeof(float2);
+  return (size_t)stage_buffers(ndim) * inv_buffer_elems(planes, ndim, out_sizes, modes) *
+         sizeof(float2);
 }
 
 }  // namespace fno

@@ -584,6 +584,45 @@ def test_fno_domain_padding(domain_padding, cuda_device):
     assert rel_err(y, ref) <= TOL
 
 
+@pytest.mark.parametrize("kind", ["dense", "tucker-factorized", "cp", "separable", "complex"])
+def test_spectral_conv_4d(kind, cuda_device):
+    """Four spatial axes (reference test_spectral_convolution.py:10, dim 4):
+    the window transforms alternate their two stage buffers over four axes."""
+    print(f"4d {kind}", flush=True)
+    torch.manual_seed(30)
+    C, sizes, nm = 3, (6, 8, 5, 8), (4, 4, 4, 4)
+    kw = {}
+    if kind == "tucker-factorized":
+        kw = dict(factorization="Tucker", rank=0.5, implementation="factorized")
+    elif kind == "cp":
+        kw = dict(factorization="CP", rank=0.5)
+    elif kind == "separable":
+        kw = dict(separable=True)
+    elif kind == "complex":
+        kw = dict(complex_data=True)
+    conv = na.SpectralConv(C, C, nm, **kw).to(cuda_device)
+    with torch.no_grad():
+        conv.bias.normal_()
+    dtype = torch.complex64 if kind == "complex" else torch.float32
+    x = torch.randn(2, C, *sizes, dtype=dtype)
+    with torch.no_grad():
+        y = conv(x.to(cuda_device))
+    if kind == "tucker-factorized":
+        w = {"tucker": (conv.weight.core.detach().cpu().to(torch.complex128),
+                        [f.detach().cpu().to(torch.complex128) for f in conv.weight.factors])}
+        extra = dict(implementation="factorized")
+    else:
+        w = conv.weight.to_tensor().detach().cpu().to(torch.complex128)
+        extra = {}
+    ref = R.spectral_conv_forward(x.to(torch.complex128 if kind == "complex" else torch.float64), w,
+                                  conv.bias.detach().cpu().double(), conv.n_modes, conv.max_n_modes,
+                                  separable=(kind == "separable"), complex_data=(kind == "complex"),
+                                  **extra)
+    if kind == "complex":
+        y, ref = torch.view_as_real(y), torch.view_as_real(ref)
+    assert rel_err(y, ref) <= TOL
+
+
 def test_deterministic(cuda_device):
     torch.manual_seed(11)
     conv = na.SpectralConv(64, 64, (64, 64)).to(cuda_device)
