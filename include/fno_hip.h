@@ -13,6 +13,7 @@
  *   - The library allocates no device memory: scratch space is the caller's
  *     `workspace` of at least the size the matching *_workspace_bytes() call
  *     reports.
+ *   - ndim (spatial axes) is 1..4, each axis 1..4096 points.
  *   - Spectrum window layout ("window order"): along every axis but the last,
  *     window index j holds frequency j - m/2 (integer division), which is the
  *     fftshift-ed order the reference's weights use; along the last (rfft)
