@@ -11,6 +11,7 @@ import torch.nn.functional as F
 
 from .channel_mlp import ChannelMLP
 from .embeddings import GridEmbeddingND
+from .complex import ComplexValued
 from .fno_block import FNOBlocks
 from .padding import DomainPadding
 from .spectral_convolution import SpectralConv
@@ -124,6 +125,9 @@ class FNO(nn.Module):
         self.projection = ChannelMLP(in_channels=self.hidden_channels, out_channels=out_channels,
                                      hidden_channels=self.projection_channels, n_layers=2,
                                      n_dim=self.n_dim, non_linearity=non_linearity)
+        if complex_data:   # fno.py:327-340
+            self.lifting = ComplexValued(self.lifting)
+            self.projection = ComplexValued(self.projection)
 
     def forward(self, x, output_shape=None, **kwargs):
         """fno.py:342-408."""

@@ -21,6 +21,7 @@ from torch import nn
 from . import _native as nat
 from . import functional as Fh
 from .channel_mlp import ChannelMLP
+from .complex import CGELU, ComplexValued, ctanh
 from .skip_connections import Flattened1dConv, SoftGating, skip_connection
 from .spectral_convolution import SpectralConv, _attach
 from .utils import get_active_profiler, maybe_profile, validate_scaling_factor
@@ -118,9 +119,9 @@ class FNOBlocks(nn.Module):
         self.preactivation = preactivation
         self.ada_in_features = ada_in_features
         self.enforce_hermitian_symmetry = enforce_hermitian_symmetry
-        if complex_data:
-            raise NotImplementedError("complex_data=True FNO blocks are not built")
-        self.non_linearity = non_linearity
+        self.complex_data = complex_data
+        # complex data: CGELU and complex-linear wrappers (fno_block.py:169-171, :226-302)
+        self.non_linearity = CGELU if complex_data else non_linearity
 
         self.convs = nn.ModuleList([
             conv_module(
@@ -183,6 +184,14 @@ class FNOBlocks(nn.Module):
             raise ValueError(f"Got norm={norm} but expected None or one of "
                              "[instance_norm, group_norm, batch_norm, ada_in]")
 
+        if complex_data:
+            wrap = lambda ms: nn.ModuleList([ComplexValued(m) for m in ms]) if ms is not None else None
+            self.fno_skips = wrap(self.fno_skips)
+            if self.use_channel_mlp:
+                self.channel_mlp = wrap(self.channel_mlp)
+                self.channel_mlp_skips = wrap(self.channel_mlp_skips)
+            self.norm = wrap(self.norm)
+
     # ------------------------------------------------------------------ fused
     def _fused_skip(self, index):
         """(skip_kind, skip_weight) if the fno skip can run inside the kernel."""
@@ -199,7 +208,7 @@ class FNOBlocks(nn.Module):
 
     def _can_fuse(self, x, index, output_shape):
         conv = self.convs[index]
-        if not isinstance(conv, SpectralConv) or not x.is_cuda:
+        if not isinstance(conv, SpectralConv) or not x.is_cuda or x.is_complex():
             return False
         if _needs_grad(self, x):
             return False   # the composed path carries the gradients
@@ -273,7 +282,7 @@ class FNOBlocks(nn.Module):
                     x_skip_fno = self.fno_skips[index](x)
                     x_skip_fno = self.convs[index].transform(x_skip_fno, output_shape=output_shape)
             if self.stabilizer == "tanh":
-                x = torch.tanh(x)
+                x = ctanh(x) if x.is_complex() else torch.tanh(x)
             x_fno = self.convs[index](x, output_shape=output_shape)
             if self.norm is not None:
                 x_fno = self.norm[self.n_norms * index](x_fno)
@@ -320,7 +329,7 @@ class FNOBlocks(nn.Module):
             x_skip_channel_mlp = self.convs[index].transform(self.channel_mlp_skips[index](x),
                                                              output_shape=output_shape)
         if self.stabilizer == "tanh":
-            x = torch.tanh(x)
+            x = ctanh(x) if x.is_complex() else torch.tanh(x)
         x_fno = self.convs[index](x, output_shape=output_shape)
         x = x_fno + x_skip_fno if self.fno_skips is not None else x_fno
         if index < (self.n_layers - 1):

@@ -18,6 +18,7 @@ import torch.nn.functional as F
 from torch import nn
 
 from .channel_mlp import ChannelMLP
+from .complex import ComplexValued
 from .embeddings import GridEmbeddingND
 from .fno_block import FNOBlocks
 from .padding import DomainPadding
@@ -152,6 +153,9 @@ class FNOStaged(FNOBlocks):
         self.projection = ChannelMLP(in_channels=hidden_channels, out_channels=out_channels,
                                      hidden_channels=self.projection_channels, n_layers=2,
                                      n_dim=self.n_dim, non_linearity=non_linearity)
+        if complex_data:   # fno_staged.py:349-366
+            self.lifting = ComplexValued(self.lifting)
+            self.projection = ComplexValued(self.projection)
 
     @staticmethod
     def _bitrev_spatial(x: torch.Tensor) -> torch.Tensor:

@@ -442,12 +442,32 @@ def spectral_block_forward(x, conv: dict, ws, activation=True):
     return gelu(y) if activation else y
 
 
+def cgelu(x):
+    """CGELU (layers/complex.py:8-27): GELU on the real and imaginary parts."""
+    return torch.complex(gelu(x.real), gelu(x.imag))
+
+
+def complex_apply(fr, fi, x):
+    """apply_complex (layers/complex.py:54-63): the real maps fr, fi as the
+    complex-linear map fr + i fi."""
+    return torch.complex(fr(x.real) - fi(x.imag), fr(x.imag) + fi(x.real))
+
+
 def fno_block_forward(x, index, n_layers, conv: dict, fno_skip: Optional[dict], mlp: Optional[dict],
                       mlp_skip: Optional[dict], non_linearity=gelu, output_shape=None):
     """FNOBlocks.forward_with_postactivation (fno_block.py:327-381) without
     norms/stabilizer.  ``fno_skip``/``mlp_skip`` are {"type": "linear", "w": ..}
     or {"type": "soft-gating", "w": .., "b": ..} or {"type": "identity"} or None."""
+    complex_data = conv.get("complex_data", False)
+
     def apply_skip(s, inp):
+        if complex_data and s["type"] != "identity":
+            # ComplexValued skip (fno_block.py:226-227): real and imaginary copies
+            real = lambda part: (lambda t: real_skip(dict(part, type=s["type"]), t))
+            return complex_apply(real(s["fr"]), real(s["fi"]), inp)
+        return real_skip(s, inp)
+
+    def real_skip(s, inp):
         if s["type"] == "linear":
             return linear_skip(inp, s["w"])
         if s["type"] == "soft-gating":
@@ -481,7 +501,11 @@ def fno_block_forward(x, index, n_layers, conv: dict, fno_skip: Optional[dict], 
     if index < n_layers - 1:
         x = non_linearity(x)
     if mlp is not None:
-        x = channel_mlp(x, mlp["weights"], mlp["biases"], non_linearity)
+        if complex_data:
+            x = complex_apply(lambda t: channel_mlp(t, mlp["fr"]["weights"], mlp["fr"]["biases"]),
+                              lambda t: channel_mlp(t, mlp["fi"]["weights"], mlp["fi"]["biases"]), x)
+        else:
+            x = channel_mlp(x, mlp["weights"], mlp["biases"], non_linearity)
         if x_skip_mlp is not None:
             x = x + x_skip_mlp
     if index < n_layers - 1:
@@ -512,17 +536,25 @@ def fno_forward(x, params: dict):
     "layers": [ {conv, fno_skip, mlp, mlp_skip}, ...], "positional_embedding": bool,
     "domain_padding": per-axis fractions or None}
     """
+    complex_data = params.get("complex_data", False)
+
+    def mlp(p, t):
+        if complex_data:   # ComplexValued lifting / projection (fno.py:327-340)
+            return complex_apply(lambda u: channel_mlp(u, p["fr"]["weights"], p["fr"]["biases"]),
+                                 lambda u: channel_mlp(u, p["fi"]["weights"], p["fi"]["biases"]), t)
+        return channel_mlp(t, p["weights"], p["biases"])
+
     if params.get("positional_embedding", True):
         x = grid_embedding_nd(x)
-    x = channel_mlp(x, params["lifting"]["weights"], params["lifting"]["biases"])
+    x = mlp(params["lifting"], x)
     pads = None
     if params.get("domain_padding") is not None:
         x, pads = domain_pad(x, params["domain_padding"])
     n_layers = len(params["layers"])
     for i, layer in enumerate(params["layers"]):
         x = fno_block_forward(x, i, n_layers, layer["conv"], layer.get("fno_skip"),
-                              layer.get("mlp"), layer.get("mlp_skip"))
+                              layer.get("mlp"), layer.get("mlp_skip"),
+                              non_linearity=cgelu if complex_data else gelu)
     if pads is not None:
         x = domain_unpad(x, pads)
-    x = channel_mlp(x, params["projection"]["weights"], params["projection"]["biases"])
-    return x
+    return mlp(params["projection"], x)

@@ -623,6 +623,46 @@ def test_spectral_conv_4d(kind, cuda_device):
     assert rel_err(y, ref) <= TOL
 
 
+def _complex_layer_params(blocks, i):
+    conv = blocks.convs[i]
+    d = lambda t: t.detach().cpu().double()
+    real_mlp = lambda m: {"weights": [d(f.weight) for f in m.fcs], "biases": [d(f.bias) for f in m.fcs]}
+    return {"conv": dict(weight=conv.weight.to_tensor().detach().cpu().to(torch.complex128),
+                         bias=d(conv.bias), n_modes=conv.n_modes, max_n_modes=conv.max_n_modes,
+                         complex_data=True),
+            "fno_skip": {"type": "linear", "fr": {"w": d(blocks.fno_skips[i].fr.conv.weight)[:, :, 0]},
+                         "fi": {"w": d(blocks.fno_skips[i].fi.conv.weight)[:, :, 0]}},
+            "mlp": {"fr": real_mlp(blocks.channel_mlp[i].fr), "fi": real_mlp(blocks.channel_mlp[i].fi)},
+            "mlp_skip": {"type": "soft-gating", "fr": {"w": d(blocks.channel_mlp_skips[i].fr.weight)},
+                         "fi": {"w": d(blocks.channel_mlp_skips[i].fi.weight)}}}
+
+
+@pytest.mark.parametrize("dim,size,nm", [(1, (64,), (16,)), (2, (16, 24), (8, 8))])
+def test_fno_complex_data(dim, size, nm, cuda_device):
+    """FNO(complex_data=True) (reference test_fno.py:13-84 with complex data):
+    complex spectral layers, ComplexValued skips / MLPs / lifting /
+    projection and CGELU, against the oracle restatement."""
+    torch.manual_seed(32)
+    model = na.FNO(nm, in_channels=2, out_channels=1, hidden_channels=8, n_layers=2,
+                   complex_data=True).to(cuda_device)
+    with torch.no_grad():
+        for sk in model.fno_blocks.channel_mlp_skips:
+            sk.fr.weight.uniform_(0.5, 1.5)
+            sk.fi.weight.uniform_(-0.5, 0.5)
+    x = torch.randn(2, 2, *size, dtype=torch.complex64)
+    with torch.no_grad():
+        y = model(x.to(cuda_device))
+    assert y.dtype == torch.complex64 and list(y.shape) == [2, 1, *size]
+    d = lambda t: t.detach().cpu().double()
+    real_mlp = lambda m: {"weights": [d(f.weight) for f in m.fcs], "biases": [d(f.bias) for f in m.fcs]}
+    params = {"complex_data": True,
+              "lifting": {"fr": real_mlp(model.lifting.fr), "fi": real_mlp(model.lifting.fi)},
+              "projection": {"fr": real_mlp(model.projection.fr), "fi": real_mlp(model.projection.fi)},
+              "layers": [_complex_layer_params(model.fno_blocks, i) for i in range(2)]}
+    ref = R.fno_forward(x.to(torch.complex128), params)
+    assert rel_err(torch.view_as_real(y), torch.view_as_real(ref)) <= TOL
+
+
 def test_deterministic(cuda_device):
     torch.manual_seed(11)
     conv = na.SpectralConv(64, 64, (64, 64)).to(cuda_device)

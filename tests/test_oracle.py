@@ -129,6 +129,20 @@ def test_domain_padding_restatement():
     assert torch.equal(R.domain_unpad(y, pads), x)
 
 
+def test_complex_valued_wrappers():
+    """apply_complex is the complex-linear map with matrix A + iB when the real
+    parts apply A and B; CGELU is GELU on each part."""
+    g = torch.Generator().manual_seed(31)
+    A = torch.randn(4, 5, generator=g, dtype=torch.float64)
+    B = torch.randn(4, 5, generator=g, dtype=torch.float64)
+    x = torch.complex(torch.randn(5, 3, generator=g, dtype=torch.float64),
+                      torch.randn(5, 3, generator=g, dtype=torch.float64))
+    y = R.complex_apply(lambda t: A @ t, lambda t: B @ t, x)
+    assert torch.allclose(y, torch.complex(A, B) @ x, atol=1e-12)
+    z = R.cgelu(x)
+    assert torch.equal(z.real, R.gelu(x.real)) and torch.equal(z.imag, R.gelu(x.imag))
+
+
 def test_circular_shift_equivariance():
     torch.manual_seed(2)
     nms = R.stored_n_modes((6, 6))
