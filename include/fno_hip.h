@@ -168,14 +168,20 @@ int fno_block_epilogue_f32(const float* spec, const float* x, const float* skip_
  *   skip_kind FNO_SKIP_NONE, FNO_SKIP_SOFT_GATING (skip_x [B, Co, P] scaled
  *           by skip_weight [Co] plus skip_bias [Co] or NULL) or
  *           FNO_SKIP_IDENTITY (skip_x added)
- * Covered: (Ci, Ch, Co) in {(32,16,32), (64,32,64), (128,64,128)}, P % 4 == 0;
+ *   bf16_products 0: fp32 products; 1: the two 1x1 layers take x, W1, the
+ *           hidden activation and W2 rounded to bf16 (nearest even) with fp32
+ *           accumulation, as Conv1d runs under torch.autocast(dtype=bfloat16);
+ *           biases, skip and activations stay fp32, y is fp32 either way
+ * Covered: (Ci, Ch, Co) in {(32,16,32), (64,32,64), (128,64,128)} (block
+ * MLPs), Ci <= 4 with (Ch, Co) in {(128,64), (64,32)} (lifting) and
+ * (Ci, Ch) in {(64,128), (32,64)} with Co <= 16 (projection), P % 4 == 0;
  * otherwise FNO_ERR_UNSUPPORTED (fno_channel_mlp_is_supported tells which).
  */
 int fno_channel_mlp_f32(const float* x, const float* w1, const float* b1, const float* w2,
                         const float* b2, const float* skip_x, const float* skip_weight,
                         const float* skip_bias, float* y, int64_t batch, int32_t in_channels,
                         int32_t hidden_channels, int32_t out_channels, int64_t points,
-                        int32_t skip_kind, int32_t act, void* stream);
+                        int32_t skip_kind, int32_t act, int32_t bf16_products, void* stream);
 int fno_channel_mlp_is_supported(int32_t in_channels, int32_t hidden_channels,
                                  int32_t out_channels, int64_t points);
 

@@ -50,7 +50,8 @@ _SIGNATURES = {
     "fno_spectral_block_is_fused": (_c_i32, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32p, _c_i32p,
                                              _c_i32]),
     "fno_channel_mlp_f32": (_c_i32, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
-                                     _c_i64, _c_i32, _c_i32, _c_i32, _c_i64, _c_i32, _c_i32, _c_vp]),
+                                     _c_i64, _c_i32, _c_i32, _c_i32, _c_i64, _c_i32, _c_i32, _c_i32,
+                                     _c_vp]),
     "fno_channel_mlp_is_supported": (_c_i32, [_c_i32, _c_i32, _c_i32, _c_i64]),
     "fno_fft_window_c64": (_c_i32, [_c_vp, _c_vp, _c_i64, _c_i32, _c_i32p, _c_i32p, _c_i32, _c_vp,
                                     _c_size, _c_vp]),

@@ -2,7 +2,9 @@
 
 The default two-layer GELU MLP runs as one fno_channel_mlp_f32 call on the GPU
 when the library covers its widths (the lifting, projection and block MLPs of
-FNO); other configurations run as torch ops."""
+FNO); other configurations run as torch ops.  Under
+torch.autocast(dtype=torch.bfloat16) the kernel takes bf16-rounded operands
+with fp32 accumulation, as Conv1d does there; its output stays fp32."""
 from __future__ import annotations
 
 import torch
@@ -56,7 +58,8 @@ class ChannelMLP(nn.Module):
             y = Fh.channel_mlp(x.detach(), fc0.weight.detach(),
                                None if fc0.bias is None else fc0.bias.detach(), fc1.weight.detach(),
                                None if fc1.bias is None else fc1.bias.detach(), nat.SKIP_NONE, None,
-                               None, None, nat.ACT_NONE)
+                               None, None, nat.ACT_NONE,
+                               bf16_products=Fh.autocast_bf16(x.device.type))
             return _attach(y, x, *self.parameters())
         reshaped = False
         size = list(x.shape)

@@ -37,7 +37,8 @@ int block_epilogue(const float* spec, const float* x, const float* ws, float* y,
 bool channel_mlp_supported(int Ci, int Ch, int Co, int64_t P);
 int channel_mlp(const float* x, const float* w1, const float* b1, const float* w2, const float* b2,
                 const float* xs, const float* sw, const float* sb, float* y, int64_t B, int Ci,
-                int Ch, int Co, int64_t P, int skip_kind, int act, hipStream_t st);
+                int Ch, int Co, int64_t P, int skip_kind, int act, bool bf16_products,
+                hipStream_t st);
 bool fast2d_supported(int B, int Ci, int Co, int ndim, const int32_t* sizes, const int32_t* modes,
                       int skip_kind);
 size_t fast2d_workspace(int B, int Ci, int Co, const int32_t* sizes, const int32_t* modes);
@@ -293,9 +294,11 @@ int fno_channel_mlp_f32(const float* x, const float* w1, const float* b1, const 
                         const float* b2, const float* skip_x, const float* skip_weight,
                         const float* skip_bias, float* y, int64_t batch, int32_t in_channels,
                         int32_t hidden_channels, int32_t out_channels, int64_t points,
-                        int32_t skip_kind, int32_t act, void* stream) {
+                        int32_t skip_kind, int32_t act, int32_t bf16_products, void* stream) {
   clear_error();
   FNO_CHECK_ARG(x && w1 && w2 && y, "x/w1/w2/y must not be NULL");
+  FNO_CHECK_ARG(bf16_products == 0 || bf16_products == 1, "bf16_products must be 0 or 1 (got %d)",
+                bf16_products);
   FNO_CHECK_ARG(batch >= 1 && in_channels >= 1 && hidden_channels >= 1 && out_channels >= 1 &&
                     points >= 1,
                 "bad batch/channels/points");
@@ -319,7 +322,7 @@ int fno_channel_mlp_f32(const float* x, const float* w1, const float* b1, const 
     return FNO_ERR_UNSUPPORTED;
   }
   return channel_mlp(x, w1, b1, w2, b2, skip_x, skip_weight, skip_bias, y, batch, in_channels,
-                     hidden_channels, out_channels, points, skip_kind, act,
+                     hidden_channels, out_channels, points, skip_kind, act, bf16_products != 0,
                      reinterpret_cast<hipStream_t>(stream));
 }
 

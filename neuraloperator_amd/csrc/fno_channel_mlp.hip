@@ -22,7 +22,15 @@
 //     so k-step (m, r) contracts hidden row 16m + 4G + r in lane group G, and
 //     W2 is staged in that order;
 //   * bias, skip, activation and the store of y from GEMM 2's accumulators.
-// fp32 operands and accumulation throughout.
+// BF = false: fp32 operands and accumulation throughout.  BF = true: the two
+// GEMMs take bf16-rounded operands (round to nearest even) on
+// v_mfma_f32_16x16x32_bf16 with fp32 accumulation, the arithmetic of a 1x1
+// convolution under torch.autocast(dtype=torch.bfloat16); bias, skip and
+// activations stay fp32.  Its k order is permuted the same way: element j of
+// lane group G is input row 32 kb + 16 (j / 4) + 4 (j % 4) + G in GEMM 1 (so
+// the slab swizzle still separates the groups) and hidden row
+// 16 (2 kb + j / 4) + 4 G + j % 4 in GEMM 2 (two of GEMM 1's accumulator
+// tiles per k-step).
 #include "fno_common.h"
 
 namespace fno {
@@ -39,11 +47,22 @@ __device__ __forceinline__ int slab_col(int row, int c) { return c ^ ((row & 3) 
 // the swizzle follows G = (row / 4) % 4
 __device__ __forceinline__ int out_col(int row, int c) { return c ^ (((row >> 2) & 3) << 4); }
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+// LDS bytes of the staged weights: fp32 lane-order operands, or bf16 ones as
+// 64 lanes x 8 elements (1 KB) per (M tile, k-step)
+template <int CI, int CH, int CO, bool TWO, bool BF>
+struct MlpLds {
+  static constexpr int MT1 = CH / 16, MT2 = CO / 16, KB1 = (CI + 31) / 32, KB2 = (MT1 + 1) / 2;
+  static constexpr size_t w1 = BF ? (size_t)MT1 * KB1 * 1024 : (size_t)CH * CI * 4;
+  static constexpr size_t w2 = !TWO ? 0 : BF ? (size_t)MT2 * KB2 * 1024 : (size_t)CO * CH * 4;
+  static constexpr size_t total = w1 + w2 + (size_t)(CI * kMlpXS + 2 * CO) * 4;
+};
 }  // namespace
 
 // TWO = false: a single 1x1 layer y = act(W1 x + b2 + skip) (CH == CO), the
 // linear skip of the block epilogue with the spectral term as identity skip.
-template <int CI, int CH, int CO, bool TWO>
+template <int CI, int CH, int CO, bool TWO, bool BF>
 __global__ void __launch_bounds__(kMlpThreads) __attribute__((amdgpu_waves_per_eu(CI <= 64 ? 2 : 1)))
 k_channel_mlp(const float* x, const float* __restrict__ w1, const float* __restrict__ b1,
               const float* __restrict__ w2, const float* __restrict__ b2, const float* xs,
@@ -60,24 +79,42 @@ k_channel_mlp(const float* x, const float* __restrict__ w1, const float* __restr
   constexpr int NQ = CI * kMlpTP / 4;                  // float4s per slab
   constexpr int LPT = (NQ + kMlpThreads - 1) / kMlpThreads;   // ... per thread
   static_assert(NQ % kMlpThreads == 0 || NQ < kMlpThreads, "slab split");
+  using LD = MlpLds<CI, CH, CO, TWO, BF>;
+  constexpr int KB1 = LD::KB1, KB2 = LD::KB2;
   extern __shared__ float4 smem4[];
-  float* w1s = reinterpret_cast<float*>(smem4);   // [MT1][KS1][64] lane order
-  float* w2s = w1s + CH * CI;                     // [MT2][MT1][4][64] lane order
-  float* slab = w2s + (TWO ? CO * CH : 0);        // [CI][kMlpXS]
+  char* lds = reinterpret_cast<char*>(smem4);
+  float* w1s = reinterpret_cast<float*>(lds);          // [MT1][KS1][64] lane order
+  float* w2s = reinterpret_cast<float*>(lds + LD::w1);  // [MT2][MT1][4][64] lane order
+  __bf16* w1b = reinterpret_cast<__bf16*>(lds);         // [MT1][KB1][64][8]
+  __bf16* w2b = reinterpret_cast<__bf16*>(lds + LD::w1);  // [MT2][KB2][64][8]
+  float* slab = reinterpret_cast<float*>(lds + LD::w1 + LD::w2);   // [CI][kMlpXS]
   float* bos = slab + CI * kMlpXS;                // [CO] output bias (+ gate bias)
   float* gws = bos + CO;                          // [CO] gate weight
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int G = lane >> 4, t = lane & 15;
 
-  for (int e = tid; e < CH * CI; e += kMlpThreads) {
-    const int l = e & 63, ks = (e >> 6) % KS1, m = (e >> 6) / KS1;
-    const int k = 4 * ks + (l >> 4);
-    w1s[e] = k < ci ? w1[(16 * m + (l & 15)) * ci + k] : 0.f;
-  }
-  for (int e = tid; TWO && e < CO * CH; e += kMlpThreads) {
-    const int l = e & 63, r = (e >> 6) & 3, m = ((e >> 8) % MT1), mo = (e >> 8) / MT1;
-    const int oc = 16 * mo + (l & 15);
-    w2s[e] = oc < co ? w2[oc * CH + 16 * m + 4 * (l >> 4) + r] : 0.f;
+  if constexpr (BF) {
+    for (int e = tid; e < MT1 * KB1 * 512; e += kMlpThreads) {
+      const int j = e & 7, l = (e >> 3) & 63, kb = (e >> 9) % KB1, m = (e >> 9) / KB1;
+      const int k = 32 * kb + 16 * (j >> 2) + 4 * (j & 3) + (l >> 4);
+      w1b[e] = (__bf16)(k < ci ? w1[(16 * m + (l & 15)) * ci + k] : 0.f);
+    }
+    for (int e = tid; TWO && e < MT2 * KB2 * 512; e += kMlpThreads) {
+      const int j = e & 7, l = (e >> 3) & 63, kb = (e >> 9) % KB2, mo = (e >> 9) / KB2;
+      const int m = 2 * kb + (j >> 2), oc = 16 * mo + (l & 15);
+      w2b[e] = (__bf16)(oc < co && m < MT1 ? w2[oc * CH + 16 * m + 4 * (l >> 4) + (j & 3)] : 0.f);
+    }
+  } else {
+    for (int e = tid; e < CH * CI; e += kMlpThreads) {
+      const int l = e & 63, ks = (e >> 6) % KS1, m = (e >> 6) / KS1;
+      const int k = 4 * ks + (l >> 4);
+      w1s[e] = k < ci ? w1[(16 * m + (l & 15)) * ci + k] : 0.f;
+    }
+    for (int e = tid; TWO && e < CO * CH; e += kMlpThreads) {
+      const int l = e & 63, r = (e >> 6) & 3, m = ((e >> 8) % MT1), mo = (e >> 8) / MT1;
+      const int oc = 16 * mo + (l & 15);
+      w2s[e] = oc < co ? w2[oc * CH + 16 * m + 4 * (l >> 4) + r] : 0.f;
+    }
   }
   for (int o = tid; o < CO; o += kMlpThreads) {
     bos[o] = o >= co ? 0.f
@@ -164,14 +201,34 @@ k_channel_mlp(const float* x, const float* __restrict__ w1, const float* __restr
     // rows 4 ks + G: the swizzle is 16 G for every ks
     const float* bcol0 = slab + G * kMlpXS + slab_col(G, 32 * wave + t);
     const float* bcol1 = slab + G * kMlpXS + slab_col(G, 32 * wave + 16 + t);
+    if constexpr (BF) {
 #pragma unroll
-    for (int ks = 0; ks < KS1; ++ks) {
-      const float xb0 = bcol0[4 * ks * kMlpXS], xb1 = bcol1[4 * ks * kMlpXS];
+      for (int kb = 0; kb < KB1; ++kb) {
+        v8bf xb0, xb1;
 #pragma unroll
-      for (int m = 0; m < MT1; ++m) {
-        const float a = w1s[(m * KS1 + ks) * 64 + lane];
-        h[m][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, xb0, h[m][0], 0, 0, 0);
-        h[m][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, xb1, h[m][1], 0, 0, 0);
+        for (int j = 0; j < 8; ++j) {
+          // input row r0 + G; rows at or past CI (a multiple of 4) are zero
+          const int r0 = 32 * kb + 16 * (j >> 2) + 4 * (j & 3);
+          xb0[j] = (__bf16)(r0 < CI ? bcol0[r0 * kMlpXS] : 0.f);
+          xb1[j] = (__bf16)(r0 < CI ? bcol1[r0 * kMlpXS] : 0.f);
+        }
+#pragma unroll
+        for (int m = 0; m < MT1; ++m) {
+          const v8bf a = *reinterpret_cast<const v8bf*>(w1b + ((m * KB1 + kb) * 64 + lane) * 8);
+          h[m][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, xb0, h[m][0], 0, 0, 0);
+          h[m][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, xb1, h[m][1], 0, 0, 0);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < KS1; ++ks) {
+        const float xb0 = bcol0[4 * ks * kMlpXS], xb1 = bcol1[4 * ks * kMlpXS];
+#pragma unroll
+        for (int m = 0; m < MT1; ++m) {
+          const float a = w1s[(m * KS1 + ks) * 64 + lane];
+          h[m][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, xb0, h[m][0], 0, 0, 0);
+          h[m][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, xb1, h[m][1], 0, 0, 0);
+        }
       }
     }
     v4f o[MT2][2];
@@ -186,16 +243,35 @@ k_channel_mlp(const float* x, const float* __restrict__ w1, const float* __restr
       // GEMM 2: k-step (m, r) contracts hidden row 16m + 4G + r of lane group G
 #pragma unroll
       for (int mo = 0; mo < MT2; ++mo) o[mo][0] = o[mo][1] = (v4f)0.f;
+      if constexpr (BF) {
 #pragma unroll
-      for (int m = 0; m < MT1; ++m)
+        for (int kb = 0; kb < KB2; ++kb) {
+          v8bf hb0, hb1;
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
+          for (int j = 0; j < 8; ++j) {
+            const int m = 2 * kb + (j >> 2), mc = m < MT1 ? m : 0;
+            hb0[j] = (__bf16)(m < MT1 ? h[mc][0][j & 3] : 0.f);
+            hb1[j] = (__bf16)(m < MT1 ? h[mc][1][j & 3] : 0.f);
+          }
 #pragma unroll
           for (int mo = 0; mo < MT2; ++mo) {
-            const float a = w2s[((mo * MT1 + m) * 4 + r) * 64 + lane];
-            o[mo][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, h[m][0][r], o[mo][0], 0, 0, 0);
-            o[mo][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, h[m][1][r], o[mo][1], 0, 0, 0);
+            const v8bf a = *reinterpret_cast<const v8bf*>(w2b + ((mo * KB2 + kb) * 64 + lane) * 8);
+            o[mo][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, hb0, o[mo][0], 0, 0, 0);
+            o[mo][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, hb1, o[mo][1], 0, 0, 0);
           }
+        }
+      } else {
+#pragma unroll
+        for (int m = 0; m < MT1; ++m)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int mo = 0; mo < MT2; ++mo) {
+              const float a = w2s[((mo * MT1 + m) * 4 + r) * 64 + lane];
+              o[mo][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, h[m][0][r], o[mo][0], 0, 0, 0);
+              o[mo][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, h[m][1][r], o[mo][1], 0, 0, 0);
+            }
+      }
     } else {
 #pragma unroll
       for (int mo = 0; mo < MT2; ++mo) {
@@ -264,10 +340,6 @@ k_channel_mlp(const float* x, const float* __restrict__ w1, const float* __restr
 }
 
 // --------------------------------------------------------------------- host
-template <int CI, int CH, int CO, bool TWO>
-static size_t mlp_lds_bytes() {
-  return (size_t)(CH * CI + (TWO ? CO * CH : 0) + CI * kMlpXS + 2 * CO) * sizeof(float);
-}
 
 // (Ci, Ch, Co) -> kernel widths: Ci <= 4 runs padded to 4 input channels and
 // Co <= 16 padded to 16 outputs (the lifting 3 -> 2H -> H and projection
@@ -287,13 +359,13 @@ bool channel_mlp_supported(int Ci, int Ch, int Co, int64_t P) {
   return P % 4 == 0 && mlp_variant(Ci, Ch, Co) >= 0;
 }
 
-template <int CI, int CH, int CO, bool TWO = true>
+template <int CI, int CH, int CO, bool TWO, bool BF>
 static int launch_mlp(const float* x, const float* w1, const float* b1, const float* w2,
                       const float* b2, const float* xs, const float* sw, const float* sb, float* y,
                       int64_t B, int64_t P, int ci, int co, int skip_kind, int act, hipStream_t st) {
-  const size_t lds = mlp_lds_bytes<CI, CH, CO, TWO>();
+  const size_t lds = MlpLds<CI, CH, CO, TWO, BF>::total;
   if (lds > 48 * 1024) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_channel_mlp<CI, CH, CO, TWO>),
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_channel_mlp<CI, CH, CO, TWO, BF>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) {
       set_error("channel MLP: %s", hipGetErrorString(e));
@@ -308,7 +380,7 @@ static int launch_mlp(const float* x, const float* w1, const float* b1, const fl
   if (per_cu == 0) {
     int n = 0;
     const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-        &n, reinterpret_cast<const void*>(&k_channel_mlp<CI, CH, CO, TWO>), kMlpThreads, lds);
+        &n, reinterpret_cast<const void*>(&k_channel_mlp<CI, CH, CO, TWO, BF>), kMlpThreads, lds);
     per_cu = (e == hipSuccess && n > 0) ? n : 1;
   }
   int dev = 0, cus = 0;
@@ -317,16 +389,21 @@ static int launch_mlp(const float* x, const float* w1, const float* b1, const fl
     cus = 256;
   int64_t grid = (int64_t)cus * per_cu;
   if (grid > tiles) grid = tiles;
-  hipLaunchKernelGGL((k_channel_mlp<CI, CH, CO, TWO>), dim3((unsigned)grid), dim3(kMlpThreads), lds, st,
+  hipLaunchKernelGGL((k_channel_mlp<CI, CH, CO, TWO, BF>), dim3((unsigned)grid), dim3(kMlpThreads), lds, st,
                      x, w1, b1, w2, b2, xs, sw, sb, y, P, tps, tiles, ci, co, skip_kind, act);
   return launch_status("k_channel_mlp");
 }
 
 int channel_mlp(const float* x, const float* w1, const float* b1, const float* w2, const float* b2,
                 const float* xs, const float* sw, const float* sb, float* y, int64_t B, int Ci,
-                int Ch, int Co, int64_t P, int skip_kind, int act, hipStream_t st) {
+                int Ch, int Co, int64_t P, int skip_kind, int act, bool bf16_products,
+                hipStream_t st) {
 #define FNO_MLP(ci_, ch_, co_)                                                                     \
-  launch_mlp<ci_, ch_, co_>(x, w1, b1, w2, b2, xs, sw, sb, y, B, P, Ci, Co, skip_kind, act, st)
+  (bf16_products                                                                                   \
+       ? launch_mlp<ci_, ch_, co_, true, true>(x, w1, b1, w2, b2, xs, sw, sb, y, B, P, Ci, Co,     \
+                                               skip_kind, act, st)                                 \
+       : launch_mlp<ci_, ch_, co_, true, false>(x, w1, b1, w2, b2, xs, sw, sb, y, B, P, Ci, Co,    \
+                                                skip_kind, act, st))
   switch (mlp_variant(Ci, Ch, Co)) {
     case 0: return FNO_MLP(64, 32, 64);
     case 1: return FNO_MLP(32, 16, 32);
@@ -354,8 +431,8 @@ bool skip_gemm_supported(int Ci, int Co, int64_t P, const void* x, const void* s
 int skip_gemm(const float* x, const float* ws, const float* spec, float* y, int64_t B, int Ci,
               int Co, int64_t P, int act, hipStream_t st) {
 #define FNO_SKIPG(c)                                                                               \
-  launch_mlp<c, c, c, false>(x, ws, nullptr, nullptr, nullptr, spec, nullptr, nullptr, y, B, P, Ci, \
-                             Co, FNO_SKIP_IDENTITY, act, st)
+  launch_mlp<c, c, c, false, false>(x, ws, nullptr, nullptr, nullptr, spec, nullptr, nullptr, y, B, \
+                                    P, Ci, Co, FNO_SKIP_IDENTITY, act, st)
   if (Ci == 32) return FNO_SKIPG(32);
   if (Ci == 64) return FNO_SKIPG(64);
   return FNO_SKIPG(128);

@@ -301,7 +301,8 @@ class FNOBlocks(nn.Module):
                     x_in.detach() if kind != nat.SKIP_NONE else None,
                     gate.weight.detach() if gate is not None else None,
                     gate.bias.detach() if gate is not None and gate.bias is not None else None,
-                    nat.ACT_GELU if index < (self.n_layers - 1) else nat.ACT_NONE)
+                    nat.ACT_GELU if index < (self.n_layers - 1) else nat.ACT_NONE,
+                    bf16_products=Fh.autocast_bf16(x.device.type))
             params = [x, x_in] + list(mlp.parameters())
             if gate is not None:
                 params += list(gate.parameters())

@@ -187,14 +187,23 @@ def channel_mlp_is_supported(Ci: int, Ch: int, Co: int, P: int, *tensors) -> boo
     return bool(nat.load().fno_channel_mlp_is_supported(Ci, Ch, Co, P))
 
 
+def autocast_bf16(device_type: str = "cuda") -> bool:
+    """True inside torch.autocast(device_type, dtype=torch.bfloat16), where
+    torch runs Conv1d on bf16 operands with fp32 accumulation."""
+    return (torch.is_autocast_enabled(device_type)
+            and torch.get_autocast_dtype(device_type) == torch.bfloat16)
+
+
 def channel_mlp(x: torch.Tensor, w1: torch.Tensor, b1: Optional[torch.Tensor], w2: torch.Tensor,
                 b2: Optional[torch.Tensor], skip_kind: int = nat.SKIP_NONE,
                 skip_x: Optional[torch.Tensor] = None, skip_weight: Optional[torch.Tensor] = None,
                 skip_bias: Optional[torch.Tensor] = None, act: int = nat.ACT_NONE,
-                out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                out: Optional[torch.Tensor] = None, bf16_products: bool = False) -> torch.Tensor:
     """act(W2 gelu(W1 x + b1) + b2 + skip(skip_x)) over x [B, Ci, *S]
     (ChannelMLP.forward with two layers, channel_mlp.py:82-119, plus the
-    channel-MLP skip and second activation of fno_block.py:363-379)."""
+    channel-MLP skip and second activation of fno_block.py:363-379).
+    bf16_products: both 1x1 layers on bf16-rounded operands with fp32
+    accumulation (Conv1d under a bf16 autocast); the output stays fp32."""
     _require_gpu(x, w1, w2, skip_x)
     lib = nat.load()
     B, Ci, *S = x.shape
@@ -210,7 +219,7 @@ def channel_mlp(x: torch.Tensor, w1: torch.Tensor, b1: Optional[torch.Tensor], w
                                     for t in (w1, b1, w2, b2, skip_weight, skip_bias))
     nat.check(lib.fno_channel_mlp_f32(_ptr(xx), _ptr(w1f), _ptr(b1f), _ptr(w2f), _ptr(b2f), _ptr(sx),
                                       _ptr(swf), _ptr(sbf), _ptr(y), B, Ci, Ch, Co, P, skip_kind,
-                                      act, _stream(x.device)),
+                                      act, int(bool(bf16_products)), _stream(x.device)),
               "fno_channel_mlp_f32")
     return y
 

@@ -401,13 +401,25 @@ def soft_gating(x, w, b=None):
     return w * x + b if b is not None else w * x
 
 
-def channel_mlp(x, weights, biases, non_linearity=gelu):
-    """ChannelMLP.forward (channel_mlp.py:212-249) with 1x1 Conv1d layers."""
+def bf16_round(t):
+    """Round to the nearest bfloat16 (ties to even) and widen back."""
+    return t.to(torch.bfloat16).to(t.dtype)
+
+
+def channel_mlp(x, weights, biases, non_linearity=gelu, bf16_products=False):
+    """ChannelMLP.forward (channel_mlp.py:212-249) with 1x1 Conv1d layers.
+
+    bf16_products: each layer's input and weight rounded to bf16 before the
+    product, accumulation and bias at full precision.  The reference's mixed
+    precision wraps the model in torch.autocast (training/trainer.py:671);
+    with dtype=torch.bfloat16, Conv1d takes operands rounded this way.  The
+    layer outputs are not rounded here."""
     size = list(x.shape)
     h = x.reshape(size[0], size[1], -1)
     n = len(weights)
+    rnd = bf16_round if bf16_products else (lambda t: t)
     for i, (w, b) in enumerate(zip(weights, biases)):
-        h = F.conv1d(h, w.reshape(w.shape[0], w.shape[1], 1), b)
+        h = F.conv1d(rnd(h), rnd(w.reshape(w.shape[0], w.shape[1], 1)), b)
         if i < n - 1:
             h = non_linearity(h)
     return h.reshape(size[0], h.shape[1], *size[2:])

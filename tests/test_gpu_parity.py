@@ -798,6 +798,75 @@ def test_channel_mlp_lifting_projection(Ci, Ch, Co, P, cuda_device):
     assert rel_err(y, ref) <= TOL
 
 
+@pytest.mark.parametrize("Ci,Ch,Co,P,skip", [(64, 32, 64, 260, "soft-gating"), (32, 16, 32, 132, "identity"),
+                                             (128, 64, 128, 256, "soft-gating"), (3, 128, 64, 512, None),
+                                             (3, 64, 32, 132, None), (64, 128, 1, 260, None),
+                                             (32, 64, 1, 1024, None)])
+def test_channel_mlp_bf16_products(Ci, Ch, Co, P, skip, cuda_device):
+    """bf16_products: both layers on bf16-rounded operands with fp32
+    accumulation (Conv1d under a bf16 autocast).  Against the oracle with the
+    same operand rounding, outputs agree except where a hidden value sits so
+    close to a bf16 rounding boundary that the kernel's fp32 GELU and the
+    float64 one round it to neighbouring values (max error <= 2e-3); the mean
+    error is then < 5% of the mean error against the unrounded oracle (so the
+    bf16 operands are the ones the oracle rounds), and the unrounded oracle
+    stays within the bf16 configuration's 2e-2."""
+    print(f"channel mlp bf16 products {Ci}->{Ch}->{Co} P{P} {skip}", flush=True)
+    g = torch.Generator().manual_seed(27)
+    B = 3
+    x = torch.randn(B, Ci, P, generator=g)
+    xs = torch.randn(B, Co, P, generator=g)
+    w1, b1 = torch.randn(Ch, Ci, 1, generator=g) / Ci ** 0.5, torch.randn(Ch, generator=g) * 0.1
+    w2, b2 = torch.randn(Co, Ch, 1, generator=g) / Ch ** 0.5, torch.randn(Co, generator=g) * 0.1
+    gw = torch.rand(1, Co, 1, generator=g) + 0.5
+    kind, act = nat.SKIP_NONE, nat.ACT_NONE
+    refs = []
+    for rounded in (True, False):
+        r = R.channel_mlp(x.double(), [w1.double(), w2.double()], [b1.double(), b2.double()],
+                          bf16_products=rounded)
+        if skip == "soft-gating":
+            kind, act = nat.SKIP_SOFT_GATING, nat.ACT_GELU
+            r = R.gelu(r + R.soft_gating(xs.double(), gw.double()))
+        elif skip == "identity":
+            kind, act = nat.SKIP_IDENTITY, nat.ACT_GELU
+            r = R.gelu(r + xs.double())
+        refs.append(r)
+    d = lambda t: t.to(cuda_device)
+    with torch.no_grad():
+        y = Fh.channel_mlp(d(x), d(w1), d(b1), d(w2), d(b2), kind,
+                           d(xs) if kind != nat.SKIP_NONE else None,
+                           d(gw) if kind == nat.SKIP_SOFT_GATING else None, None, act,
+                           bf16_products=True)
+    torch.cuda.synchronize()
+    assert y.dtype == torch.float32
+    yd = y.double().cpu()
+    assert rel_err(y, refs[0]) <= 2e-3
+    assert (yd - refs[0]).abs().mean() < 0.05 * (yd - refs[1]).abs().mean()
+    assert rel_err(y, refs[1]) <= 2e-2
+
+
+def test_fno_autocast_bf16(cuda_device):
+    """FNO forward under torch.autocast(dtype=bfloat16): lifting, block and
+    projection MLPs take the bf16-product kernel, the spectral path stays
+    fp32.  Within 2e-2 of the fp32 oracle, and not equal to the fp32 run."""
+    torch.manual_seed(33)
+    model = na.FNO((16, 16), in_channels=1, out_channels=1, hidden_channels=64, n_layers=2).to(cuda_device)
+    with torch.no_grad():
+        for sk in model.fno_blocks.channel_mlp_skips:
+            sk.weight.uniform_(0.5, 1.5)
+    x = gaussian_random_field((2, 1, 64, 128), seed=5)
+    with torch.no_grad():
+        y32 = model(x.to(cuda_device))
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            ybf = model(x.to(cuda_device))
+    assert ybf.dtype == torch.float32
+    params = {"lifting": _mlp(model.lifting), "projection": _mlp(model.projection),
+              "layers": [_layer_params(model.fno_blocks, i) for i in range(2)]}
+    ref = R.fno_forward(x.double(), params)
+    assert rel_err(y32, ref) <= TOL
+    assert 1e-4 < rel_err(ybf, ref) <= 2e-2
+
+
 def test_channel_mlp_in_place(cuda_device):
     """y written over x (the layout FNOBlocks may use) matches the out-of-place result."""
     g = torch.Generator().manual_seed(24)

@@ -129,6 +129,34 @@ def test_domain_padding_restatement():
     assert torch.equal(R.domain_unpad(y, pads), x)
 
 
+def test_channel_mlp_bf16_products_rounding():
+    """The bf16-product MLP rounds each layer's input and weight to the
+    nearest bf16, ties to even: 1 + 2^-8 (halfway between 1 and 1 + 2^-7)
+    becomes 1 and 1 + 3 * 2^-8 becomes 1 + 2^-6; GELU(1) between the layers is
+    rounded before the second product; bf16-exact operands change nothing."""
+    one = torch.ones(1, 1, 1, dtype=torch.float64)
+    w = [one.reshape(1, 1), one.reshape(1, 1)]
+    b = [torch.zeros(1, dtype=torch.float64)] * 2
+    y = R.channel_mlp(one * (1 + 2.0 ** -8), w, b, bf16_products=True)
+    g1 = 0.5 * (1 + math.erf(1 / math.sqrt(2)))       # GELU(1)
+    assert y.item() == torch.tensor(g1).to(torch.bfloat16).item()
+    y = R.channel_mlp(one * (1 + 3 * 2.0 ** -8), [one.reshape(1, 1) * 2, one.reshape(1, 1)], b,
+                      bf16_products=True)
+    x2 = 2 * (1 + 2.0 ** -6)
+    assert y.item() == torch.tensor(0.5 * x2 * (1 + math.erf(x2 / math.sqrt(2)))).to(torch.bfloat16).item()
+    g = torch.Generator().manual_seed(5)
+    xs = torch.randn(2, 3, 7, generator=g).to(torch.bfloat16).double()
+    ws = [torch.randn(4, 3, generator=g).to(torch.bfloat16).double(),
+          torch.randn(2, 4, generator=g).to(torch.bfloat16).double()]
+    bs = [torch.randn(4, generator=g, dtype=torch.float64), torch.randn(2, generator=g, dtype=torch.float64)]
+    ref = R.channel_mlp(xs, ws, bs)
+    h = R.gelu(torch.einsum("oi,bip->bop", ws[0], xs) + bs[0][:, None])
+    exact_hidden = R.bf16_round(h)
+    assert torch.allclose(R.channel_mlp(xs, ws, bs, bf16_products=True),
+                          torch.einsum("oi,bip->bop", ws[1], exact_hidden) + bs[1][:, None], atol=1e-12)
+    assert (R.channel_mlp(xs, ws, bs, bf16_products=True) - ref).abs().max() > 0
+
+
 def test_complex_valued_wrappers():
     """apply_complex is the complex-linear map with matrix A + iB when the real
     parts apply A and B; CGELU is GELU on each part."""
