@@ -24,6 +24,8 @@ raise on backward.
 """
 from __future__ import annotations
 
+import math
+
 from typing import List, Optional, Tuple, Union
 
 import torch
@@ -146,6 +148,61 @@ class _SpectralConvFn(torch.autograd.Function):
         if ctx.bias_shape is not None and ctx.needs_input_grad[2]:
             dims = [0] + list(range(2, gy.ndim))
             gb = gy.sum(dim=dims).reshape(ctx.bias_shape)
+        return gx, gw, gb, None, None
+
+
+def _last_axis_phase(n: int, ndim: int, device) -> torch.Tensor:
+    """psi_t = exp(-2 pi i (n//2) t / n) along the last axis (1 in 1D): the
+    complex-data forward window takes last-axis frequencies j - n//2 and the
+    inverse puts them back at j (spectral_convolution.py:448-449, :531-538),
+    so each transform's adjoint is the other library transform times psi."""
+    if ndim == 1:
+        return torch.ones(n, dtype=torch.complex64, device=device)
+    t = torch.arange(n, dtype=torch.float64, device=device)
+    return torch.polar(torch.ones_like(t), -2.0 * math.pi * (n // 2) * t / n).to(torch.complex64)
+
+
+class _SpectralConvComplexFn(torch.autograd.Function):
+    """complex_data=True spectral convolution y = I(W . F(x)) + bias with
+    its gradients, output size == input size.  F (windowed fftn) and I
+    (zero-filled ifftn) are C-linear, so with psi from _last_axis_phase and
+    the dual norm:
+
+        gY = I^H gy = F_dual(gy . psi)      gX = gY . conj(W)^T
+        gW = conj(X)^T . gY                gx = F^H gX = I_dual(gX) . psi
+        gbias = sum Re(gy)   (the real bias is added to the real part)"""
+
+    @staticmethod
+    def forward(ctx, x, w, bias, kept, fft_norm):
+        sizes = list(x.shape[2:])
+        xhat = Fh.fft_window(x, kept, fft_norm)
+        yhat = Fh.contract_dense(xhat, w)
+        b = bias.reshape(-1) if bias is not None else None
+        y = Fh.ifft_window(yhat, sizes, sizes, b, fft_norm)
+        ctx.save_for_backward(xhat, w)
+        ctx.kept, ctx.fft_norm, ctx.sizes = list(kept), fft_norm, sizes
+        ctx.bias_shape = None if bias is None else bias.shape
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        xhat, w = ctx.saved_tensors
+        kept, sizes = ctx.kept, ctx.sizes
+        dual = _DUAL_NORM[ctx.fft_norm]
+        gy = gy.contiguous().to(torch.complex64)
+        psi = _last_axis_phase(sizes[-1], len(sizes), gy.device)
+        gY = Fh.fft_window((gy * psi).contiguous(), kept, dual)          # [B, Co, *m]
+        gx = gw = gb = None
+        if ctx.needs_input_grad[0]:
+            wt = w.conj().transpose(0, 1).contiguous()                   # [Co, Ci, *m]
+            gX = Fh.contract_dense(gY, wt)                               # [B, Ci, *m]
+            gx = Fh.ifft_window(gX, sizes, sizes, None, dual) * psi
+        if ctx.needs_input_grad[1]:
+            xt = xhat.conj().transpose(0, 1).contiguous()                # [Ci, B, *m]
+            gw = Fh.contract_dense(xt, gY)                               # [Ci, Co, *m]
+        if ctx.bias_shape is not None and ctx.needs_input_grad[2]:
+            dims = [0] + list(range(2, gy.ndim))
+            gb = gy.real.sum(dim=dims).reshape(ctx.bias_shape)
         return gx, gw, gb, None, None
 
 
@@ -317,10 +374,20 @@ class SpectralConv(BaseSpectralConv):
 
     def _forward_complex(self, x, output_shape=None):
         """complex_data=True: fftn / window / contraction / ifftn on complex
-        fields (spectral_convolution.py:436-449, :500-538), output complex."""
+        fields (spectral_convolution.py:436-449, :500-538), output complex.
+        With gradients (output size == input size, non-separable) through
+        _SpectralConvComplexFn on the dense window weight."""
         sizes = list(x.shape[2:])
         kept, sl = self.window(sizes)
         out_sizes = self.output_sizes(sizes, output_shape)
+        if torch.is_grad_enabled() and (x.requires_grad or
+                                        any(p.requires_grad for p in self.parameters())):
+            if out_sizes != sizes or self.separable:
+                raise NotImplementedError(
+                    "gradients of the HIP spectral path cover output size == input size, "
+                    "non-separable weights")
+            return _SpectralConvComplexFn.apply(x, self.dense_window_weight(sl), self.bias, kept,
+                                                self.fft_norm)
         xhat = Fh.fft_window(x.detach(), kept, self.fft_norm)
         if self._contract == "tucker" and not self.separable:
             wv = self.weight[sl]

@@ -511,6 +511,118 @@ def test_complex_data_spectral_conv(sizes, nm, out, norm, cuda_device):
     assert rel_err(torch.view_as_real(y), torch.view_as_real(ref)) <= TOL
 
 
+@pytest.mark.parametrize("sizes,nm", [((64,), (20,)), ((37,), (12,)), ((16, 20), (8, 10)),
+                                      ((12, 9), (6, 5)), ((64, 128), (16, 32)), ((8, 12, 16), (4, 6, 8))])
+@pytest.mark.parametrize("norm", ["forward", "backward", "ortho"])
+def test_complex_spectral_conv_gradients(sizes, nm, norm, cuda_device):
+    """x, weight and bias gradients of SpectralConv(complex_data=True) for
+    the real loss Re(sum y * g) against torch autograd through the float64
+    oracle (fftn / window / ifftn with the reference's last-axis window)."""
+    print(f"complex grad {sizes} {nm} {norm}", flush=True)
+    torch.manual_seed(19)
+    Ci, Co, B = 3, 4, 2
+    conv = na.SpectralConv(Ci, Co, nm, complex_data=True, fft_norm=norm).to(cuda_device)
+    with torch.no_grad():
+        conv.bias.normal_()
+    x = torch.randn(B, Ci, *sizes, dtype=torch.complex64)
+    g = torch.randn(B, Co, *sizes, dtype=torch.complex64)
+    xg = x.to(cuda_device).requires_grad_(True)
+    (conv(xg) * g.to(cuda_device)).real.sum().backward()
+    xd = x.to(torch.complex128).requires_grad_(True)
+    wd = conv.weight.to_tensor().detach().cpu().to(torch.complex128).requires_grad_(True)
+    bd = conv.bias.detach().cpu().double().requires_grad_(True)
+    yd = R.spectral_conv_forward(xd, wd, bd, conv.n_modes, conv.max_n_modes, fft_norm=norm,
+                                 complex_data=True)
+    (yd * g.to(torch.complex128)).real.sum().backward()
+    assert rel_err(torch.view_as_real(xg.grad), torch.view_as_real(xd.grad)) <= TOL
+    assert rel_err(torch.view_as_real(conv.weight.to_tensor().grad), torch.view_as_real(wd.grad)) <= TOL
+    assert rel_err(conv.bias.grad, bd.grad) <= TOL
+
+
+def test_fno_complex_backward_gradients(cuda_device):
+    """Complex-data FNO training step: the input, lifting, spectral and
+    channel-MLP gradients against torch autograd through the float64
+    oracle, for the loss |sum y| of the reference's test_fno.py:73-78."""
+    torch.manual_seed(34)
+    model = na.FNO((8, 8), in_channels=2, out_channels=1, hidden_channels=8, n_layers=2,
+                   complex_data=True).to(cuda_device)
+    with torch.no_grad():
+        for sk in model.fno_blocks.channel_mlp_skips:
+            sk.fr.weight.uniform_(0.5, 1.5)
+            sk.fi.weight.uniform_(-0.5, 0.5)
+        for conv in model.fno_blocks.convs:
+            conv.bias.normal_()
+    x = torch.randn(2, 2, 16, 12, dtype=torch.complex64)
+    xg = x.to(cuda_device).requires_grad_(True)
+    out = model(xg).sum()
+    ((out.real ** 2 + out.imag ** 2) ** 0.5).backward()
+    for name, p in model.named_parameters():
+        assert p.grad is not None, name
+    blocks = model.fno_blocks
+    d = lambda t: t.detach().cpu().double().requires_grad_(True)
+    real_mlp = lambda m: {"weights": [d(f.weight) for f in m.fcs], "biases": [d(f.bias) for f in m.fcs]}
+    layers = []
+    for i in range(2):
+        conv = blocks.convs[i]
+        layers.append({
+            "conv": dict(weight=conv.weight.to_tensor().detach().cpu().to(torch.complex128).requires_grad_(True),
+                         bias=d(conv.bias), n_modes=conv.n_modes, max_n_modes=conv.max_n_modes,
+                         complex_data=True),
+            "fno_skip": {"type": "linear", "fr": {"w": d(blocks.fno_skips[i].fr.conv.weight[:, :, 0])},
+                         "fi": {"w": d(blocks.fno_skips[i].fi.conv.weight[:, :, 0])}},
+            "mlp": {"fr": real_mlp(blocks.channel_mlp[i].fr), "fi": real_mlp(blocks.channel_mlp[i].fi)},
+            "mlp_skip": {"type": "soft-gating", "fr": {"w": d(blocks.channel_mlp_skips[i].fr.weight)},
+                         "fi": {"w": d(blocks.channel_mlp_skips[i].fi.weight)}}})
+    params = {"complex_data": True,
+              "lifting": {"fr": real_mlp(model.lifting.fr), "fi": real_mlp(model.lifting.fi)},
+              "projection": {"fr": real_mlp(model.projection.fr), "fi": real_mlp(model.projection.fi)},
+              "layers": layers}
+    xd = x.to(torch.complex128).requires_grad_(True)
+    ref = R.fno_forward(xd, params).sum()
+    ((ref.real ** 2 + ref.imag ** 2) ** 0.5).backward()
+    assert rel_err(torch.view_as_real(xg.grad), torch.view_as_real(xd.grad)) <= TOL
+    assert rel_err(model.lifting.fr.fcs[0].weight.grad, params["lifting"]["fr"]["weights"][0].grad) <= TOL
+    assert rel_err(model.projection.fi.fcs[1].weight.grad,
+                   params["projection"]["fi"]["weights"][1].grad) <= TOL
+    for i in range(2):
+        assert rel_err(torch.view_as_real(blocks.convs[i].weight.to_tensor().grad),
+                       torch.view_as_real(layers[i]["conv"]["weight"].grad)) <= TOL
+        assert rel_err(blocks.convs[i].bias.grad, layers[i]["conv"]["bias"].grad) <= TOL
+        assert rel_err(blocks.fno_skips[i].fi.conv.weight.grad[:, :, 0],
+                       layers[i]["fno_skip"]["fi"]["w"].grad) <= TOL
+        assert rel_err(blocks.channel_mlp[i].fr.fcs[0].weight.grad,
+                       layers[i]["mlp"]["fr"]["weights"][0].grad) <= TOL
+
+
+@pytest.mark.parametrize("n_dim", [1, 2, 3, 4])
+@pytest.mark.parametrize("stabilizer", [None, "tanh"])
+@pytest.mark.parametrize("lifting_channel_ratio", [1, 2])
+@pytest.mark.parametrize("preactivation", [False, True])
+@pytest.mark.parametrize("complex_data", [True, False])
+@pytest.mark.parametrize("enforce_hermitian_symmetry", [True, False])
+def test_fno_reference_matrix(n_dim, stabilizer, lifting_channel_ratio, preactivation, complex_data,
+                              enforce_hermitian_symmetry, cuda_device):
+    """The reference's test_fno matrix (test_fno.py:13-84, its GPU sizes:
+    s 12, 8 modes, width 12, batch 4, 4 layers, rank 0.2): output shape, and
+    a gradient for every parameter after loss.backward()."""
+    s, modes, width, batch, n_layers = 12, 8, 12, 4, 4
+    model = na.FNO(in_channels=3, out_channels=1, hidden_channels=width, n_modes=(modes,) * n_dim,
+                   rank=0.2, fixed_rank_modes=False, n_layers=n_layers, stabilizer=stabilizer,
+                   lifting_channel_ratio=lifting_channel_ratio, preactivation=preactivation,
+                   complex_data=complex_data, fno_block_precision="full",
+                   enforce_hermitian_symmetry=enforce_hermitian_symmetry).to(cuda_device)
+    dtype = torch.cfloat if complex_data else torch.float32
+    x = torch.randn(batch, 3, *(s,) * n_dim, dtype=dtype).to(cuda_device)
+    out = model(x)
+    assert list(out.shape) == [batch, 1, *(s,) * n_dim]
+    loss = out.sum()
+    if complex_data:
+        loss = (loss.real ** 2 + loss.imag ** 2) ** 0.5
+    loss.backward()
+    unused = [n for n, p in model.named_parameters() if p.grad is None]
+    assert not unused, unused
+
+
 def test_complex_data_tucker(cuda_device):
     torch.manual_seed(23)
     conv = na.SpectralConv(4, 4, (8, 8, 8), complex_data=True, factorization="Tucker", rank=0.5,
