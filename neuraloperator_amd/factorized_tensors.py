@@ -124,6 +124,19 @@ class FactorizedTensor(nn.Module):
             return TTTensor(shape, tt_rank(shape, rank), dtype=dtype, device=device)
         raise ValueError(f"Got unexpected factorization {factorization}")
 
+    @staticmethod
+    def from_tensor(tensor, rank=None, factorization="ComplexDense"):
+        """A weight container holding a copy of a full tensor (tltorch's
+        FactorizedTensor.from_tensor, used as in the reference's
+        test_spectral_convolution.py:52-55).  Only the dense form is built:
+        decomposing into CP / Tucker / TT factors is not."""
+        key = (factorization or "Dense").lower()
+        if key.startswith("complex"):
+            key = key[len("complex"):]
+        if key != "dense":
+            raise NotImplementedError(f"from_tensor into a {factorization} factorization is not built")
+        return DenseTensor(tensor.shape, tensor=tensor.detach().clone())
+
     @property
     def dtype(self):
         return self.to_tensor().dtype
@@ -172,10 +185,6 @@ class DenseTensor(FactorizedTensor):
             tensor = torch.empty(tuple(shape), dtype=dtype, device=device)
         self.tensor = nn.Parameter(tensor)
         self.rank = None
-
-    @classmethod
-    def from_tensor(cls, tensor):
-        return cls(tensor.shape, tensor=tensor.detach().clone())
 
     @property
     def shape(self):

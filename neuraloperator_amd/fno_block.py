@@ -48,6 +48,33 @@ class InstanceNorm(nn.Module):
         return x
 
 
+class AdaIN(nn.Module):
+    """Adaptive instance norm (neuralop/layers/normalization_layers.py:5-56):
+    each channel normalised over its spatial points, then scaled and shifted
+    by the two halves of mlp(embedding); the embedding is set before the
+    forward.  The default mlp is Linear(embed_dim, 512), GELU,
+    Linear(512, 2 in_channels)."""
+
+    def __init__(self, embed_dim, in_channels, mlp=None, eps=1e-5):
+        super().__init__()
+        self.in_channels = in_channels
+        self.embed_dim = embed_dim
+        self.eps = eps
+        self.mlp = mlp if mlp is not None else nn.Sequential(
+            nn.Linear(embed_dim, 512), nn.GELU(), nn.Linear(512, 2 * in_channels))
+        self.embedding = None
+
+    def set_embedding(self, x):
+        self.embedding = x.reshape(self.embed_dim)
+
+    def forward(self, x):
+        if self.embedding is None:
+            raise RuntimeError("AdaIN: set the embedding (set_ada_in_embeddings) before the forward")
+        scale, shift = self.mlp(self.embedding).split(self.in_channels)
+        # one group per channel: instance statistics, per-channel affine
+        return F.group_norm(x, self.in_channels, scale, shift, eps=self.eps)
+
+
 class BatchNorm(nn.Module):
     def __init__(self, n_dim: int, num_features: int, **kwargs):
         super().__init__()
@@ -179,7 +206,8 @@ class FNOBlocks(nn.Module):
             self.norm = nn.ModuleList([BatchNorm(n_dim=self.n_dim, num_features=self.out_channels)
                                        for _ in range(n_layers * self.n_norms)])
         elif norm == "ada_in":
-            raise NotImplementedError("ada_in norm is not built")
+            self.norm = nn.ModuleList([AdaIN(ada_in_features, self.out_channels)
+                                       for _ in range(n_layers * self.n_norms)])
         else:
             raise ValueError(f"Got norm={norm} but expected None or one of "
                              "[instance_norm, group_norm, batch_norm, ada_in]")
@@ -220,6 +248,18 @@ class FNOBlocks(nn.Module):
             return False
         kind, _ = self._fused_skip(index)
         return kind is not None
+
+    def set_ada_in_embeddings(self, *embeddings):
+        """Embeddings of the Ada-IN norms (fno_block.py:304-321): one for all
+        norm layers, or one per layer."""
+        if self.norm is None:
+            return
+        if len(embeddings) == 1:
+            embeddings = embeddings * len(self.norm)
+        for n, e in zip(self.norm, embeddings):
+            # a complex-data norm holds a real copy for each part
+            for part in ((n.fr, n.fi) if isinstance(n, ComplexValued) else (n,)):
+                part.set_embedding(e)
 
     def forward(self, x, index=0, output_shape=None):
         if self.preactivation:

@@ -77,8 +77,8 @@ def get_contract_fun(weight, implementation="reconstructed", separable=False):
 
 
 class _NoGradThroughHip(torch.autograd.Function):
-    """Attaches the HIP forward result to the graph with a backward that
-    raises: the backward kernels of the spectral path are not built."""
+    """Attaches a HIP forward result to the graph with a backward that
+    raises: for the cases the gradient functions do not cover."""
 
     @staticmethod
     def forward(ctx, y, *inputs):
@@ -87,7 +87,8 @@ class _NoGradThroughHip(torch.autograd.Function):
     @staticmethod
     def backward(ctx, *grads):
         raise NotImplementedError(
-            "backward of the HIP spectral path is not implemented (forward-only build)")
+            "gradients of the HIP spectral path cover output size == input size and "
+            "non-separable weights")
 
 
 _DUAL_NORM = {"forward": "backward", "backward": "forward", "ortho": "ortho"}
@@ -376,16 +377,13 @@ class SpectralConv(BaseSpectralConv):
         """complex_data=True: fftn / window / contraction / ifftn on complex
         fields (spectral_convolution.py:436-449, :500-538), output complex.
         With gradients (output size == input size, non-separable) through
-        _SpectralConvComplexFn on the dense window weight."""
+        _SpectralConvComplexFn on the dense window weight; other cases run
+        the same forward and raise if a backward reaches them."""
         sizes = list(x.shape[2:])
         kept, sl = self.window(sizes)
         out_sizes = self.output_sizes(sizes, output_shape)
-        if torch.is_grad_enabled() and (x.requires_grad or
-                                        any(p.requires_grad for p in self.parameters())):
-            if out_sizes != sizes or self.separable:
-                raise NotImplementedError(
-                    "gradients of the HIP spectral path cover output size == input size, "
-                    "non-separable weights")
+        if (torch.is_grad_enabled() and out_sizes == sizes and not self.separable and
+                (x.requires_grad or any(p.requires_grad for p in self.parameters()))):
             return _SpectralConvComplexFn.apply(x, self.dense_window_weight(sl), self.bias, kept,
                                                 self.fft_norm)
         xhat = Fh.fft_window(x.detach(), kept, self.fft_norm)
@@ -402,13 +400,12 @@ class SpectralConv(BaseSpectralConv):
     def _forward_autograd(self, x, output_shape=None):
         """Forward with gradients for x, the weight (through its dense window,
         so factorized weights get theirs through the reconstruction) and the
-        bias; output size == input size, non-separable."""
+        bias; output size == input size, non-separable.  Other cases run the
+        plain forward, whose backward raises."""
         sizes = list(x.shape[2:])
         out_sizes = self.output_sizes(sizes, output_shape)
         if out_sizes != sizes or self.separable:
-            raise NotImplementedError(
-                "gradients of the HIP spectral path cover output size == input size, "
-                "non-separable weights")
+            return self._forward_hip(x, output_shape)
         kept, sl = self.window(sizes)
         w = self.dense_window_weight(sl)
         return _SpectralConvFn.apply(x, w, self.bias, kept, self.fft_norm)

@@ -525,6 +525,35 @@ def fno_block_forward(x, index, n_layers, conv: dict, fno_skip: Optional[dict], 
     return x
 
 
+def spectral_resample(x, new_size):
+    """Spectral resample of 3+ spatial axes (resample.py:54-69): rfftn with
+    norm "forward", the first floor(m/2) and last ceil(m/2) entries of every
+    non-last axis (m = min(old, new) per axis) and the first min(old, new)//2+1
+    bins of the last axis copied to the same offsets from each end of a zero
+    spectrum of the new size, irfftn (norm "forward") to new_size."""
+    axes = list(range(2, x.ndim))
+    X = torch.fft.rfftn(x, dim=axes, norm="forward")
+    new_half = list(new_size[:-1]) + [new_size[-1] // 2 + 1]
+    Y = X
+    for d, ax in enumerate(axes):
+        n_old, n_new = Y.shape[ax], new_half[d]
+        if d == len(axes) - 1:
+            m = min(n_old, n_new)
+            src = torch.arange(m)
+            dst = src
+        else:
+            m = min(n_old, n_new)
+            lo, hi = m // 2, m - m // 2
+            src = torch.cat([torch.arange(lo), torch.arange(n_old - hi, n_old)])
+            dst = torch.cat([torch.arange(lo), torch.arange(n_new - hi, n_new)])
+        shape = list(Y.shape)
+        shape[ax] = n_new
+        Z = torch.zeros(shape, dtype=Y.dtype)
+        Z.index_copy_(ax, dst, Y.index_select(ax, src))
+        Y = Z
+    return torch.fft.irfftn(Y, s=list(new_size), dim=axes, norm="forward")
+
+
 def domain_pad(x, fractions):
     """DomainPadding.pad without resolution scaling (padding.py:54-138):
     round(p * n) zeros on both sides of every spatial axis."""

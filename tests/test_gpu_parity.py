@@ -793,12 +793,16 @@ def test_errors_raise(cuda_device):
         conv(torch.randn(1, 3, 8, 8))            # CPU input
     with pytest.raises(RuntimeError, match="4096"):
         conv(torch.randn(1, 3, 8, 8200, device=cuda_device))
-    # gradients cover output size == input size, non-separable weights
+    # gradients cover output size == input size, non-separable weights: other
+    # forwards run with gradients enabled and raise if a backward reaches them
     x = torch.randn(1, 3, 8, 8, device=cuda_device, requires_grad=True)
+    y = conv(x, output_shape=(16, 16))
+    assert list(y.shape[2:]) == [16, 16]
     with pytest.raises(NotImplementedError):
-        conv(x, output_shape=(16, 16))
+        y.sum().backward()
+    y = na.SpectralConv(3, 3, (4, 4), separable=True).to(cuda_device)(x)
     with pytest.raises(NotImplementedError):
-        na.SpectralConv(3, 3, (4, 4), separable=True).to(cuda_device)(x)
+        y.sum().backward()
 
 
 @pytest.mark.parametrize("Ci,Co,S", [(3, 4, (8, 9)), (32, 32, (16, 16, 16)), (20, 24, (37,)),

@@ -150,3 +150,28 @@ def test_fno_staged_bitrev():
     assert torch.equal(y[:, :, :, :], x[:, :, [0, 8, 4, 12, 2, 10, 6, 14, 1, 9, 5, 13, 3, 11, 7, 15], :])
     z = torch.randn(1, 1, 9, 10)
     assert torch.equal(z, na.FNOStaged._bitrev_spatial(z))
+
+
+def test_ada_in_norm_closed_form():
+    """AdaIN (normalization_layers.py:5-56): per-channel instance statistics,
+    then scale and shift from the two halves of mlp(embedding); one embedding
+    for every norm layer or one per layer (fno_block.py:304-321)."""
+    torch.manual_seed(3)
+    block = na.FNOBlocks(3, 4, (8, 8), n_layers=1, norm="ada_in", ada_in_features=5,
+                         channel_mlp_skip="linear")
+    e = torch.randn(5)
+    block.set_ada_in_embeddings(e)
+    x = torch.randn(2, 4, 10, 6)
+    norm = block.norm[0]
+    scale, shift = norm.mlp(e).split(4)
+    mean = x.mean(dim=(2, 3), keepdim=True)
+    var = x.var(dim=(2, 3), unbiased=False, keepdim=True)
+    want = (x - mean) / torch.sqrt(var + 1e-5) * scale.view(1, 4, 1, 1) + shift.view(1, 4, 1, 1)
+    assert torch.allclose(norm(x), want, atol=1e-5)
+    e2 = [torch.randn(5), torch.randn(5)]
+    block.set_ada_in_embeddings(*e2)
+    assert torch.equal(block.norm[1].embedding, e2[1])
+    cblock = na.FNOBlocks(3, 4, (8, 8), n_layers=1, norm="ada_in", ada_in_features=5,
+                          channel_mlp_skip="linear", complex_data=True)
+    cblock.set_ada_in_embeddings(e)
+    assert torch.equal(cblock.norm[0].fi.embedding, e)

@@ -157,6 +157,45 @@ def test_channel_mlp_bf16_products_rounding():
     assert (R.channel_mlp(xs, ws, bs, bf16_products=True) - ref).abs().max() > 0
 
 
+def _wave(shape, freqs):
+    """cos(2 pi sum_d f_d n_d / N_d) on a grid of the given shape."""
+    grids = torch.meshgrid(*[torch.arange(n, dtype=torch.float64) for n in shape], indexing="ij")
+    return torch.cos(sum(2 * math.pi * f * g / n for f, g, n in zip(freqs, grids, shape)))
+
+
+@pytest.mark.parametrize("old,new,freqs", [
+    ((8, 10, 12), (16, 20, 24), (3, -2, 5)),     # upsampling, even grids
+    ((16, 20, 24), (8, 10, 12), (3, -4, 5)),     # downsampling below both Nyquists
+    ((9, 11, 13), (12, 7, 20), (2, -3, 3)),      # odd grids, mixed up / down
+    ((6, 6, 6, 8), (12, 9, 6, 4), (1, 2, -2, 1)),  # 4D
+])
+def test_spectral_resample_band_limited(old, new, freqs):
+    """A plane wave strictly inside both grids' bands is resampled exactly."""
+    x = _wave(old, freqs)[None, None]
+    y = R.spectral_resample(x, new)
+    assert list(y.shape) == [1, 1, *new]
+    assert torch.allclose(y[0, 0], _wave(new, freqs), atol=1e-12)
+
+
+def test_spectral_resample_odd_grid_residues():
+    """On an odd axis of size 2k+1 the kept frequencies are -k-1 .. k-1 (the
+    slices [:m//2] and [-m//2:]): upsampling moves the old +k to -k-1, and
+    downsampling onto 2k+1 brings the old -k-1 to +k (same residue)."""
+    k = 3
+    old, new = (2 * k + 1, 4, 6), (12, 4, 6)
+    n = torch.arange(new[0], dtype=torch.float64)
+    x = _wave(old, (k, 0, 0))[None, None]          # e^{+ik..} + e^{-ik..}, halves
+    y = R.spectral_resample(x, new)[0, 0, :, 0, 0]
+    want = 0.5 * (torch.cos(2 * math.pi * (-k - 1) * n / new[0]) + torch.cos(2 * math.pi * k * n / new[0]))
+    assert torch.allclose(y, want, atol=1e-12)
+    x = _wave((12, 4, 6), (-k - 1, 0, 0))[None, None]
+    y = R.spectral_resample(x, (2 * k + 1, 4, 6))[0, 0, :, 0, 0]
+    m = torch.arange(2 * k + 1, dtype=torch.float64)
+    # the old +k+1 component is dropped (outside -k-1 .. k-1), -k-1 lands on +k
+    want = 0.5 * torch.cos(2 * math.pi * k * m / (2 * k + 1))
+    assert torch.allclose(y, want, atol=1e-12)
+
+
 def test_complex_valued_wrappers():
     """apply_complex is the complex-linear map with matrix A + iB when the real
     parts apply A and B; CGELU is GELU on each part."""
