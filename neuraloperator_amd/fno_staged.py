@@ -5,8 +5,18 @@ The layers are FNOBlocks' own (so the fused spectral block and channel-MLP
 calls apply per layer), with each layer's SpectralConv built at that layer's
 n_modes / max_n_modes.  The module keeps the reference's top-level attribute
 names (convs, fno_skips, channel_mlp, channel_mlp_skips, norm, lifting,
-projection, positional_embedding).  The fork's bit-reversed butterfly path
-(no_br=True) is not built.
+projection, positional_embedding).
+
+no_br=True (fno_staged.py:110-115, :478-493): the reference runs its layers
+on bit-reversed data, each SpectralConv replaced by a butterfly conv that
+takes and returns bit-reversed order, so such a layer computes P B P (P the
+bit reversal, B the natural-order block: every other op of the block is
+pointwise or a norm over all points).  Where its butterfly conv falls back
+(a dimension that is not a power of two, complex data, half precision, an
+output_shape, another conv module) the natural conv sees permuted data.  The
+forward here keeps the data in natural order and applies P only around the
+layers of the second kind, so the common case needs no permutation at all
+and the spectral work is the library's natural-order kernels either way.
 """
 from __future__ import annotations
 
@@ -78,8 +88,8 @@ class FNOStaged(FNOBlocks):
             raise ValueError(
                 "max_n_modes_per_layer must be None or have the same length as n_modes_per_layer")
         max_n_modes_per_layer = [list(m) for m in max_n_modes_per_layer]
-        if no_br:
-            raise NotImplementedError("no_br=True (bit-reversed butterfly spectral path) is not built")
+        if no_br and resolution_scaling_factor is not None:
+            raise NotImplementedError("no_br=True with resolution scaling is not built")
         pad_on = domain_padding is not None and (
             (isinstance(domain_padding, list) and sum(domain_padding) > 0)
             or (isinstance(domain_padding, (float, int)) and domain_padding > 0))
@@ -113,6 +123,7 @@ class FNOStaged(FNOBlocks):
         self.projection_channel_ratio = projection_channel_ratio
         self.projection_channels = int(projection_channel_ratio * hidden_channels)
         self.no_br = no_br
+        self._natural_convs = conv_module is SpectralConv
 
         # per-layer spectral convolutions (fno_staged.py:162-190)
         self.convs = nn.ModuleList([
@@ -172,8 +183,15 @@ class FNOStaged(FNOBlocks):
                 x = torch.index_select(x, dim, rev)
         return x
 
+    def _butterfly_layer(self, x, output_shape) -> bool:
+        """Whether the reference's butterfly conv runs this layer
+        (butterfly_fft.py:109-122), so that the layer is P B P."""
+        return (self._natural_convs and output_shape is None and not self.complex_data
+                and self.fno_block_precision == "full"
+                and all(n > 0 and (n & (n - 1)) == 0 for n in x.shape[2:]))
+
     def forward(self, x, output_shape=None, **kwargs):
-        """fno_staged.py:460-502 (without the no_br path)."""
+        """fno_staged.py:460-502."""
         if kwargs:
             warnings.warn(
                 f"FNOStaged.forward() received unexpected keyword arguments: {list(kwargs.keys())}. "
@@ -191,8 +209,17 @@ class FNOStaged(FNOBlocks):
         if self.domain_padding is not None:
             with maybe_profile(profiler, "fno/domain_padding/pad", x.device):
                 x = self.domain_padding.pad(x)
+        # permuted: x holds the reference's bit-reversed data (else its
+        # natural-order view)
+        permuted = False
         for layer_idx in range(self.n_layers):
+            if self.no_br and not self._butterfly_layer(x, output_shape[layer_idx]) and not permuted:
+                x, permuted = self._bitrev_spatial(x), True
+            elif self.no_br and self._butterfly_layer(x, output_shape[layer_idx]) and permuted:
+                x, permuted = self._bitrev_spatial(x), False
             x = super().forward(x, layer_idx, output_shape=output_shape[layer_idx])
+        if permuted:
+            x = self._bitrev_spatial(x)
         if self.domain_padding is not None:
             with maybe_profile(profiler, "fno/domain_padding/unpad", x.device):
                 x = self.domain_padding.unpad(x)

@@ -81,6 +81,6 @@ def resample(x, res_scale, axis, output_shape=None):
         return F.interpolate(x, size=new_size[0], mode="linear", align_corners=True)
     if len(axis) == 2:
         return F.interpolate(x, size=new_size, mode="bicubic", align_corners=True)
-    if list(axis) != list(range(x.ndim - len(axis), x.ndim)):
+    if sorted(a % x.ndim for a in axis) != list(range(x.ndim - len(axis), x.ndim)):
         raise NotImplementedError("the spectral resample covers the trailing spatial axes")
     return spectral_resample(x, new_size)

@@ -674,6 +674,59 @@ def test_fno_staged_matches_oracle(cuda_device):
     assert rel_err(y, ref) <= TOL
 
 
+def _staged_no_br_reference(model, x, output_shape):
+    """no_br=True as the reference runs it (fno_staged.py:478-493,
+    butterfly_fft.py:109-122): bit-reversed data through the layers, a
+    butterfly layer computing P B P and a fallback layer B on the permuted
+    data, then the inverse permutation; B is the natural-order block."""
+    P = na.FNOStaged._bitrev_spatial
+    r = P(model.lifting(x))
+    for i in range(model.n_layers):
+        shape = output_shape[i]
+        pow2 = all((n & (n - 1)) == 0 for n in r.shape[2:])
+        if pow2 and shape is None and not model.complex_data:
+            r = P(na.FNOBlocks.forward(model, P(r), i, output_shape=shape))
+        else:
+            r = na.FNOBlocks.forward(model, r, i, output_shape=shape)
+    return model.projection(P(r))
+
+
+@pytest.mark.parametrize("spatial,n_layers,complex_data,last_shape", [
+    ((16, 16), 1, False, None), ((32, 32), 4, False, None),     # test_fno_staged_no_br.py:46-54
+    ((12, 12), 2, False, None),                                  # :57-66, bit reversal a no-op
+    ((16, 32), 3, True, None),                                   # complex data: every layer falls back
+    ((16, 16), 3, False, (16, 16)),                              # output_shape: the last layer falls back
+])
+def test_fno_staged_no_br(spatial, n_layers, complex_data, last_shape, cuda_device):
+    """FNOStaged(no_br=True) against the reference's no_br semantics composed
+    from the natural-order blocks, and against no_br=False where the bit
+    reversals cancel."""
+    print(f"no_br {spatial} {n_layers} {complex_data} {last_shape}", flush=True)
+    torch.manual_seed(35)
+    kw = dict(in_channels=1, out_channels=1, hidden_channels=8, positional_embedding=None,
+              domain_padding=None, fno_skip="linear", use_channel_mlp=False, complex_data=complex_data)
+    model = na.FNOStaged([[8, 8]] * n_layers, no_br=True, **kw).to(cuda_device)
+    dtype = torch.cfloat if complex_data else torch.float32
+    x = torch.randn(2, 1, *spatial, dtype=dtype).to(cuda_device)
+    shapes = [None] * (n_layers - 1) + [last_shape]
+    with torch.no_grad():
+        y = model(x, output_shape=last_shape)
+        ref = _staged_no_br_reference(model, x, shapes)
+    assert y.shape == x.shape
+    assert rel_err(torch.view_as_real(y) if complex_data else y,
+                   torch.view_as_real(ref) if complex_data else ref) <= TOL
+    natural = na.FNOStaged([[8, 8]] * n_layers, no_br=False, **kw).to(cuda_device)
+    natural.load_state_dict(model.state_dict())
+    with torch.no_grad():
+        yn = natural(x, output_shape=last_shape)
+    cancels = not complex_data and last_shape is None
+    if cancels:
+        assert rel_err(y, yn) <= TOL
+    else:   # the permuted layers give another function
+        assert rel_err(torch.view_as_real(y) if complex_data else y,
+                       torch.view_as_real(yn) if complex_data else yn) > 1e-3
+
+
 @pytest.mark.parametrize("domain_padding", [0.1, [0.1, 0.2]])
 def test_fno_domain_padding(domain_padding, cuda_device):
     """FNO with domain padding (reference test_fno.py:219-253): output size kept,

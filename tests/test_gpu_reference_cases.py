@@ -104,6 +104,23 @@ def test_spectral_resample(old, new, cuda_device):
     assert rel_err(y, R.spectral_resample(x.double(), new)) <= TOL
 
 
+def test_resample_reference(cuda_device):
+    """test_resample.py:5-27: bicubic 2D on two axes, spectral 3D on three
+    (scales 0.5, 3, 4), shapes as the reference asserts and values against
+    the oracle."""
+    from neuraloperator_amd.resample import resample
+    g = torch.Generator().manual_seed(43)
+    a = torch.randn(10, 20, 40, 50, generator=g).to(cuda_device)
+    b = resample(a, [2, 3], [-2, -1])
+    assert b.shape[-1] == 3 * a.shape[-1] and b.shape[-2] == 2 * a.shape[-2]
+    a = torch.randn(2, 3, 40, 50, 60, generator=g)
+    with torch.no_grad():
+        b = resample(a.to(cuda_device), [0.5, 3, 4], [-3, -2, -1])
+    assert b.shape[-1] == 4 * a.shape[-1] and b.shape[-2] == 3 * a.shape[-2] and \
+        b.shape[-3] == int(0.5 * a.shape[-3])
+    assert rel_err(b, R.spectral_resample(a.double(), list(b.shape[2:]))) <= TOL
+
+
 def test_fno_block_resolution_scaling(cuda_device):
     """test_fno_block.py:6-68: the n_modes setter, and outputs resized by
     0.5 and 2 in 1-4 dims."""

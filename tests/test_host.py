@@ -137,7 +137,7 @@ def test_fno_staged_construction():
     with pytest.raises(ValueError):
         na.FNOStaged([(8, 8), (6, 6)], 1, 1, 8, max_n_modes_per_layer=[(8, 8)])
     with pytest.raises(NotImplementedError):
-        na.FNOStaged([(8, 8)], 1, 1, 8, no_br=True)
+        na.FNOStaged([(8, 8)], 1, 1, 8, no_br=True, resolution_scaling_factor=2)
 
 
 def test_fno_staged_bitrev():
