@@ -30,6 +30,17 @@ Pinning status (what checks each function; see tests/test_oracle.py):
   fno_block_forward / fno_forward -> composition of pinned pieces plus
     GridEmbeddingND coordinates checked against the linspace(0,1,N+1)[:-1]
     closed form.
+  spectral_conv_forward(complex_data=True) -> closed-form plane waves that
+    fix the last-axis window of the reference (frequency j - N/2 forward,
+    put back at j by the inverse).
+  domain_pad / domain_unpad -> round-trip identity and the padded sizes
+    round(p * n) on both sides.
+  cgelu / complex_apply -> GELU of each part; the complex matrix (A + iB) x.
+  channel_mlp(bf16_products=True) / bf16_round -> ties-to-even closed forms
+    (1 + 2^-8 -> 1, 1 + 3 * 2^-8 -> 1 + 2^-6, the hidden GELU rounded) and
+    bf16-exact operands, where the rounding must change nothing.
+  spectral_resample -> band-limited plane waves resampled exactly, and the
+    odd-grid residue rule of the reference's slices (-k-1 .. k-1).
   tucker_rank_from_fraction -> parity unpinned (restates tensorly 0.9.0's
     rank rule; tensorly is not importable here, and no reference test pins
     the resulting tuple).
