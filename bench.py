@@ -35,6 +35,9 @@ WORKLOADS = {
     "c2": (32, 64, 256, 256, (64, 64)),
     "c2_32": (32, 64, 256, 256, (32, 32)),
     "c1": (32, 64, 128, 128, (32, 32)),
+    # a non-power-of-two grid (the Darcy-flow resolution of the FNO paper):
+    # the generic path, pruned direct DFTs on both axes
+    "darcy421": (16, 32, 421, 421, (32, 32)),
 }
 
 

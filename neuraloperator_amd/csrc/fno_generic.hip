@@ -118,6 +118,86 @@ k_r2c_direct(const float* __restrict__ x, float2* __restrict__ out, int64_t rows
   }
 }
 
+// Last axis, real -> window, on the matrix cores.  For rows of N points and m
+// kept bins the pruned DFT is the product [rows x N] . [N x 2m] with
+//   T[n][2j] = cos(2 pi j n / N),  T[n][2j+1] = -sin(2 pi j n / N),
+// run on v_mfma_f32_16x16x4f32 (fp32 products and accumulation); the output
+// columns 2j, 2j+1 are the float2 bins of the window.  A wave owns 16 rows
+// and all NT = ceil(2m / 16) column tiles.  The k order is permuted so the x
+// loads stay row-contiguous: in k-step (c, i) lane group G supplies point
+// n = 16c + 4G + i, so lane (G, r) holds points 16c + 4G .. +3 of row r.  The
+// B entries come from the LDS twiddle table at index j n mod N, kept per
+// (tile, i) as a running index that steps by 16 j mod N per chunk.
+typedef float v4f_g __attribute__((ext_vector_type(4)));
+
+template <int NT>
+__global__ void __launch_bounds__(kThreads)
+k_r2c_mfma(const float* __restrict__ x, float* __restrict__ out, int64_t rows, int N, int m,
+           float scale) {
+  extern __shared__ float smem[];
+  float2* tw = reinterpret_cast<float2*>(smem);
+  for (int t = threadIdx.x; t < N; t += blockDim.x) tw[t] = twiddle_any(t, N);
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int G = lane >> 4, col = lane & 15;
+  const int64_t r0 = ((int64_t)blockIdx.x * (kThreads / 64) + wave) * 16;
+  if (r0 >= rows) return;   // no barrier follows
+  const int64_t row = r0 + col;                    // this lane's A row
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)(rows * N * 4));
+  int step[NT], idx[NT][4];
+  bool on[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int j = (16 * t + col) >> 1;
+    on[t] = j < m;
+    step[t] = (16 * j) % N;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) idx[t][i] = (j * (4 * G + i)) % N;
+  }
+  v4f_g acc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] = (v4f_g)0.f;
+  // points 16c + 4G + i of the row; past the row or the last row: zero
+  auto load = [&](int c, float (&dst)[4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int n = 16 * c + 4 * G + i;
+      const uint32_t off = (row < rows && n < N) ? (uint32_t)((row * N + n) * 4) : 0x80000000u;
+      dst[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx, (int)off, 0, 0));
+    }
+  };
+  const int nc = (N + 15) / 16;
+  float a[4], an[4];
+  load(0, a);
+  for (int c = 0; c < nc; ++c) {
+    if (c + 1 < nc) load(c + 1, an);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const float2 w = tw[idx[t][i]];
+        const float bv = on[t] ? ((col & 1) ? -w.y : w.x) : 0.f;
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], bv, acc[t], 0, 0, 0);
+        idx[t][i] += step[t];
+        if (idx[t][i] >= N) idx[t][i] -= N;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a[i] = an[i];
+  }
+  // D: lane (G, col) register r is row r0 + 4G + r, column 16t + col
+  const int w2 = 2 * m;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int q = 16 * t + col;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t ro = r0 + 4 * G + r;
+      if (ro < rows && q < w2) out[ro * w2 + q] = acc[t][r] * scale;
+    }
+  }
+}
+
 // Non-last axis (or the last axis of complex data), complex -> complex: window
 // entry j is frequency j + off (off = -m/2: the centred window):
 //   out[o, j, q] = s * sum_n in[o, n, q] exp(-2 pi i (j + off) n / N)
@@ -503,12 +583,32 @@ int rfft_window(const float* x, float2* xhat, int64_t planes, int32_t ndim, cons
     if (r2c_fft_supported(N, m, rows)) {
       int rc = r2c_fft(x, dst, rows, N, m, sc, st);
       if (rc) return rc;
+    } else if (m <= 64 && rows >= 16384 && rows * (int64_t)N * 4 < (int64_t(1) << 31)) {
+      // many rows: the DFT product on the matrix cores, 64 rows per workgroup
+      const unsigned blocks = (unsigned)((rows + 63) / 64);
+      const size_t lds = (size_t)N * 8;
+      float* o = reinterpret_cast<float*>(dst);
+#define FNO_R2C_MFMA(nt)                                                                          \
+  case nt:                                                                                        \
+    hipLaunchKernelGGL(k_r2c_mfma<nt>, dim3(blocks), dim3(kThreads), lds, st, x, o, rows, N, m, sc); \
+    break;
+      switch ((2 * m + 15) / 16) {
+        FNO_R2C_MFMA(1) FNO_R2C_MFMA(2) FNO_R2C_MFMA(3) FNO_R2C_MFMA(4)
+        FNO_R2C_MFMA(5) FNO_R2C_MFMA(6) FNO_R2C_MFMA(7) FNO_R2C_MFMA(8)
+        default: break;
+      }
+#undef FNO_R2C_MFMA
+      int rc = launch_status("k_r2c_mfma");
+      if (rc) return rc;
     } else {
       int rpb = (int)((48 * 1024 - 8 * N) / (4 * N));
       if (rpb < 1) rpb = 1;
       if (rpb > 64) rpb = 64;
-      // one pass of 16 tasks per workgroup: more workgroups for few bins
-      const int rfill = (16 + m - 1) / m;
+      // one pass of 16 tasks per workgroup: more workgroups for few bins,
+      // unless there are rows enough for 2048 workgroups of more rows each
+      // (every workgroup builds the N-entry twiddle table first)
+      int rfill = (16 + m - 1) / m;
+      if (rows / 2048 > rfill) rfill = (int)(rows / 2048 < 64 ? rows / 2048 : 64);
       if (rpb > rfill) rpb = rfill;
       const size_t lds = (size_t)N * 8 + (size_t)rpb * N * 4;
       const int64_t blocks = (rows + rpb - 1) / rpb;
@@ -702,6 +802,12 @@ int irfft_window(const float2* yhat, const float* bias, float* y, int64_t batch,
     } else {
       const int K = m < Np / 2 + 1 ? m : Np / 2 + 1;
       int rpb = kThreads / (Np < kThreads ? Np : kThreads);
+      // rows enough for 2048 workgroups: more rows per workgroup, so the
+      // Np-entry twiddle table each one builds is shared, within 48 KB of LDS
+      if (rows / 2048 > rpb) {
+        const int64_t lds_rows = (48 * 1024 - (int64_t)Np * 8) / ((int64_t)K * 8);
+        rpb = (int)(rows / 2048 < lds_rows ? rows / 2048 : lds_rows);
+      }
       if (rpb < 1) rpb = 1;
       if (rpb > 32) rpb = 32;
       const size_t lds = (size_t)Np * 8 + (size_t)rpb * K * 8;

@@ -828,6 +828,26 @@ def test_fno_complex_data(dim, size, nm, cuda_device):
     assert rel_err(torch.view_as_real(y), torch.view_as_real(ref)) <= TOL
 
 
+@pytest.mark.parametrize("shape,modes", [((64, 256, 421), (17,)), ((64, 256, 421), (64,)),
+                                         ((64, 256, 421), (9,)), ((4, 32, 128, 421), (16, 17)),
+                                         ((2, 64, 130, 250), (20, 33))])
+def test_rfft_window_matrix_core_dft(shape, modes, cuda_device):
+    """Last-axis pruned DFTs of 16384+ rows of a size the line FFTs do not
+    cover run as the DFT product on the matrix cores: the window against
+    float64 numpy (rfftn with norm="forward", centred rows)."""
+    print(f"rfft window mfma {shape} {modes}", flush=True)
+    x = torch.randn(*shape, generator=torch.Generator().manual_seed(44))
+    with torch.no_grad():
+        y = Fh.rfft_window(x.to(cuda_device), list(modes), "forward")
+    spatial = shape[2:]
+    X = np.fft.rfftn(x.double().numpy(), axes=tuple(range(2, x.ndim)), norm="forward")
+    for d, (n, m) in enumerate(zip(spatial[:-1], modes[:-1])):
+        X = np.fft.fftshift(X, axes=2 + d)
+        X = np.take(X, range(n // 2 - m // 2, n // 2 - m // 2 + m), axis=2 + d)
+    X = X[..., :modes[-1]]
+    assert rel_err(torch.view_as_real(y), torch.view_as_real(torch.from_numpy(X))) <= TOL
+
+
 def test_deterministic(cuda_device):
     torch.manual_seed(11)
     conv = na.SpectralConv(64, 64, (64, 64)).to(cuda_device)
