@@ -306,6 +306,98 @@ k_c2r_direct(const float2* __restrict__ in, float* __restrict__ out, const float
   }
 }
 
+// Last axis, window -> real length Np on the matrix cores (the irfft of
+// k_c2r_direct as a product): y[r, n] = s sum_k A[r, k] T[k, n] + bias with
+//   A[r, 2j] = c_j Re Z_j,  A[r, 2j+1] = c_j Im Z_j   (Hermitian fix-ups as in
+//   k_c2r_direct), T[2j, n] = cos(2 pi j n / Np), T[2j+1, n] = -sin(...).
+// A wave owns 16 rows and CT column tiles of 16 points; a workgroup's four
+// waves take consecutive column tiles of the same rows.  In k-step (c, i)
+// lane group G supplies k = 16c + 4G + i (four consecutive floats of a Z row
+// per lane), and the B entry of lane (G, col) in tile t is the twiddle at
+// j n mod Np with j = 8c + 2G + i/2, kept as a running index per (t, i/2).
+template <int CT>
+__global__ void __launch_bounds__(kThreads)
+k_c2r_mfma(const float2* __restrict__ in, float* __restrict__ out, const float* __restrict__ bias,
+           int64_t rows, int64_t rows_per_plane, int channels, int N, int Np, int m, int enforce,
+           int col_groups, float scale) {
+  extern __shared__ float smem[];
+  float2* tw = reinterpret_cast<float2*>(smem);
+  for (int t = threadIdx.x; t < Np; t += blockDim.x) tw[t] = twiddle_any(t, Np);
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int G = lane >> 4, col = lane & 15;
+  const int64_t r0 = (int64_t)(blockIdx.x / col_groups) * 16;
+  const int tile0 = ((int)(blockIdx.x % col_groups) * (kThreads / 64) + wave) * CT;
+  const int ntiles = (Np + 15) / 16;
+  if (tile0 >= ntiles) return;   // no barrier follows
+  const int K = m < Np / 2 + 1 ? m : Np / 2 + 1;   // bins used
+  const int64_t row = r0 + col;                      // this lane's A row
+  const float* zf = reinterpret_cast<const float*>(in);
+  const __amdgpu_buffer_rsrc_t rz = make_rsrc(zf, (uint32_t)(rows * m * 8));
+  int idx[CT][2], step[CT];
+#pragma unroll
+  for (int t = 0; t < CT; ++t) {
+    const int n = 16 * (tile0 + t) + col;
+    step[t] = (int)((8LL * n) % Np);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) idx[t][h] = (int)(((int64_t)(2 * G + h) * n) % Np);
+  }
+  v4f_g acc[CT];
+#pragma unroll
+  for (int t = 0; t < CT; ++t) acc[t] = (v4f_g)0.f;
+  // A entries k = 16c + 4G + i of the row, Hermitian weights applied
+  auto load = [&](int c, float (&dst)[4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int k = 16 * c + 4 * G + i, j = k >> 1;
+      const bool live = row < rows && j < K;
+      const uint32_t off = live ? (uint32_t)((row * m * 2 + k) * 4) : 0x80000000u;
+      float v = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rz, (int)off, 0, 0));
+      if (k & 1) {   // imaginary part
+        if (j == 0 || (enforce && (Np % 2 == 0) && j == N / 2)) v = 0.f;
+      }
+      const float cw = (j == 0 || ((Np % 2 == 0) && j == Np / 2)) ? 1.f : 2.f;
+      dst[i] = v * cw;
+    }
+  };
+  const int nc = (2 * K + 15) / 16;
+  float a[4], an[4];
+  load(0, a);
+  for (int c = 0; c < nc; ++c) {
+    if (c + 1 < nc) load(c + 1, an);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int t = 0; t < CT; ++t) {
+        const float2 w = tw[idx[t][i >> 1]];
+        const float bv = (i & 1) ? -w.y : w.x;
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], bv, acc[t], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < CT; ++t)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        idx[t][h] += step[t];
+        if (idx[t][h] >= Np) idx[t][h] -= Np;
+      }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a[i] = an[i];
+  }
+  // D: lane (G, col) register r is row r0 + 4G + r, point 16 (tile0 + t) + col
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int64_t ro = r0 + 4 * G + r;
+    if (ro >= rows) continue;
+    const float bb = bias ? bias[(ro / rows_per_plane) % channels] : 0.f;
+#pragma unroll
+    for (int t = 0; t < CT; ++t) {
+      const int n = 16 * (tile0 + t) + col;
+      if (n < Np) out[ro * Np + n] = acc[t][r] * scale + bb;
+    }
+  }
+}
+
 // ----------------------------------------------------------------- contraction
 // y[b, o, k] = sum_i x[b, i, k] * w[i*sWi + o*sWo + k*sWk]     (complex)
 // One lane per mode k; each thread owns a TB x TO tile of (b, o).
@@ -798,6 +890,18 @@ int irfft_window(const float2* yhat, const float* bias, float* y, int64_t batch,
     if (c2r_fft_supported(Np, rows)) {
       int rc = c2r_fft(src, y, bias, rows, rows_per_plane, channels, N, Np, m, enforce,
                        (float)scale, st);
+      if (rc) return rc;
+    } else if (m <= 64 && rows >= 16384 && rows * (int64_t)(Np > 2 * m ? Np : 2 * m) * 4 <
+                                                  (int64_t(1) << 31)) {
+      // many rows: the synthesis product on the matrix cores; a workgroup's
+      // four waves take 8 column tiles each of the same 16 rows
+      constexpr int CT = 8;
+      const int col_groups = ((Np + 15) / 16 + 4 * CT - 1) / (4 * CT);
+      const unsigned blocks = (unsigned)(((rows + 15) / 16) * col_groups);
+      hipLaunchKernelGGL(k_c2r_mfma<CT>, dim3(blocks), dim3(kThreads), (size_t)Np * 8, st, src, y,
+                         bias, rows, rows_per_plane, channels, N, Np, m, enforce, col_groups,
+                         (float)scale);
+      int rc = launch_status("k_c2r_mfma");
       if (rc) return rc;
     } else {
       const int K = m < Np / 2 + 1 ? m : Np / 2 + 1;

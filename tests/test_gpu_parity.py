@@ -848,6 +848,30 @@ def test_rfft_window_matrix_core_dft(shape, modes, cuda_device):
     assert rel_err(torch.view_as_real(y), torch.view_as_real(torch.from_numpy(X))) <= TOL
 
 
+@pytest.mark.parametrize("B,sizes,nm,out", [(4, (128, 421), (16, 32), None),
+                                            (4, (128, 210), (16, 32), (128, 421)),
+                                            (512, (421,), (30,), None),
+                                            (4, (128, 250), (16, 40), None)])
+def test_spectral_conv_matrix_core_dft(B, sizes, nm, out, cuda_device):
+    """SpectralConv on grids the line FFTs do not cover, with 16384+ rows on
+    the last axis: forward and inverse last-axis DFTs as products on the
+    matrix cores (bias, Hermitian weights, resized output), against the
+    float64 oracle."""
+    print(f"spectral conv mfma dft B{B} {sizes} {nm} {out}", flush=True)
+    torch.manual_seed(45)
+    conv = na.SpectralConv(32, 32, nm).to(cuda_device)
+    with torch.no_grad():
+        conv.bias.normal_()
+    x = torch.randn(B, 32, *sizes)
+    with torch.no_grad():
+        y = conv(x.to(cuda_device), output_shape=out)
+    ref = R.spectral_conv_forward(x.double(), conv.weight.to_tensor().detach().cpu().to(torch.complex128),
+                                  conv.bias.detach().cpu().double(), conv.n_modes, conv.max_n_modes,
+                                  output_shape=out)
+    assert list(y.shape) == list(ref.shape)
+    assert rel_err(y, ref) <= TOL
+
+
 def test_deterministic(cuda_device):
     torch.manual_seed(11)
     conv = na.SpectralConv(64, 64, (64, 64)).to(cuda_device)
