@@ -252,12 +252,20 @@ k_c2c_inv_direct(const float2* __restrict__ in, float2* __restrict__ out, int64_
     const int64_t o = t2 / Np;
     const float2* src = in + o * (int64_t)m * inner + q;
     float2 acc = make_float2(0.f, 0.f);
+    // window entry j is frequency t = (j + off) mod N, at twiddle t n mod Np:
+    // both indices advance by one step per entry (t wraps at N to 0)
+    int t = off % N;
+    if (t < 0) t += N;
+    int idx = (int)(((int64_t)t * n) % Np);
     for (int j = 0; j < m; ++j) {
-      int t = (j + off) % N;
-      if (t < 0) t += N;
-      if (t >= Np) continue;
-      const int idx = (int)(((int64_t)t * n) % Np);
-      cfma(acc, src[(int64_t)j * inner], tw[idx]);
+      if (t < Np) cfma(acc, src[(int64_t)j * inner], tw[idx]);
+      ++t;
+      idx += n;
+      if (idx >= Np) idx -= Np;
+      if (t == N) {
+        t = 0;
+        idx = 0;
+      }
     }
     out[task] = cscale(acc, scale);
   }
@@ -580,6 +588,13 @@ static int grid_for(int64_t total) {
   return (int)g;
 }
 
+// grid-stride kernels that first build an N-entry twiddle table: at most
+// 2048 workgroups (8 per CU), so each table serves many tasks
+static int grid_for_table(int64_t total) {
+  const int g = grid_for(total);
+  return g > 2048 ? 2048 : g;
+}
+
 static int validate_axes(int32_t ndim, const int32_t* sizes, const int32_t* modes) {
   FNO_CHECK_ARG(ndim >= 1 && ndim <= 4, "ndim must be 1..4 (got %d)", ndim);
   FNO_CHECK_ARG(sizes && modes, "sizes/modes must not be NULL");
@@ -724,7 +739,7 @@ int rfft_window(const float* x, float2* xhat, int64_t planes, int32_t ndim, cons
     if (c2c_fft_supported(N, outer, inner)) {
       rc = c2c_fft_fwd(src, dst, outer, inner, N, m, -(m / 2), sc, st);
     } else {
-      hipLaunchKernelGGL(k_c2c_fwd_direct, dim3(grid_for(outer * m * inner)), dim3(kThreads),
+      hipLaunchKernelGGL(k_c2c_fwd_direct, dim3(grid_for_table(outer * m * inner)), dim3(kThreads),
                          (size_t)N * 8, st, src, dst, outer, N, inner, m, -(m / 2), sc);
       rc = launch_status("k_c2c_fwd_direct");
     }
@@ -740,7 +755,7 @@ int rfft_window(const float* x, float2* xhat, int64_t planes, int32_t ndim, cons
 static int c2c_axis_fwd(const float2* src, float2* dst, int64_t outer, int N, int64_t inner, int m,
                         int off, float sc, hipStream_t st) {
   if (c2c_fft_supported(N, outer, inner)) return c2c_fft_fwd(src, dst, outer, inner, N, m, off, sc, st);
-  hipLaunchKernelGGL(k_c2c_fwd_direct, dim3(grid_for(outer * m * inner)), dim3(kThreads),
+  hipLaunchKernelGGL(k_c2c_fwd_direct, dim3(grid_for_table(outer * m * inner)), dim3(kThreads),
                      (size_t)N * 8, st, src, dst, outer, N, inner, m, off, sc);
   return launch_status("k_c2c_fwd_direct");
 }
@@ -749,7 +764,7 @@ static int c2c_axis_inv(const float2* src, float2* dst, int64_t outer, int N, in
                         int m, int off, float sc, hipStream_t st) {
   if (c2c_fft_supported(Np, outer, inner))
     return c2c_fft_inv(src, dst, outer, inner, N, Np, m, off, sc, st);
-  hipLaunchKernelGGL(k_c2c_inv_direct, dim3(grid_for(outer * Np * inner)), dim3(kThreads),
+  hipLaunchKernelGGL(k_c2c_inv_direct, dim3(grid_for_table(outer * Np * inner)), dim3(kThreads),
                      (size_t)Np * 8, st, src, dst, outer, N, Np, inner, m, off, sc);
   return launch_status("k_c2c_inv_direct");
 }
@@ -873,7 +888,7 @@ int irfft_window(const float2* yhat, const float* bias, float* y, int64_t batch,
     if (c2c_fft_supported(Np, outer, inner)) {
       rc = c2c_fft_inv(src, dst, outer, inner, N, Np, m, -(m / 2), 1.f, st);
     } else {
-      hipLaunchKernelGGL(k_c2c_inv_direct, dim3(grid_for(outer * Np * inner)), dim3(kThreads),
+      hipLaunchKernelGGL(k_c2c_inv_direct, dim3(grid_for_table(outer * Np * inner)), dim3(kThreads),
                          (size_t)Np * 8, st, src, dst, outer, N, Np, inner, m, -(m / 2), 1.f);
       rc = launch_status("k_c2c_inv_direct");
     }
