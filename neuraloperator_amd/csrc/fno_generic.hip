@@ -271,6 +271,125 @@ k_c2c_inv_direct(const float2* __restrict__ in, float2* __restrict__ out, int64_
   }
 }
 
+// Non-last axis (or the last axis of complex data), complex -> complex, on the
+// matrix cores: Out[o, r, q] = s sum_{j<S} W(r, j) In[o, j, q] over the C =
+// outer * inner columns (o, q), as the real product
+//   D[2r + po][c] = sum_{2j + pi} A[2r + po][2j + pi] B[2j + pi][c]
+// with A the real form of the twiddle w = W(r, j) (re: w.re, -w.im; im: w.im,
+// w.re) and B the real and imaginary parts of In.
+//   DIR = -1 (analysis):  R = m rows, S = N points,  W = exp(-2 pi i f n / N),
+//                         f = (r + off) mod N
+//   DIR = +1 (synthesis): R = Np points, S = m entries, W = exp(2 pi i r t / Np),
+//                         t = (j + off) mod N, zero where t >= Np
+// A wave owns MT row tiles of 16 and one column tile of 16.  In k-step ks lane
+// group G supplies k = 4 ks + G, i.e. j = 2 ks + G/2 and part G & 1, so j steps
+// by 2 per k-step and the twiddle index j f mod N (analysis) or r t mod Np
+// (synthesis) is a running sum per row tile.
+template <int DIR, int MT>
+__global__ void __launch_bounds__(kThreads)
+k_c2c_axis_mfma(const float2* __restrict__ in, float2* __restrict__ out, int64_t outer,
+                int64_t inner, int N, int Np, int m, int off, int mgroups, float scale) {
+  extern __shared__ float smem[];
+  float2* tw = reinterpret_cast<float2*>(smem);
+  const int L = DIR < 0 ? N : Np;
+  for (int t = threadIdx.x; t < L; t += blockDim.x) tw[t] = twiddle_any(t, L);
+  __syncthreads();
+  const int R = DIR < 0 ? m : Np, S = DIR < 0 ? N : m;
+  const int64_t C = outer * inner;
+  const int lane = threadIdx.x & 63, G = lane >> 4, col = lane & 15;
+  const int64_t wid = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  const int mt0 = (int)(wid % mgroups) * MT;
+  const int64_t c0 = (wid / mgroups) * 16;
+  const int mtiles = (2 * R + 15) / 16;
+  if (c0 >= C || mt0 >= mtiles) return;   // no barrier follows
+  const int pi = G & 1;
+  // B column of this lane
+  const int64_t cb = c0 + col;
+  const bool cl = cb < C;
+  const int64_t ob = cl ? cb / inner : 0, qb = cl ? cb % inner : 0;
+  const float* inf = reinterpret_cast<const float*>(in);
+  const __amdgpu_buffer_rsrc_t rin = make_rsrc(inf, (uint32_t)(outer * S * inner * 8));
+  // A rows of this lane: row r of tile t, its running twiddle index
+  int rr[MT], idx[MT], step[MT];
+  int t = 0;   // synthesis: frequency of entry j = G / 2 (+ 2 per k-step)
+  if (DIR > 0) {
+    t = (G >> 1) + off;
+    t %= N;
+    if (t < 0) t += N;
+  }
+#pragma unroll
+  for (int u = 0; u < MT; ++u) {
+    const int rho = 16 * (mt0 + u) + col;
+    rr[u] = rho >> 1;
+    if (DIR < 0) {
+      int f = (rr[u] + off) % N;
+      if (f < 0) f += N;
+      idx[u] = (int)(((int64_t)f * (G >> 1)) % N);
+      step[u] = (int)((2LL * f) % N);
+    } else {
+      idx[u] = (int)(((int64_t)rr[u] * t) % Np);
+      step[u] = (int)((2LL * rr[u]) % Np);
+    }
+  }
+  v4f_g acc[MT];
+#pragma unroll
+  for (int u = 0; u < MT; ++u) acc[u] = (v4f_g)0.f;
+  const int ksteps = (2 * S + 3) / 4;
+  auto load_b = [&](int ks) __attribute__((always_inline)) {
+    const int j = 2 * ks + (G >> 1);
+    const uint32_t off_b = (cl && j < S) ? (uint32_t)((((ob * S + j) * inner + qb) * 2 + pi) * 4)
+                                         : 0x80000000u;
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rin, (int)off_b, 0, 0));
+  };
+  // B values in blocks of KB k-steps, the next block in flight; k-steps past
+  // the last read zero (j >= S), so a partial last block adds nothing
+  constexpr int KB = 8;
+  float bc[KB], bn[KB];
+#pragma unroll
+  for (int i = 0; i < KB; ++i) bc[i] = load_b(i);
+  for (int k0 = 0; k0 < ksteps; k0 += KB) {
+#pragma unroll
+    for (int i = 0; i < KB; ++i) bn[i] = k0 + KB < ksteps ? load_b(k0 + KB + i) : 0.f;
+#pragma unroll
+    for (int i = 0; i < KB; ++i) {
+      const bool live = DIR < 0 || t < Np;
+#pragma unroll
+      for (int u = 0; u < MT; ++u) {
+        const float2 w = tw[idx[u]];
+        const float wi = DIR < 0 ? -w.y : w.y;   // imaginary part of W
+        const int po = col & 1;                   // A row 2r + po of this lane
+        float av = (po == pi) ? w.x : (po ? wi : -wi);
+        av = live && rr[u] < R ? av : 0.f;
+        acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bc[i], acc[u], 0, 0, 0);
+        idx[u] += step[u];
+        if (idx[u] >= L) idx[u] -= L;
+      }
+      if (DIR > 0) {   // the entries two further on: t + 2, wrapping at N
+        t += 2;
+        if (t >= N) {
+          while (t >= N) t -= N;
+#pragma unroll
+          for (int u = 0; u < MT; ++u) idx[u] = (int)(((int64_t)rr[u] * t) % Np);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < KB; ++i) bc[i] = bn[i];
+  }
+  // D: lane (G, col) register v is row 16 (mt0 + u) + 4G + v, column c0 + col
+  const int64_t cd = c0 + col;
+  if (cd >= C) return;
+  const int64_t od = cd / inner, qd = cd % inner;
+  float* outf = reinterpret_cast<float*>(out);
+#pragma unroll
+  for (int u = 0; u < MT; ++u)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int rho = 16 * (mt0 + u) + 4 * G + v, r = rho >> 1;
+      if (r < R) outf[((od * R + r) * inner + qd) * 2 + (rho & 1)] = acc[u][v] * scale;
+    }
+}
+
 // Last axis, window -> real length N' (irfft semantics) + bias:
 //   y[r, n] = s * sum_{j < N'/2+1} c_j Re(Z_j exp(2 pi i j n / N')) + bias[channel(r)]
 __global__ void __launch_bounds__(kThreads)
@@ -595,6 +714,11 @@ static int grid_for_table(int64_t total) {
   return g > 2048 ? 2048 : g;
 }
 
+static int c2c_axis_fwd(const float2* src, float2* dst, int64_t outer, int N, int64_t inner, int m,
+                        int off, float sc, hipStream_t st);
+static int c2c_axis_inv(const float2* src, float2* dst, int64_t outer, int N, int Np, int64_t inner,
+                        int m, int off, float sc, hipStream_t st);
+
 static int validate_axes(int32_t ndim, const int32_t* sizes, const int32_t* modes) {
   FNO_CHECK_ARG(ndim >= 1 && ndim <= 4, "ndim must be 1..4 (got %d)", ndim);
   FNO_CHECK_ARG(sizes && modes, "sizes/modes must not be NULL");
@@ -735,14 +859,7 @@ int rfft_window(const float* x, float2* xhat, int64_t planes, int32_t ndim, cons
     const int N = sizes[d], m = modes[d];
     float2* dst = (d == 0) ? xhat : bufs[(ndim - 1 - d) % 2];
     const float sc = (d == 0) ? (float)scale : 1.f;
-    int rc;
-    if (c2c_fft_supported(N, outer, inner)) {
-      rc = c2c_fft_fwd(src, dst, outer, inner, N, m, -(m / 2), sc, st);
-    } else {
-      hipLaunchKernelGGL(k_c2c_fwd_direct, dim3(grid_for_table(outer * m * inner)), dim3(kThreads),
-                         (size_t)N * 8, st, src, dst, outer, N, inner, m, -(m / 2), sc);
-      rc = launch_status("k_c2c_fwd_direct");
-    }
+    const int rc = c2c_axis_fwd(src, dst, outer, N, inner, m, -(m / 2), sc, st);
     if (rc) return rc;
     src = dst;
   }
@@ -752,9 +869,31 @@ int rfft_window(const float* x, float2* xhat, int64_t planes, int32_t ndim, cons
 // ------------------------------------------------- complex-data windows
 // One axis of a complex window transform: line FFTs for 64/128/256 points,
 // direct sums otherwise.  Window entry j is frequency j + off.
+// the matrix-core form when there are columns enough for 64+ waves and the
+// buffer offsets fit 31 bits
+static bool c2c_mfma_ok(int64_t outer, int64_t inner, int S, int R) {
+  const int64_t C = outer * inner;
+  return C >= 1024 && C * (S > R ? S : R) * 8 < (int64_t(1) << 31);
+}
+
+template <int DIR, int MT>
+static int launch_c2c_mfma(const float2* src, float2* dst, int64_t outer, int64_t inner, int N,
+                           int Np, int m, int off, float sc, hipStream_t st) {
+  const int R = DIR < 0 ? m : Np;
+  const int mgroups = ((2 * R + 15) / 16 + MT - 1) / MT;
+  const int64_t waves = (outer * inner + 15) / 16 * mgroups;
+  const unsigned blocks = (unsigned)((waves + kThreads / 64 - 1) / (kThreads / 64));
+  hipLaunchKernelGGL((k_c2c_axis_mfma<DIR, MT>), dim3(blocks), dim3(kThreads),
+                     (size_t)(DIR < 0 ? N : Np) * 8, st, src, dst, outer, inner, N, Np, m, off,
+                     mgroups, sc);
+  return launch_status("k_c2c_axis_mfma");
+}
+
 static int c2c_axis_fwd(const float2* src, float2* dst, int64_t outer, int N, int64_t inner, int m,
                         int off, float sc, hipStream_t st) {
   if (c2c_fft_supported(N, outer, inner)) return c2c_fft_fwd(src, dst, outer, inner, N, m, off, sc, st);
+  if (c2c_mfma_ok(outer, inner, N, m))
+    return launch_c2c_mfma<-1, 1>(src, dst, outer, inner, N, N, m, off, sc, st);
   hipLaunchKernelGGL(k_c2c_fwd_direct, dim3(grid_for_table(outer * m * inner)), dim3(kThreads),
                      (size_t)N * 8, st, src, dst, outer, N, inner, m, off, sc);
   return launch_status("k_c2c_fwd_direct");
@@ -764,6 +903,8 @@ static int c2c_axis_inv(const float2* src, float2* dst, int64_t outer, int N, in
                         int m, int off, float sc, hipStream_t st) {
   if (c2c_fft_supported(Np, outer, inner))
     return c2c_fft_inv(src, dst, outer, inner, N, Np, m, off, sc, st);
+  if (c2c_mfma_ok(outer, inner, m, Np))
+    return launch_c2c_mfma<1, 4>(src, dst, outer, inner, N, Np, m, off, sc, st);
   hipLaunchKernelGGL(k_c2c_inv_direct, dim3(grid_for_table(outer * Np * inner)), dim3(kThreads),
                      (size_t)Np * 8, st, src, dst, outer, N, Np, inner, m, off, sc);
   return launch_status("k_c2c_inv_direct");
@@ -884,14 +1025,7 @@ int irfft_window(const float2* yhat, const float* bias, float* y, int64_t batch,
     for (int a = d + 1; a < ndim; ++a) inner *= modes[a];
     float2* dst = bufs[d % 2];
     const int N = in_sizes[d], Np = out_sizes[d], m = modes[d];
-    int rc;
-    if (c2c_fft_supported(Np, outer, inner)) {
-      rc = c2c_fft_inv(src, dst, outer, inner, N, Np, m, -(m / 2), 1.f, st);
-    } else {
-      hipLaunchKernelGGL(k_c2c_inv_direct, dim3(grid_for_table(outer * Np * inner)), dim3(kThreads),
-                         (size_t)Np * 8, st, src, dst, outer, N, Np, inner, m, -(m / 2), 1.f);
-      rc = launch_status("k_c2c_inv_direct");
-    }
+    const int rc = c2c_axis_inv(src, dst, outer, N, Np, inner, m, -(m / 2), 1.f, st);
     if (rc) return rc;
     src = dst;
   }
