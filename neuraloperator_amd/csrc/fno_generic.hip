@@ -891,6 +891,9 @@ static int launch_c2c_mfma(const float2* src, float2* dst, int64_t outer, int64_
 
 static int c2c_axis_fwd(const float2* src, float2* dst, int64_t outer, int N, int64_t inner, int m,
                         int off, float sc, hipStream_t st) {
+  // lines fewer than a 16-line tile apart: the product form reads them whole
+  if (inner < 16 && c2c_mfma_ok(outer, inner, N, m))
+    return launch_c2c_mfma<-1, 1>(src, dst, outer, inner, N, N, m, off, sc, st);
   if (c2c_fft_supported(N, outer, inner)) return c2c_fft_fwd(src, dst, outer, inner, N, m, off, sc, st);
   if (c2c_mfma_ok(outer, inner, N, m))
     return launch_c2c_mfma<-1, 1>(src, dst, outer, inner, N, N, m, off, sc, st);
@@ -901,6 +904,8 @@ static int c2c_axis_fwd(const float2* src, float2* dst, int64_t outer, int N, in
 
 static int c2c_axis_inv(const float2* src, float2* dst, int64_t outer, int N, int Np, int64_t inner,
                         int m, int off, float sc, hipStream_t st) {
+  if (inner < 16 && c2c_mfma_ok(outer, inner, m, Np))
+    return launch_c2c_mfma<1, 4>(src, dst, outer, inner, N, Np, m, off, sc, st);
   if (c2c_fft_supported(Np, outer, inner))
     return c2c_fft_inv(src, dst, outer, inner, N, Np, m, off, sc, st);
   if (c2c_mfma_ok(outer, inner, m, Np))
