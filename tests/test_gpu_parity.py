@@ -623,6 +623,29 @@ def test_fno_reference_matrix(n_dim, stabilizer, lifting_channel_ratio, preactiv
     assert not unused, unused
 
 
+@pytest.mark.parametrize("sizes,nm,out", [((64, 37), (16, 12), None), ((37,), (12,), None),
+                                          ((40, 37), (12, 12), (64, 50)), ((9, 10, 37), (6, 6, 8), None)])
+def test_complex_data_matrix_core_axes(sizes, nm, out, cuda_device):
+    """Complex data with 1024+ columns per axis: the analysis and synthesis
+    along every axis the line FFTs do not take run as products on the matrix
+    cores, the last axis with the reference's window (frequency j - N/2
+    forward, j inverse), against the float64 oracle."""
+    print(f"complex mfma axes {sizes} {nm} {out}", flush=True)
+    torch.manual_seed(46)
+    B = 4096 if len(sizes) == 1 else 16
+    conv = na.SpectralConv(8, 8, nm, complex_data=True).to(cuda_device)
+    with torch.no_grad():
+        conv.bias.normal_()
+    x = torch.randn(B, 8, *sizes, dtype=torch.complex64)
+    with torch.no_grad():
+        y = conv(x.to(cuda_device), output_shape=out)
+    ref = R.spectral_conv_forward(x.to(torch.complex128),
+                                  conv.weight.to_tensor().detach().cpu().to(torch.complex128),
+                                  conv.bias.detach().cpu().double(), conv.n_modes, conv.max_n_modes,
+                                  complex_data=True, output_shape=out)
+    assert rel_err(torch.view_as_real(y), torch.view_as_real(ref)) <= TOL
+
+
 def test_complex_data_tucker(cuda_device):
     torch.manual_seed(23)
     conv = na.SpectralConv(4, 4, (8, 8, 8), complex_data=True, factorization="Tucker", rank=0.5,
