@@ -124,6 +124,42 @@ def event_times(fn, iters, stream, flush=None):
     return out
 
 
+def timed_region(step, warmup, steps, stream):
+    """W untimed warm-up steps, then exactly K timed steps bracketed by
+    synchronisations.  Returns (wall ms per step, HIP-event µs per step): the
+    events sit on the launch stream at both ends of the same K back-to-back
+    calls, so both figures describe the same region."""
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    return (t1 - t0) * 1e3 / steps, e0.elapsed_time(e1) * 1e3 / steps
+
+
+N_WARM_EXTRA, N_EVENT_CALLS = 10, 50
+
+
+def per_call_medians(step, stream, dev):
+    """Median µs of single calls timed with HIP events: warm (calls back to
+    back, 10 warm-ups then 50 calls) and cold (a 1 GiB scratch write before
+    each of 50 calls evicts the 256 MB Infinity Cache)."""
+    for _ in range(N_WARM_EXTRA):
+        step()
+    warm = event_times(step, N_EVENT_CALLS, stream)
+    scratch = torch.empty(1 << 28, dtype=torch.float32, device=dev)
+    cold = event_times(step, N_EVENT_CALLS, stream, flush=lambda: scratch.fill_(1.0))
+    del scratch
+    return statistics.median(warm) * 1e3, statistics.median(cold) * 1e3
+
+
 def cpu_baseline(B, C, H, W, nm, total_bytes, budget_s=20.0):
     """The oracle (plain-torch restatement of the reference forward) on the
     host cores, on a bounded sample of the batch."""
@@ -180,9 +216,99 @@ def _oracle_layer(blocks, i):
     return layer
 
 
+C4_TUCKER_RANK = (20, 20, 10, 10, 6)   # what rank=0.1 gives for the (32, 32, 16, 16, 9) weight
+
+
+def torch_rocm_conv1d(x, w, bias, m):
+    """The reference op sequence of a 1D SpectralConv in torch on the GPU:
+    rfft(norm="forward"), first m bins, einsum, zero-padded irfft, bias."""
+    B, _, N = x.shape
+    X = torch.fft.rfft(x, norm="forward")
+    out = torch.zeros(B, w.shape[1], N // 2 + 1, dtype=torch.complex64, device=x.device)
+    out[..., :m] = torch.einsum("bix,iox->box", X[..., :m], w)
+    return torch.fft.irfft(out, n=N, norm="forward") + bias.view(1, -1, 1)
+
+
+def torch_rocm_tucker3d(x, core, factors, bias, ws, m):
+    """The reference's factorized Tucker 3D SpectralConv + 1x1 skip + GELU in
+    torch on the GPU: rfftn, fftshift, centred window, the Tucker chain as
+    pairwise einsums (input factor, core with the mode factors, output
+    factor), ifftshift, ifftn over the first two axes, Hermitian fix-up,
+    irfft, bias."""
+    B, C, D1, D2, D3 = x.shape
+    m1, m2, m3 = m
+    X = torch.fft.fftshift(torch.fft.rfftn(x, norm="forward", dim=(-3, -2, -1)), dim=(-3, -2))
+    r1, r2 = D1 // 2 - m1 // 2, D2 // 2 - m2 // 2
+    Xw = X[:, :, r1:r1 + m1, r2:r2 + m2, :m3]
+    Uin, Uout, U1, U2, U3 = factors
+    K = torch.einsum("ghabc,xa->ghxbc", core, U1)
+    K = torch.einsum("ghxbc,yb->ghxyc", K, U2)
+    K = torch.einsum("ghxyc,zc->ghxyz", K, U3)
+    t = torch.einsum("bixyz,ig->bgxyz", Xw, Uin)
+    t = torch.einsum("bgxyz,ghxyz->bhxyz", t, K)
+    Y = torch.einsum("bhxyz,oh->boxyz", t, Uout)
+    out = torch.zeros(B, Y.shape[1], D1, D2, D3 // 2 + 1, dtype=torch.complex64, device=x.device)
+    out[:, :, r1:r1 + m1, r2:r2 + m2, :m3] = Y
+    out = torch.fft.ifftn(torch.fft.ifftshift(out, dim=(-3, -2)), s=(D1, D2), dim=(-3, -2),
+                          norm="forward")
+    out[..., 0].imag.zero_()
+    out[..., -1].imag.zero_()
+    y = torch.fft.irfft(out, n=D3, dim=-1, norm="forward") + bias.view(1, -1, 1, 1, 1)
+    y = y + F.conv1d(x.reshape(B, C, -1), ws.view(ws.shape[0], C, 1)).view_as(y)
+    return F.gelu(y)
+
+
+def _torch_mlp(m, x):
+    """ChannelMLP (two 1x1 Conv1d with GELU between) in torch."""
+    B, C, *S = x.shape
+    h = x.reshape(B, C, -1)
+    fc0, fc1 = m.fcs
+    h = F.gelu(F.conv1d(h, fc0.weight, fc0.bias))
+    h = F.conv1d(h, fc1.weight, fc1.bias)
+    return h.reshape(B, h.shape[1], *S)
+
+
+def torch_rocm_fno(model, x):
+    """The reference FNO forward (grid embedding, lifting, blocks with
+    spectral conv + linear skip + GELU, channel MLP + soft-gating + GELU, no
+    activations in the last layer, projection) in torch on the GPU, 1x1
+    layers as Conv1d."""
+    B, _, H, W = x.shape
+    gx = torch.linspace(0, 1, H + 1, device=x.device)[:-1]
+    gy = torch.linspace(0, 1, W + 1, device=x.device)[:-1]
+    g0, g1 = torch.meshgrid(gx, gy, indexing="ij")
+    h = torch.cat([x, g0.expand(B, 1, H, W), g1.expand(B, 1, H, W)], dim=1)
+    h = _torch_mlp(model.lifting, h)
+    blk = model.fno_blocks
+    for i in range(blk.n_layers):
+        conv = blk.convs[i]
+        w = conv.weight.to_tensor()
+        m1, m2h = w.shape[2], w.shape[3]
+        Cc = h.shape[1]
+        X = torch.fft.fftshift(torch.fft.rfftn(h.float(), norm="forward", dim=(-2, -1)), dim=(-2,))
+        out = torch.zeros(B, w.shape[1], H, W // 2 + 1, dtype=torch.complex64, device=x.device)
+        r0 = H // 2 - m1 // 2
+        out[:, :, r0:r0 + m1, :m2h] = torch.einsum("bixy,ioxy->boxy", X[:, :, r0:r0 + m1, :m2h], w)
+        out = torch.fft.ifftn(torch.fft.ifftshift(out, dim=(-2,)), s=(H,), dim=(-2,), norm="forward")
+        out[..., 0].imag.zero_()
+        out[..., -1].imag.zero_()
+        spec = torch.fft.irfft(out, n=W, dim=-1, norm="forward") + conv.bias.view(1, -1, 1, 1)
+        sk = F.conv1d(h.reshape(B, Cc, -1), blk.fno_skips[i].conv.weight).view(B, -1, H, W)
+        gate = blk.channel_mlp_skips[i].weight * h
+        last = i == blk.n_layers - 1
+        h = spec + sk
+        if not last:
+            h = F.gelu(h)
+        h = _torch_mlp(blk.channel_mlp[i], h) + gate
+        if not last:
+            h = F.gelu(h)
+    return _torch_mlp(model.projection, h)
+
+
 def module_workload(name, dev):
-    """(step function, algorithmic bytes, dtype, cpu-baseline runner or None)
-    for the workloads timed through the module API."""
+    """The workloads timed through the module API: a dict with the step
+    function, algorithmic bytes, dtype, the CPU-baseline runner, the torch
+    ROCm path of the same computation and extra config entries."""
     import neuraloperator_amd as na
     from neuraloperator_amd import _native as nat
     from neuraloperator_amd.synthetic import gaussian_random_field
@@ -203,11 +329,17 @@ def module_workload(name, dev):
             return lambda: R.spectral_conv_forward(
                 xc, conv.weight.to_tensor().detach().cpu(), conv.bias.detach().cpu(), conv.n_modes,
                 conv.max_n_modes), B, B
-        return (lambda: conv(x)), nbytes, "f32", cpu
+        wt = conv.weight.to_tensor().detach()
+        return dict(step=lambda: conv(x), nbytes=nbytes, dtype="f32", cpu=cpu,
+                    rocm=(lambda: torch_rocm_conv1d(x, wt, conv.bias.detach(), 16),
+                          "torch.fft.rfft + einsum + irfft + bias (rocFFT, rocBLAS), same GPU"),
+                    extra={"batch": B, "channels": C, "N": N, "modes": [16]})
     if name == "c4":
         B, C, S = 8, 32, 64
         conv = na.SpectralConv(C, C, (16, 16, 16), factorization="Tucker", rank=0.1,
                                implementation="factorized").to(dev)
+        if tuple(conv.weight.rank) != C4_TUCKER_RANK:
+            raise RuntimeError(f"Tucker rank {conv.weight.rank} != recorded {C4_TUCKER_RANK}")
         x = gaussian_random_field((B, C, S, S, S), seed=2024, device=dev)
         ws = (torch.randn(C, C) / (C ** 0.5)).to(dev)
         nbytes = 2 * B * C * S ** 3 * 4 + C * C * 4 + C * 4 + sum(
@@ -222,7 +354,16 @@ def module_workload(name, dev):
             return lambda: R.gelu(R.spectral_conv_forward(
                 xs, {"tucker": (core, factors)}, conv.bias.detach().cpu(), conv.n_modes,
                 conv.max_n_modes, implementation="factorized") + R.linear_skip(xs, wsc)), 1, B
-        return (lambda: conv._forward_hip(x, None, nat.SKIP_LINEAR, ws, nat.ACT_GELU)), nbytes, "f32", cpu
+        core = conv.weight.core.detach()
+        factors = [f.detach() for f in conv.weight.factors]
+        return dict(step=lambda: conv._forward_hip(x, None, nat.SKIP_LINEAR, ws, nat.ACT_GELU),
+                    nbytes=nbytes, dtype="f32", cpu=cpu,
+                    rocm=(lambda: torch_rocm_tucker3d(x, core, factors, conv.bias.detach(), ws,
+                                                      (16, 16, 9)),
+                          "torch.fft.rfftn + Tucker einsum chain + ifftn/irfft + conv1d skip + "
+                          "gelu (rocFFT, rocBLAS, MIOpen), same GPU"),
+                    extra={"batch": B, "channels": C, "grid": [S, S, S], "modes": [16, 16, 9],
+                           "tucker_rank": list(C4_TUCKER_RANK)})
     # c3
     B, H = 64, 256
     model = na.FNO((64, 64), in_channels=1, out_channels=1, hidden_channels=64, n_layers=4).to(dev)
@@ -247,41 +388,57 @@ def module_workload(name, dev):
     def step():
         with torch.autocast("cuda", dtype=torch.bfloat16):
             return model(x.float())
-    return step, nbytes, "bf16 1x1-layer operands (autocast), fp32 accumulation and activations", cpu
+
+    def rocm():
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            return torch_rocm_fno(model, x.float())
+    return dict(step=step, nbytes=nbytes,
+                dtype="bf16 1x1-layer operands (autocast), fp32 accumulation and activations",
+                cpu=cpu,
+                rocm=(rocm, "the same FNO forward in torch ops under the same autocast: "
+                            "torch.fft + einsum + Conv1d + gelu (rocFFT, rocBLAS, MIOpen), same GPU"),
+                extra={"batch": B, "grid": [H, H], "hidden": 64, "n_layers": 4, "modes": [64, 33]})
 
 
 def bench_module(args):
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream(dev)
-    step, nbytes, dtype, cpu = module_workload(args.workload, dev)
+    wl = module_workload(args.workload, dev)
+    step, nbytes, dtype, cpu, extra = wl["step"], wl["nbytes"], wl["dtype"], wl["cpu"], wl["extra"]
+    rocm_fn, rocm_what = wl["rocm"] if wl.get("rocm") else (None, None)
     with torch.no_grad():
-        for _ in range(args.warmup):
-            step()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            step()
-        torch.cuda.synchronize()
-        ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
-        warm = event_times(step, max(args.steps, 20), stream)
-    us_warm = statistics.median(warm) * 1e3
+        ms_per_step, us_events = timed_region(step, args.warmup, args.steps, stream)
+        us_warm, us_cold = per_call_medians(step, stream, dev)
     line = {
         "metric": f"µs/call + achieved HBM GB/s, {MODULE_WORKLOADS[args.workload]}",
         "value": round(nbytes / (ms_per_step * 1e-3) / 1e9, 1),
         "unit": "GB/s",
         "us_per_call": round(ms_per_step * 1e3, 1),
         "us_per_call_median_warm": round(us_warm, 1),
+        "us_per_call_median_cold": round(us_cold, 1),
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": dtype,
         "data": "synthetic (seeded Gaussian random field / normal inputs, seeded random-init weights)",
-        "config": {"workload": MODULE_WORKLOADS[args.workload], "algorithmic_bytes": nbytes},
-        "roofline": {"bound": "hbm", "achieved": round(nbytes / (us_warm * 1e-6) / 1e9, 1),
+        "config": {"workload": MODULE_WORKLOADS[args.workload], "algorithmic_bytes": nbytes,
+                   **extra},
+        "roofline": {"bound": "hbm", "achieved": round(nbytes / (us_events * 1e-6) / 1e9, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(nbytes / (us_warm * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": "whole forward, HIP events on the launch stream"},
+                     "frac": round(nbytes / (us_events * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                     "traffic": None, "us_per_call": round(us_events, 1),
+                     "kernel": "whole forward; HIP events on the launch stream around the timed "
+                               "steps, per call"},
     }
+    if rocm_fn is not None and not args.no_torch:
+        with torch.no_grad():
+            for _ in range(2):
+                rocm_fn()
+            tt = event_times(rocm_fn, 5, stream)
+        line["torch_rocm_baseline"] = {
+            "us_per_call": round(statistics.median(tt) * 1e3, 1),
+            "gbs": round(nbytes / (statistics.median(tt) * 1e-3) / 1e9, 1),
+            "what": rocm_what}
     if not args.no_cpu:
         torch.set_num_threads(os.cpu_count() or 1)
         run, done, total = cpu()
@@ -349,25 +506,8 @@ def main():
         if rc:
             raise RuntimeError(nat.last_error())
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    ms_per_step = (t1 - t0) * 1e3 / args.steps
-
-    # per-call event timing over the same calls (warm) and with a 1 GiB scratch
-    # write between calls to evict the 256 MB Infinity Cache (cold)
-    warm = event_times(step, max(args.steps, 20), stream)
-    scratch = torch.empty(1 << 28, dtype=torch.float32, device=dev)
-    cold = event_times(step, max(args.steps, 20), stream, flush=lambda: scratch.fill_(1.0))
-    del scratch
-    us_warm = statistics.median(warm) * 1e3
-    us_cold = statistics.median(cold) * 1e3
-    us_mean = statistics.mean(warm) * 1e3
+    ms_per_step, us_events = timed_region(step, args.warmup, args.steps, stream)
+    us_warm, us_cold = per_call_medians(step, stream, dev)
 
     # device copy bandwidth as a calibration of what HBM delivers
     src = torch.empty(1 << 28, dtype=torch.float32, device=dev)
@@ -388,7 +528,7 @@ def main():
                 "what": "torch.fft (rocFFT) + einsum + irfft + conv + gelu, same GPU"}
 
     value = total_bytes / (ms_per_step * 1e-3) / 1e9
-    achieved_block = total_bytes / (us_mean * 1e-6) / 1e9
+    achieved_block = total_bytes / (us_events * 1e-6) / 1e9
     line = {
         "metric": METRIC if args.workload == "c2" else
                   f"µs/call + achieved HBM GB/s, fused 2D spectral block B{B} C{C} {H}x{W} "
@@ -414,8 +554,9 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved_block, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved_block / HBM_PEAK_GBS, 4),
                      "traffic": profiled_traffic(args.workload),
-                     "kernel": "fno_spectral_block_f32: k_fwd_stream, k_contract_mfma, k_inv_cols, "
-                               "k_row_epilogue_r on one stream, HIP events on that stream"},
+                     "us_per_call": round(us_events, 1),
+                     "kernel": "fno_spectral_block_f32 (all launches of one call) on one stream; "
+                               "HIP events on that stream around the timed steps, per call"},
         "copy_bandwidth_gbs": round(copy_gbs, 1),
         "torch_rocm_baseline": rocm,
     }

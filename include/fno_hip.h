@@ -162,8 +162,10 @@ int fno_block_epilogue_f32(const float* spec, const float* x, const float* skip_
  * :82-119: two 1x1 Conv1d with GELU between), the channel-MLP skip
  * (SoftGating.forward, skip_connections.py:88-93, or identity) and the second
  * activation of FNOBlocks.forward_with_postactivation (fno_block.py:363-379).
- *   x       float32 [B, Ci, P]; y float32 [B, Co, P], may alias x or skip_x;
- *           x, y and skip_x 16-byte aligned
+ *   x       float32 [B, Ci, P]; y float32 [B, Co, P]; x, y and skip_x
+ *           16-byte aligned.  y may be the same buffer as skip_x, or as x
+ *           when Ci == Co; any other overlap of y with x or skip_x returns
+ *           FNO_ERR_INVALID
  *   w1 [Ch, Ci], b1 [Ch] (may be NULL), w2 [Co, Ch], b2 [Co] (may be NULL)
  *   skip_kind FNO_SKIP_NONE, FNO_SKIP_SOFT_GATING (skip_x [B, Co, P] scaled
  *           by skip_weight [Co] plus skip_bias [Co] or NULL) or

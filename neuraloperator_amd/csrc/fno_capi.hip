@@ -55,6 +55,11 @@ static int64_t mode_count(int32_t ndim, const int32_t* modes) {
   return m;
 }
 
+static bool ranges_overlap(const void* a, size_t na, const void* b, size_t nb) {
+  const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+  return pa < pb + nb && pb < pa + na;
+}
+
 static int check_norm(int32_t norm) {
   FNO_CHECK_ARG(norm == FNO_NORM_BACKWARD || norm == FNO_NORM_FORWARD || norm == FNO_NORM_ORTHO,
                 "norm must be FNO_NORM_BACKWARD/FORWARD/ORTHO (got %d)", norm);
@@ -321,6 +326,17 @@ int fno_channel_mlp_f32(const float* x, const float* w1, const float* b1, const 
     set_error("channel MLP: x, skip_x and y must be 16-byte aligned");
     return FNO_ERR_UNSUPPORTED;
   }
+  // In place is safe only element for element: y over x when both have the
+  // same layout (Ci == Co), y over skip_x (always [B, Co, P]).  Any other
+  // overlap lets a workgroup overwrite rows another one has not read yet.
+  const size_t ybytes = (size_t)batch * out_channels * points * sizeof(float);
+  const size_t xbytes = (size_t)batch * in_channels * points * sizeof(float);
+  FNO_CHECK_ARG(!ranges_overlap(x, xbytes, y, ybytes) || (x == y && in_channels == out_channels),
+                "channel MLP: y may alias x only exactly and with in_channels == out_channels "
+                "(%d vs %d)", in_channels, out_channels);
+  FNO_CHECK_ARG(skip_kind == FNO_SKIP_NONE || !ranges_overlap(skip_x, ybytes, y, ybytes) ||
+                    skip_x == y,
+                "channel MLP: y may alias skip_x only exactly");
   return channel_mlp(x, w1, b1, w2, b2, skip_x, skip_weight, skip_bias, y, batch, in_channels,
                      hidden_channels, out_channels, points, skip_kind, act, bf16_products != 0,
                      reinterpret_cast<hipStream_t>(stream));

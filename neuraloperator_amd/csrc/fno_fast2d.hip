@@ -944,19 +944,25 @@ static int epi_rows_per_block(int H) { return H >= 64 ? 16 : H; }
 
 static bool epi_r_supported(int H, int W, int Ci, int Co, int m2h, int skip_kind);
 
-static bool epi_supported(int H, int W, int Ci, int Co, int m1, int m2h, int skip_kind) {
-  if (m1 >= 1 && m1 <= H && epi_r_supported(H, W, Ci, Co, m2h, skip_kind) &&
-      inv_lds_bytes(H, m2h) <= kMaxLds)
-    return true;
-  if (!(W == 128 || W == 256)) return false;
+// K3 has instances for H in {64, 128, 256} only: every epilogue variant needs
+// it, so the fused path covers no other column count.
+static bool inv_supported(int H, int m1, int m2h) {
   if (!(H == 64 || H == 128 || H == 256)) return false;
+  if (m1 < 1 || m1 > H || m2h < 1) return false;
+  return inv_lds_bytes(H, m2h) <= kMaxLds;
+}
+
+static bool epi_supported(int H, int W, int Ci, int Co, int m1, int m2h, int skip_kind) {
+  if (!inv_supported(H, m1, m2h)) return false;
+  if (epi_r_supported(H, W, Ci, Co, m2h, skip_kind)) return true;
+  if (!(W == 128 || W == 256)) return false;
   if (!(Co == 32 || Co == 64)) return false;
   if (skip_kind == FNO_SKIP_LINEAR && !(Ci == 32 || Ci == 64)) return false;
   if ((skip_kind == FNO_SKIP_IDENTITY || skip_kind == FNO_SKIP_SOFT_GATING) && Ci != Co)
     return false;
-  if (m1 < 1 || m1 > H || m2h < 1 || m2h > W / 2 + 1) return false;
+  if (m2h > W / 2 + 1) return false;
   if (2 * m2h > W + 8) return false;  // mirror staging fits the line's LDS rows
-  return epi_lds_bytes(W, Co, Ci, skip_kind) <= kMaxLds && inv_lds_bytes(H, m2h) <= kMaxLds;
+  return epi_lds_bytes(W, Co, Ci, skip_kind) <= kMaxLds;
 }
 
 // The fused path is taken when the epilogue kernel covers the shape; the

@@ -41,7 +41,9 @@ Pinning status (what checks each function; see tests/test_oracle.py):
     bf16-exact operands, where the rounding must change nothing.
   spectral_resample -> band-limited plane waves resampled exactly, and the
     odd-grid residue rule of the reference's slices (-k-1 .. k-1).
-  tucker_rank_from_fraction -> parity unpinned (restates tensorly 0.9.0's
-    rank rule; tensorly is not importable here, and no reference test pins
-    the resulting tuple).
+
+Not in the oracle: the float-rank -> Tucker-rank rule of tensorly 0.9.0.  The
+tests pass explicit rank tuples (the 3D TFNO workload records (20, 20, 10, 10,
+6)), and the product's own restatement of the rule is pinned in
+tests/test_host.py by closed forms of its parameter-count equation.
 """

@@ -192,40 +192,6 @@ def tt_to_tensor(factors):
     return full.squeeze(0).squeeze(-1)
 
 
-def tucker_rank_from_fraction(shape: Sequence[int], rank: float, fixed_modes=None):
-    """Restatement of tensorly 0.9.0 ``validate_tucker_rank`` for a float rank
-    (used by tltorch 0.5.0 TuckerTensor.new).  Parity unpinned: tensorly is
-    not importable here and no reference fixture holds the tuple.
-
-    Solves n_param * x**n_compressed + (sum s_i**2 + fixed) * x = rank * n_param
-    for the fraction x, then rank_i = max(round(s_i * x), 1).
-    """
-    shape = list(shape)
-    n_param = float(math.prod(shape))
-    fixed = []
-    if fixed_modes is not None:
-        fixed = [(m, shape.pop(m)) for m in sorted(fixed_modes, reverse=True)][::-1]
-    n_fixed = float(sum(s * s for _, s in fixed))
-    n_comp = len(shape)
-    sq = float(sum(s * s for s in shape))
-
-    def fun(x):
-        return n_param * x ** n_comp + sq * x + n_fixed * x - rank * n_param
-
-    lo, hi = 0.0, max(rank, 1.0)
-    for _ in range(200):
-        mid = 0.5 * (lo + hi)
-        if fun(lo) * fun(mid) <= 0:
-            hi = mid
-        else:
-            lo = mid
-    frac = 0.5 * (lo + hi)
-    out = [max(int(round(s * frac)), 1) for s in shape]
-    for mode, size in fixed:
-        out.insert(mode, size)
-    return out
-
-
 # ---------------------------------------------------------------------------
 # SpectralConv.forward restated (spectral_convolution.py:417-570)
 # ---------------------------------------------------------------------------
@@ -466,10 +432,13 @@ def complex_apply(fr, fi, x):
 
 
 def fno_block_forward(x, index, n_layers, conv: dict, fno_skip: Optional[dict], mlp: Optional[dict],
-                      mlp_skip: Optional[dict], non_linearity=gelu, output_shape=None):
+                      mlp_skip: Optional[dict], non_linearity=gelu, output_shape=None,
+                      bf16_products=False):
     """FNOBlocks.forward_with_postactivation (fno_block.py:327-381) without
     norms/stabilizer.  ``fno_skip``/``mlp_skip`` are {"type": "linear", "w": ..}
-    or {"type": "soft-gating", "w": .., "b": ..} or {"type": "identity"} or None."""
+    or {"type": "soft-gating", "w": .., "b": ..} or {"type": "identity"} or None.
+    bf16_products: the channel MLP's two 1x1 layers on bf16-rounded operands
+    (``channel_mlp``); everything else at full precision."""
     complex_data = conv.get("complex_data", False)
 
     def apply_skip(s, inp):
@@ -517,7 +486,8 @@ def fno_block_forward(x, index, n_layers, conv: dict, fno_skip: Optional[dict], 
             x = complex_apply(lambda t: channel_mlp(t, mlp["fr"]["weights"], mlp["fr"]["biases"]),
                               lambda t: channel_mlp(t, mlp["fi"]["weights"], mlp["fi"]["biases"]), x)
         else:
-            x = channel_mlp(x, mlp["weights"], mlp["biases"], non_linearity)
+            x = channel_mlp(x, mlp["weights"], mlp["biases"], non_linearity,
+                            bf16_products=bf16_products)
         if x_skip_mlp is not None:
             x = x + x_skip_mlp
     if index < n_layers - 1:
@@ -569,13 +539,17 @@ def domain_unpad(x, pads):
     return x[(Ellipsis,) + tuple(slice(p, -p) if p else slice(None) for p in pads)]
 
 
-def fno_forward(x, params: dict):
+def fno_forward(x, params: dict, bf16_products=False):
     """FNO.forward (fno.py:342-408): grid embedding, lifting, domain padding,
     blocks, unpadding, projection.
 
     ``params`` = {"lifting": {"weights", "biases"}, "projection": {...},
     "layers": [ {conv, fno_skip, mlp, mlp_skip}, ...], "positional_embedding": bool,
     "domain_padding": per-axis fractions or None}
+    bf16_products: the lifting, channel and projection MLPs take bf16-rounded
+    operands (``channel_mlp``), as their Conv1d layers do under
+    torch.autocast(dtype=bfloat16) (training/trainer.py:669-672); the spectral
+    path and the block skips stay at full precision.
     """
     complex_data = params.get("complex_data", False)
 
@@ -583,7 +557,7 @@ def fno_forward(x, params: dict):
         if complex_data:   # ComplexValued lifting / projection (fno.py:327-340)
             return complex_apply(lambda u: channel_mlp(u, p["fr"]["weights"], p["fr"]["biases"]),
                                  lambda u: channel_mlp(u, p["fi"]["weights"], p["fi"]["biases"]), t)
-        return channel_mlp(t, p["weights"], p["biases"])
+        return channel_mlp(t, p["weights"], p["biases"], bf16_products=bf16_products)
 
     if params.get("positional_embedding", True):
         x = grid_embedding_nd(x)
@@ -595,7 +569,8 @@ def fno_forward(x, params: dict):
     for i, layer in enumerate(params["layers"]):
         x = fno_block_forward(x, i, n_layers, layer["conv"], layer.get("fno_skip"),
                               layer.get("mlp"), layer.get("mlp_skip"),
-                              non_linearity=cgelu if complex_data else gelu)
+                              non_linearity=cgelu if complex_data else gelu,
+                              bf16_products=bf16_products)
     if pads is not None:
         x = domain_unpad(x, pads)
     return mlp(params["projection"], x)

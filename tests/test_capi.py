@@ -49,3 +49,35 @@ def test_workspace_and_fused_queries():
     assert ws == (32 * 64 * 64 * 33 * 2 + 32 * 64 * 256 * 33) * 8
     odd = nat.i32_array([9, 10])
     assert lib.fno_spectral_block_is_fused(2, 3, 4, 2, odd, nat.i32_array([4, 3]), 1) == 0
+
+
+def test_fused_path_only_where_inverse_column_kernel_exists():
+    """The fused block needs the inverse column kernel, which has 64-, 128-
+    and 256-row instances; other heights take the generic composition."""
+    lib = nat.load()
+    md = nat.i32_array([16, 9])
+    for H, W in [(32, 128), (48, 128), (48, 256), (512, 256), (1024, 128)]:
+        assert lib.fno_spectral_block_is_fused(2, 64, 64, 2, nat.i32_array([H, W]), md, 1) == 0, H
+    for H, W in [(64, 128), (128, 128), (256, 256)]:
+        assert lib.fno_spectral_block_is_fused(2, 64, 64, 2, nat.i32_array([H, W]), md, 1) == 1, H
+
+
+def test_channel_mlp_rejects_unsafe_aliasing():
+    """y may share storage with x only exactly and with Ci == Co, and with
+    skip_x only exactly; anything else is FNO_ERR_INVALID before any launch."""
+    lib = nat.load()
+    base = 1 << 24
+    vp = ctypes.c_void_p
+    B, P = 2, 256
+
+    def call(x, y, ci, ch, co, skip_x=None, kind=0):
+        return lib.fno_channel_mlp_f32(vp(x), vp(base), None, vp(base), None,
+                                       vp(skip_x) if skip_x else None, None, None, vp(y), B, ci, ch,
+                                       co, P, kind, 0, 0, None)
+    # lifting-like 4 -> 128 -> 64 written over its own input
+    assert call(base, base, 4, 128, 64) == 1 and "alias x" in nat.last_error()
+    # projection-like 64 -> 128 -> 16 written into the middle of its input
+    assert call(base, base + 4096, 64, 128, 16) == 1 and "alias x" in nat.last_error()
+    # square MLP with y overlapping skip_x at an offset
+    assert call(base, base + (1 << 22), 64, 32, 64, skip_x=base + (1 << 22) + 1024,
+                kind=3) == 1 and "skip_x" in nat.last_error()

@@ -383,6 +383,104 @@ def test_fno_c3_shape_bf16_input(cuda_device):
     err = rel_err(y, ref)
     assert err <= 2e-2
     assert err <= TOL
+    # the configuration as the benchmark runs it: under torch.autocast(bf16)
+    # the lifting, channel and projection MLPs take bf16-rounded operands with
+    # fp32 accumulation; against the oracle with the same rounding, and
+    # against the full-precision oracle at the configuration's 2e-2
+    print("fno c3 shape B2 under autocast(bf16)", flush=True)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        ybf = model(x.to(cuda_device).float())
+    torch.cuda.synchronize()
+    assert ybf.dtype == torch.float32
+    ref_bf = R.fno_forward(x.double(), params, bf16_products=True)
+    err_bf = rel_err(ybf, ref_bf)
+    print(f"autocast: vs rounded oracle {err_bf:.2e}, vs fp32 oracle {rel_err(ybf, ref):.2e}",
+          flush=True)
+    assert err_bf <= 2e-2
+    assert rel_err(ybf, ref) <= 2e-2
+    # the rounded oracle is the closer one: the kernels round the operands it rounds
+    assert (ybf.double().cpu() - ref_bf).abs().mean() < (ybf.double().cpu() - ref).abs().mean()
+
+
+def test_c0_workload_full_size(cuda_device):
+    """The 1D workload at its full size through the call the benchmark times
+    (SpectralConv.forward): x[16, 64, 1024] ~ N(0, 1), n_modes 30 -> 16 rfft
+    modes, W[64, 64, 16] with re/im ~ N(0, 1/4096), a nonzero bias."""
+    print("c0 full size x[16,64,1024] 16 modes", flush=True)
+    B, C, N = 16, 64, 1024
+    torch.manual_seed(31)
+    conv = na.SpectralConv(C, C, (30,)).to(cuda_device)
+    g = torch.Generator().manual_seed(32)
+    w = torch.complex(torch.randn(C, C, 16, generator=g), torch.randn(C, C, 16, generator=g)) / 64
+    bias = torch.randn(C, 1, generator=g) / 8
+    with torch.no_grad():
+        conv.weight.tensor.copy_(w.to(cuda_device))
+        conv.bias.copy_(bias.to(cuda_device))
+    x = torch.randn(B, C, N, generator=g)
+    with torch.no_grad():
+        y = conv(x.to(cuda_device))
+    torch.cuda.synchronize()
+    assert list(conv.n_modes) == [16]
+    ref = R.spectral_conv_forward(x.double(), w.to(torch.complex128), bias.double(), conv.n_modes,
+                                  conv.max_n_modes)
+    err = rel_err(y, ref)
+    assert err <= TOL, err
+
+
+C4_TUCKER_RANK = (20, 20, 10, 10, 6)
+
+
+def test_c4_workload_tucker_block(cuda_device):
+    """The 3D TFNO block at its workload shape (64^3 grid, 32 channels,
+    n_modes (16, 16, 16) -> 16x16x9, Tucker rank 0.1 = the recorded tuple
+    (20, 20, 10, 10, 6), factors from the module's init, linear skip + erf
+    GELU) through the exact call the benchmark times, on two samples of its
+    batch, against the float64 oracle contracting with the factors."""
+    print("c4 workload B2 C32 64^3 tucker (20,20,10,10,6) skip+gelu", flush=True)
+    torch.manual_seed(34)
+    B, C, S = 2, 32, 64
+    conv = na.SpectralConv(C, C, (16, 16, 16), factorization="Tucker", rank=0.1,
+                           implementation="factorized").to(cuda_device)
+    assert tuple(conv.weight.rank) == C4_TUCKER_RANK
+    with torch.no_grad():
+        conv.bias.normal_(0, 0.1)
+    x = gaussian_random_field((B, C, S, S, S), seed=35)
+    ws = torch.randn(C, C, generator=torch.Generator().manual_seed(36)) / C ** 0.5
+    with torch.no_grad():
+        y = conv._forward_hip(x.to(cuda_device), None, nat.SKIP_LINEAR, ws.to(cuda_device),
+                              nat.ACT_GELU)
+    torch.cuda.synchronize()
+    core = conv.weight.core.detach().cpu().to(torch.complex128)
+    factors = [f.detach().cpu().to(torch.complex128) for f in conv.weight.factors]
+    ref = R.spectral_conv_forward(x.double(), {"tucker": (core, factors)},
+                                  conv.bias.detach().cpu().double(), conv.n_modes, conv.max_n_modes,
+                                  implementation="factorized")
+    ref = R.gelu(ref + R.linear_skip(x.double(), ws.double()))
+    err = rel_err(y, ref)
+    assert err <= TOL, err
+
+
+@pytest.mark.parametrize("H,W", [(32, 128), (48, 128), (48, 256)])
+def test_block_heights_outside_fused_path(H, W, cuda_device):
+    """Plane heights without a fused inverse-column instance (it has 64, 128
+    and 256 rows) take the generic composition and match the oracle."""
+    print(f"block outside fused heights {H}x{W}", flush=True)
+    B, C = 2, 64
+    conv = _dense_conv(C, C, (16, 16), cuda_device, seed=3)
+    kept, _ = conv.window([H, W])
+    assert not Fh.spectral_block_is_fused(B, C, C, [H, W], kept, nat.SKIP_LINEAR)
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(B, C, H, W, generator=g)
+    ws = torch.randn(C, C, generator=g) / C ** 0.5
+    with torch.no_grad():
+        y = conv._forward_hip(x.to(cuda_device), None, nat.SKIP_LINEAR, ws.to(cuda_device),
+                              nat.ACT_GELU)
+    torch.cuda.synchronize()
+    w = conv.weight.to_tensor().detach().cpu().to(torch.complex128)
+    ref = R.spectral_conv_forward(x.double(), w, conv.bias.detach().cpu().double(), conv.n_modes,
+                                  conv.max_n_modes)
+    ref = R.gelu(ref + R.linear_skip(x.double(), ws.double()))
+    assert rel_err(y, ref) <= TOL
 
 
 @pytest.mark.parametrize("dim,sizes,nm,norm", [

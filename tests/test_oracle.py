@@ -333,12 +333,3 @@ def test_oracle_reproduces_golden(path):
         y = R.gelu(y + R.linear_skip(x, torch.from_numpy(d["skip_w"]).double()))
     exp = d["expected"]
     assert np.abs(y.numpy() - exp).max() <= 1e-6 * np.abs(exp).max()
-
-
-def test_tucker_rank_rule_for_tfno_default():
-    # rank fraction 0.1 of the 3D TFNO weight (32,32,16,16,9): the solved
-    # ranks must reproduce ~10% of the dense parameter count
-    shape = (32, 32, 16, 16, 9)
-    ranks = R.tucker_rank_from_fraction(shape, 0.1)
-    n = math.prod(ranks) + sum(s * r for s, r in zip(shape, ranks))
-    assert abs(n / math.prod(shape) - 0.1) < 0.03
