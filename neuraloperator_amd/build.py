@@ -1,6 +1,7 @@
 """Build libfnohip.so in-tree with hipcc for gfx950.
 
-    python -m neuraloperator_amd.build
+    python -m neuraloperator_amd.build        (everything)
+    python -m neuraloperator_amd.build -i     (only objects older than their sources)
 
 Every HIP source under ``csrc/`` is compiled to an object in parallel and the
 objects are linked into ``neuraloperator_amd/libfnohip.so``.  All device code
@@ -42,13 +43,23 @@ def sources():
     return sorted(CSRC.glob("*.hip"))
 
 
-def build(verbose: bool = False, jobs: int = 8) -> Path:
+def _headers_mtime() -> float:
+    heads = list(CSRC.glob("*.h")) + list((PKG.parent / "include").glob("*.h"))
+    return max((h.stat().st_mtime for h in heads), default=0.0)
+
+
+def build(verbose: bool = False, jobs: int = 8, incremental: bool = False) -> Path:
+    """Compile every source and link the library.  incremental=True keeps an
+    object that is newer than its source and every header."""
     hipcc = _hipcc()
     BUILD.mkdir(exist_ok=True)
     objs = []
+    heads = _headers_mtime()
 
     def compile_one(src: Path) -> Path:
         obj = BUILD / (src.stem + ".o")
+        if incremental and obj.exists() and obj.stat().st_mtime > max(src.stat().st_mtime, heads):
+            return obj
         cmd = [hipcc, *HIPCC_FLAGS, "-I", str(CSRC), "-c", str(src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
@@ -71,5 +82,5 @@ def build(verbose: bool = False, jobs: int = 8) -> Path:
 
 
 if __name__ == "__main__":
-    path = build(verbose="-v" in sys.argv)
+    path = build(verbose="-v" in sys.argv, incremental="-i" in sys.argv)
     print(f"built {path}")
