@@ -210,6 +210,30 @@ int fno_spectral_block_is_fused(int32_t batch, int32_t in_channels, int32_t out_
                                 int32_t ndim, const int32_t* sizes, const int32_t* modes,
                                 int32_t skip_kind);
 
+/*
+ * fno_spectral_block_f32 without a workspace argument and without any device
+ * allocation.  No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, kernels and results as
+ * fno_spectral_block_f32.
+ *   - The scratch is a fixed device array of FNO_NOALLOC_SCRATCH_BYTES owned
+ *     by the library; each GPU that runs this call holds its own copy until
+ *     the process ends.
+ *   - The batch runs in consecutive chunks whose workspace
+ *     (fno_spectral_block_workspace_bytes) fits that array.  A shape whose
+ *     single sample needs more returns FNO_ERR_UNSUPPORTED, nothing enqueued.
+ *   - Calls on one GPU share the array.  Calls that overlap in time on one
+ *     GPU (different streams or host threads) race; the caller serialises
+ *     them.  Every scratch byte the kernels read is written earlier in the
+ *     same call, so nothing needs clearing between calls.
+ */
+#define FNO_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int fno_spectral_block_f32_noalloc(const float* x, const void* w, const float* bias,
+                                   const float* skip_weight, float* y, int32_t batch,
+                                   int32_t in_channels, int32_t out_channels, int32_t ndim,
+                                   const int32_t* sizes, const int32_t* modes, int32_t norm,
+                                   int32_t skip_kind, int32_t act, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

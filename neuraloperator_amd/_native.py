@@ -49,6 +49,9 @@ _SIGNATURES = {
                                                      _c_i32p]),
     "fno_spectral_block_is_fused": (_c_i32, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32p, _c_i32p,
                                              _c_i32]),
+    "fno_spectral_block_f32_noalloc": (_c_i32, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i32, _c_i32,
+                                                _c_i32, _c_i32, _c_i32p, _c_i32p, _c_i32, _c_i32,
+                                                _c_i32, _c_vp]),
     "fno_channel_mlp_f32": (_c_i32, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                                      _c_i64, _c_i32, _c_i32, _c_i32, _c_i64, _c_i32, _c_i32, _c_i32,
                                      _c_vp]),

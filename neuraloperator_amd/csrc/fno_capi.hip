@@ -364,27 +364,31 @@ size_t fno_spectral_block_workspace_bytes(int32_t batch, int32_t in_channels,
   return fused > generic ? fused : generic;
 }
 
-int fno_spectral_block_f32(const float* x, const void* w, const float* bias,
-                           const float* skip_weight, float* y, int32_t batch, int32_t in_channels,
-                           int32_t out_channels, int32_t ndim, const int32_t* sizes,
-                           const int32_t* modes, int32_t norm, int32_t skip_kind, int32_t act,
-                           void* workspace, size_t workspace_bytes, void* stream) {
-  clear_error();
+}  // extern "C"
+
+namespace fno {
+
+int spectral_block_check(const float* x, const void* w, float* y, int32_t batch,
+                         int32_t in_channels, int32_t out_channels, int32_t ndim,
+                         const int32_t* sizes, const int32_t* modes, int32_t norm,
+                         int32_t skip_kind, int32_t act, const float* skip_weight) {
   FNO_CHECK_ARG(x && w && y, "x/w/y must not be NULL");
   FNO_CHECK_ARG(batch >= 1 && in_channels >= 1 && out_channels >= 1, "bad batch/channels");
   int rc = validate_window(ndim, sizes, modes);
   if (rc) return rc;
   rc = check_norm(norm);
   if (rc) return rc;
-  rc = check_skip(skip_kind, act, in_channels, out_channels, skip_weight);
-  if (rc) return rc;
-  const size_t need = fno_spectral_block_workspace_bytes(batch, in_channels, out_channels, ndim,
-                                                         sizes, modes);
-  if (!workspace || workspace_bytes < need) {
-    set_error("spectral block: workspace %zu < %zu bytes", workspace_bytes, need);
-    return FNO_ERR_WORKSPACE;
-  }
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  return check_skip(skip_kind, act, in_channels, out_channels, skip_weight);
+}
+
+// The block on validated arguments and a workspace of at least
+// fno_spectral_block_workspace_bytes(batch, ...) bytes.
+int spectral_block_run(const float* x, const void* w, const float* bias, const float* skip_weight,
+                       float* y, int32_t batch, int32_t in_channels, int32_t out_channels,
+                       int32_t ndim, const int32_t* sizes, const int32_t* modes, int32_t norm,
+                       int32_t skip_kind, int32_t act, void* workspace, size_t workspace_bytes,
+                       hipStream_t st) {
+  int rc;
   if (fast2d_supported(batch, in_channels, out_channels, ndim, sizes, modes, skip_kind))
     return fast2d_block(x, reinterpret_cast<const float2*>(w), bias, skip_weight, y, batch,
                         in_channels, out_channels, sizes, modes, norm, skip_kind, act, workspace,
@@ -410,6 +414,30 @@ int fno_spectral_block_f32(const float* x, const void* w, const float* bias,
   if (skip_kind == FNO_SKIP_NONE && act == FNO_ACT_NONE) return FNO_OK;
   return block_epilogue(y, x, skip_weight, y, batch, in_channels, out_channels, P, skip_kind, act,
                         st);
+}
+
+}  // namespace fno
+
+extern "C" {
+
+int fno_spectral_block_f32(const float* x, const void* w, const float* bias,
+                           const float* skip_weight, float* y, int32_t batch, int32_t in_channels,
+                           int32_t out_channels, int32_t ndim, const int32_t* sizes,
+                           const int32_t* modes, int32_t norm, int32_t skip_kind, int32_t act,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  int rc = spectral_block_check(x, w, y, batch, in_channels, out_channels, ndim, sizes, modes, norm,
+                                skip_kind, act, skip_weight);
+  if (rc) return rc;
+  const size_t need = fno_spectral_block_workspace_bytes(batch, in_channels, out_channels, ndim,
+                                                         sizes, modes);
+  if (!workspace || workspace_bytes < need) {
+    set_error("spectral block: workspace %zu < %zu bytes", workspace_bytes, need);
+    return FNO_ERR_WORKSPACE;
+  }
+  return spectral_block_run(x, w, bias, skip_weight, y, batch, in_channels, out_channels, ndim,
+                            sizes, modes, norm, skip_kind, act, workspace, workspace_bytes,
+                            reinterpret_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

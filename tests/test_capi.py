@@ -81,3 +81,18 @@ def test_channel_mlp_rejects_unsafe_aliasing():
     # square MLP with y overlapping skip_x at an offset
     assert call(base, base + (1 << 22), 64, 32, 64, skip_x=base + (1 << 22) + 1024,
                 kind=3) == 1 and "skip_x" in nat.last_error()
+
+
+def test_noalloc_block_rejects_samples_larger_than_its_scratch():
+    """The no-allocation block runs the batch in chunks of its fixed scratch
+    array; a shape whose single sample needs more is refused before any HIP
+    call (4096^2 planes of 64 channels need ~71 MB per sample)."""
+    lib = nat.load()
+    sz, md = nat.i32_array([4096, 4096]), nat.i32_array([64, 33])
+    one = lib.fno_spectral_block_workspace_bytes(1, 64, 64, 2, sz, md)
+    assert one > 64 << 20
+    v = ctypes.c_void_p(1 << 24)
+    rc = lib.fno_spectral_block_f32_noalloc(v, v, None, v, v, 2, 64, 64, 2, sz, md, 1, 1, 1, None)
+    assert rc == 2 and "scratch" in nat.last_error()
+    rc = lib.fno_spectral_block_f32_noalloc(None, v, None, v, v, 2, 64, 64, 2, sz, md, 1, 1, 1, None)
+    assert rc == 1
