@@ -42,6 +42,7 @@ int channel_mlp(const float* x, const float* w1, const float* b1, const float* w
 bool fast2d_supported(int B, int Ci, int Co, int ndim, const int32_t* sizes, const int32_t* modes,
                       int skip_kind);
 size_t fast2d_workspace(int B, int Ci, int Co, const int32_t* sizes, const int32_t* modes);
+bool rowsynth_covers(int H, int W, int Ci, int Co, int m1, int m2h);
 int fast2d_block(const float* x, const float2* w, const float* bias, const float* skip_w, float* y,
                  int B, int Ci, int Co, const int32_t* sizes, const int32_t* modes, int norm,
                  int skip_kind, int act, void* ws, size_t ws_bytes, hipStream_t st);
@@ -355,6 +356,10 @@ size_t fno_spectral_block_workspace_bytes(int32_t batch, int32_t in_channels,
   if (!sizes || !modes || ndim < 1 || ndim > 4) return 0;
   size_t fused = 0;
   if (ndim == 2) fused = fast2d_workspace(batch, in_channels, out_channels, sizes, modes);
+  // shapes the row-synthesis epilogue covers take the fused path for every skip kind
+  if (ndim == 2 && rowsynth_covers(sizes[0], sizes[1], in_channels, out_channels, modes[0],
+                                   modes[1]))
+    return fused;
   const int64_t M = mode_count(ndim, modes);
   const size_t spectra = (size_t)((int64_t)batch * in_channels * M +
                                   (int64_t)batch * out_channels * M) * sizeof(float2);

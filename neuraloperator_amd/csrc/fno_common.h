@@ -65,6 +65,19 @@ __device__ __forceinline__ float gelu_erf(float v) {
   return v >= 0.f ? v - h : h;
 }
 
+// Activation on/off without a branch: the compiler turns `on ? gelu(v) : v`
+// into a uniform branch around every element's GELU, so the choice is a
+// bit-select (v_bfi_b32) against a mask it cannot see through.
+__device__ __forceinline__ uint32_t act_mask(bool on) {
+  uint32_t m = (uint32_t)__builtin_amdgcn_readfirstlane(on ? -1 : 0);
+  asm volatile("" : "+s"(m));
+  return m;
+}
+__device__ __forceinline__ float act_select(float g, float v, uint32_t m) {
+  return __builtin_bit_cast(float, (__builtin_bit_cast(uint32_t, g) & m) |
+                                       (__builtin_bit_cast(uint32_t, v) & ~m));
+}
+
 // Raw buffer resource over [base, base + bytes): loads past the end return
 // zero, and offsets are 32-bit, so address arithmetic stays in 32-bit VGPRs.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {

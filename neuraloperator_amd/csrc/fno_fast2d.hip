@@ -45,19 +45,6 @@ namespace fno {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-// Activation on/off without a branch: the compiler turns `on ? gelu(v) : v`
-// into a uniform branch around every element's GELU, so the choice is a
-// bit-select (v_bfi_b32) against a mask it cannot see through.
-__device__ __forceinline__ uint32_t act_mask(bool on) {
-  uint32_t m = (uint32_t)__builtin_amdgcn_readfirstlane(on ? -1 : 0);
-  asm volatile("" : "+s"(m));
-  return m;
-}
-__device__ __forceinline__ float act_select(float g, float v, uint32_t m) {
-  return __builtin_bit_cast(float, (__builtin_bit_cast(uint32_t, g) & m) |
-                                       (__builtin_bit_cast(uint32_t, v) & ~m));
-}
-
 // ------------------------------------------------------------------------ K1
 
 // Kept window of a plane: rows kh in [kmin, kmin + m1), kmin = -(m1/2), stored
@@ -885,6 +872,10 @@ k_row_epilogue_r(const float* __restrict__ x, const float2* __restrict__ z,
 }
 
 // ============================================================== host side
+bool rowsynth_covers(int H, int W, int Ci, int Co, int m1, int m2h);
+int rowsynth_epilogue(const float* x, const float2* yhat, const float* skip_w, const float* bias,
+                      float* y, int B, int Ci, int H, int W, int m1, int m2h, int skip_kind,
+                      int act, float s, hipStream_t st);
 int contract_dense(const float2* X, const float2* W, float2* Y, int B, int Ci, int Co, int64_t M,
                    int64_t sWi, int64_t sWo, int64_t sWk, hipStream_t st);
 int rfft_window(const float* x, float2* xhat, int64_t planes, int32_t ndim, const int32_t* sizes,
@@ -972,13 +963,20 @@ bool fast2d_supported(int B, int Ci, int Co, int ndim, const int32_t* sizes, con
                       int skip_kind) {
   if (ndim != 2 || B < 1) return false;
   const int H = sizes[0], W = sizes[1];
+  if (rowsynth_covers(H, W, Ci, Co, modes[0], modes[1])) return true;
   return epi_supported(H, W, Ci, Co, modes[0], modes[1], skip_kind);
+}
+
+// The inverse column transform Z [B][Co][H][m2h] lives in the workspace only
+// when the epilogue reads it; the row-synthesis epilogue builds it on chip.
+static bool uses_z(int Ci, int Co, const int32_t* sizes, const int32_t* modes) {
+  return !rowsynth_covers(sizes[0], sizes[1], Ci, Co, modes[0], modes[1]);
 }
 
 size_t fast2d_workspace(int B, int Ci, int Co, const int32_t* sizes, const int32_t* modes) {
   const int64_t M = (int64_t)modes[0] * modes[1];
-  size_t e = (size_t)((int64_t)B * Ci * M + (int64_t)B * Co * M +
-                      (int64_t)B * sizes[0] * Co * modes[1]) * sizeof(float2);
+  const int64_t zel = uses_z(Ci, Co, sizes, modes) ? (int64_t)B * sizes[0] * Co * modes[1] : 0;
+  size_t e = (size_t)((int64_t)B * Ci * M + (int64_t)B * Co * M + zel) * sizeof(float2);
   if (!fwd_supported(sizes[0], sizes[1], modes[0], modes[1]))
     e += rfft_window_ws((int64_t)B * Ci, 2, sizes, modes);
   return e;
@@ -1188,6 +1186,9 @@ int fast2d_block(const float* x, const float2* w, const float* bias, const float
   if (rc) return rc;
   rc = contract_dense(xhat, w, yhat, B, Ci, Co, M, (int64_t)Co * M, M, 1, st);
   if (rc) return rc;
+  if (!uses_z(Ci, Co, sizes, modes))
+    return rowsynth_epilogue(x, yhat, skip_w, bias, y, B, Ci, H, W, m1, m2h, skip_kind, act,
+                             iscale, st);
   rc = dispatch_inv(H, yhat, zbuf, B, Co, m1, m2h, st);
   if (rc) return rc;
   if (epi_r_supported(H, W, Ci, Co, m2h, skip_kind))

@@ -45,21 +45,30 @@ def test_workspace_and_fused_queries():
     sz, md = nat.i32_array([256, 256]), nat.i32_array([64, 33])
     assert lib.fno_spectral_block_is_fused(32, 64, 64, 2, sz, md, 1) == 1
     ws = lib.fno_spectral_block_workspace_bytes(32, 64, 64, 2, sz, md)
-    # xhat + yhat (B*C*M each) + Z (B*Co*H*m2h), complex64
-    assert ws == (32 * 64 * 64 * 33 * 2 + 32 * 64 * 256 * 33) * 8
+    # xhat + yhat (B*C*M each), complex64: the epilogue synthesises the
+    # inverse column transform on chip
+    assert ws == 32 * 64 * 64 * 33 * 2 * 8
+    # 32 output channels still go through Z (B*Co*H*m2h)
+    ws32 = lib.fno_spectral_block_workspace_bytes(32, 32, 32, 2, sz, md)
+    assert ws32 == (32 * 32 * 64 * 33 * 2 + 32 * 32 * 256 * 33) * 8
     odd = nat.i32_array([9, 10])
     assert lib.fno_spectral_block_is_fused(2, 3, 4, 2, odd, nat.i32_array([4, 3]), 1) == 0
 
 
-def test_fused_path_only_where_inverse_column_kernel_exists():
-    """The fused block needs the inverse column kernel, which has 64-, 128-
-    and 256-row instances; other heights take the generic composition."""
+def test_fused_path_coverage():
+    """64 output channels take the fused path on any height that is a
+    multiple of 8 (the row-synthesis epilogue builds the inverse column
+    transform itself); other channel counts need the inverse column kernel,
+    which has 64-, 128- and 256-row instances, and take the generic
+    composition elsewhere."""
     lib = nat.load()
     md = nat.i32_array([16, 9])
-    for H, W in [(32, 128), (48, 128), (48, 256), (512, 256), (1024, 128)]:
-        assert lib.fno_spectral_block_is_fused(2, 64, 64, 2, nat.i32_array([H, W]), md, 1) == 0, H
-    for H, W in [(64, 128), (128, 128), (256, 256)]:
+    for H, W in [(32, 128), (48, 128), (48, 256), (512, 256), (1024, 128), (256, 256)]:
         assert lib.fno_spectral_block_is_fused(2, 64, 64, 2, nat.i32_array([H, W]), md, 1) == 1, H
+    for H, W in [(32, 128), (48, 128), (48, 256), (512, 256), (1024, 128)]:
+        assert lib.fno_spectral_block_is_fused(2, 32, 32, 2, nat.i32_array([H, W]), md, 1) == 0, H
+    for H, W in [(64, 128), (128, 128), (256, 256)]:
+        assert lib.fno_spectral_block_is_fused(2, 32, 32, 2, nat.i32_array([H, W]), md, 1) == 1, H
 
 
 def test_channel_mlp_rejects_unsafe_aliasing():

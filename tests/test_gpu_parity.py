@@ -140,6 +140,7 @@ def test_headline_block_per_sample_slice(cuda_device):
                                   [64, 33], [64, 33])
     ref = R.gelu(ref + R.linear_skip(x.double(), ws.double()))
     err = rel_err(y, ref)
+    print(f"headline slice max rel err {err:.3e}", flush=True)
     assert err <= TOL, err
 
 
@@ -169,7 +170,10 @@ def test_headline_full_batch_properties(cuda_device):
         f = lambda t: Fh.spectral_block(t, w, None, [64, 33], nat.SKIP_NONE, None, nat.ACT_NONE)
         lhs = f(x + 2.0 * x2)
         rhs = f(x) + 2.0 * f(x2)
-        assert rel_err(lhs, rhs) <= 1e-5
+        # the row products split each operand into two bf16 terms, which
+        # rounds each call separately (~1e-5 of the result): linear to the
+        # parity bar, not bit for bit
+        assert rel_err(lhs, rhs) <= TOL
         del x2, lhs, rhs
     torch.cuda.synchronize()
     xl = x[B - 1:].double().cpu()
@@ -460,15 +464,18 @@ def test_c4_workload_tucker_block(cuda_device):
     assert err <= TOL, err
 
 
-@pytest.mark.parametrize("H,W", [(32, 128), (48, 128), (48, 256)])
-def test_block_heights_outside_fused_path(H, W, cuda_device):
-    """Plane heights without a fused inverse-column instance (it has 64, 128
-    and 256 rows) take the generic composition and match the oracle."""
-    print(f"block outside fused heights {H}x{W}", flush=True)
-    B, C = 2, 64
+@pytest.mark.parametrize("C", [32, 64])
+@pytest.mark.parametrize("H,W", [(32, 128), (48, 128), (48, 256), (512, 256)])
+def test_block_heights_outside_inverse_column_kernel(H, W, C, cuda_device):
+    """Plane heights without an inverse-column-kernel instance (it has 64,
+    128 and 256 rows): 64 output channels stay on the fused path (the row
+    epilogue synthesises the columns itself), 32 take the generic
+    composition; both match the oracle."""
+    print(f"block heights outside the inverse column kernel {H}x{W} C{C}", flush=True)
+    B = 2
     conv = _dense_conv(C, C, (16, 16), cuda_device, seed=3)
     kept, _ = conv.window([H, W])
-    assert not Fh.spectral_block_is_fused(B, C, C, [H, W], kept, nat.SKIP_LINEAR)
+    assert Fh.spectral_block_is_fused(B, C, C, [H, W], kept, nat.SKIP_LINEAR) == (C == 64)
     g = torch.Generator().manual_seed(4)
     x = torch.randn(B, C, H, W, generator=g)
     ws = torch.randn(C, C, generator=g) / C ** 0.5

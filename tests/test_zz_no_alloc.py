@@ -50,9 +50,9 @@ def _run_both(B, C, sizes, modes, seed, dev):
 
 
 @pytest.mark.parametrize("first,second", [
-    # fused 2D path: 12 samples need two chunks of the 64 MiB array, then a
-    # smaller call on another shape
-    ((12, 64, (256, 256), (64, 33)), (3, 32, (64, 128), (16, 9))),
+    # fused 2D path: 32 samples (2.2 MB of window spectra each) need two
+    # chunks of the 64 MiB array, then a smaller call on another shape
+    ((32, 64, (256, 256), (64, 33)), (3, 32, (64, 128), (16, 9))),
     # generic 3D path: 4 samples of 64^3 need two chunks, then a smaller 1D call
     ((4, 32, (64, 64, 64), (16, 16, 9)), (2, 16, (256,), (20,))),
 ])
