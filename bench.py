@@ -59,17 +59,18 @@ def profiled_traffic(workload):
     """HBM bytes per block call measured with rocprofv3 --pmc FETCH_SIZE and
     WRITE_SIZE passes over this script, each scaled by what the counter reads
     for a plain 1 GiB device copy (see the profile's calibration table), summed
-    over the four kernels; None when no such profile is committed."""
+    over the block's kernels; None when no such profile is committed."""
     B, C, H, W, nm = WORKLOADS[workload]
     m1, m2h = nm[0], nm[1] // 2 + 1
-    path = os.path.join(PROFILES, f"fused2d_block_b{B}c{C}_{H}x{W}_m{m1}x{m2h}_traffic.md")
-    try:
-        with open(path) as f:
-            for line in f:
-                if line.startswith("traffic_bytes_per_call:"):
-                    return int(line.split(":", 1)[1].strip().replace(",", ""))
-    except OSError:
-        pass
+    stem = os.path.join(PROFILES, f"fused2d_block_b{B}c{C}_{H}x{W}_m{m1}x{m2h}")
+    for path in (stem + "_traffic.md", stem + ".md"):
+        try:
+            with open(path) as f:
+                for line in f:
+                    if line.startswith("traffic_bytes_per_call:"):
+                        return int(line.split(":", 1)[1].strip().replace(",", ""))
+        except OSError:
+            pass
     return None
 
 
