@@ -161,6 +161,33 @@ def per_call_medians(step, stream, dev):
     return statistics.median(warm) * 1e3, statistics.median(cold) * 1e3
 
 
+def graph_us_per_call(step, stream, calls=20, replays=10):
+    """µs per call of `calls` forward calls captured in one HIP graph and
+    replayed back to back (the same kernels, without the host launch path);
+    None when the step cannot be captured."""
+    try:
+        for _ in range(3):
+            step()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(calls):
+                step()
+        g.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        cur = torch.cuda.current_stream()
+        e0.record(cur)
+        for _ in range(replays):
+            g.replay()
+        e1.record(cur)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (calls * replays)
+    except RuntimeError:
+        return None
+
+
 def cpu_baseline(B, C, H, W, nm, total_bytes, budget_s=20.0):
     """The oracle (plain-torch restatement of the reference forward) on the
     host cores, on a bounded sample of the batch."""
@@ -331,7 +358,7 @@ def module_workload(name, dev):
                 xc, conv.weight.to_tensor().detach().cpu(), conv.bias.detach().cpu(), conv.n_modes,
                 conv.max_n_modes), B, B
         wt = conv.weight.to_tensor().detach()
-        return dict(step=lambda: conv(x), nbytes=nbytes, dtype="f32", cpu=cpu,
+        return dict(step=lambda: conv(x), nbytes=nbytes, dtype="f32", cpu=cpu, graph=True,
                     rocm=(lambda: torch_rocm_conv1d(x, wt, conv.bias.detach(), 16),
                           "torch.fft.rfft + einsum + irfft + bias (rocFFT, rocBLAS), same GPU"),
                     extra={"batch": B, "channels": C, "N": N, "modes": [16]})
@@ -410,6 +437,7 @@ def bench_module(args):
     with torch.no_grad():
         ms_per_step, us_events = timed_region(step, args.warmup, args.steps, stream)
         us_warm, us_cold = per_call_medians(step, stream, dev)
+        us_graph = graph_us_per_call(step, stream) if wl.get("graph") else None
     line = {
         "metric": f"µs/call + achieved HBM GB/s, {MODULE_WORKLOADS[args.workload]}",
         "value": round(nbytes / (ms_per_step * 1e-3) / 1e9, 1),
@@ -417,6 +445,7 @@ def bench_module(args):
         "us_per_call": round(ms_per_step * 1e3, 1),
         "us_per_call_median_warm": round(us_warm, 1),
         "us_per_call_median_cold": round(us_cold, 1),
+        "us_per_call_graph": None if us_graph is None else round(us_graph, 2),
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,

@@ -1261,3 +1261,44 @@ def test_kernel_gelu_matches_exact_erf(cuda_device):
     assert err.max().item() <= 2e-6
     big = ref.abs() >= 0.1
     assert (err[big] / ref.abs()[big]).max().item() <= 1e-5
+
+
+@pytest.mark.parametrize("N,m,Ci,Co", [(1024, 16, 64, 64), (1024, 1, 32, 16), (512, 9, 64, 128),
+                                       (256, 16, 32, 32), (256, 5, 64, 48)])
+@pytest.mark.parametrize("skip", ["linear", "soft-gating", "identity", "none"])
+@pytest.mark.parametrize("norm", ["forward", "backward", "ortho"])
+def test_fused_1d_block(N, m, Ci, Co, skip, norm, cuda_device):
+    """The one-launch 1D block (forward DFT product, contraction and the
+    synthesis product with skip, bias and GELU in one kernel) against the
+    float64 oracle: the SpectralConv forward (first m rfft bins) plus the
+    skip and erf GELU."""
+    if skip in ("soft-gating", "identity") and Ci != Co:
+        pytest.skip("gating/identity skips need Ci == Co")
+    print(f"fused 1d N{N} m{m} Ci{Ci} Co{Co} {skip} {norm}", flush=True)
+    g = torch.Generator().manual_seed(40 + N + m)
+    B = 3
+    x = torch.randn(B, Ci, N, generator=g)
+    w = torch.complex(torch.randn(Ci, Co, m, generator=g), torch.randn(Ci, Co, m, generator=g)) / Ci
+    bias = torch.randn(Co, generator=g) / 4
+    kind = {"linear": nat.SKIP_LINEAR, "soft-gating": nat.SKIP_SOFT_GATING,
+            "identity": nat.SKIP_IDENTITY, "none": nat.SKIP_NONE}[skip]
+    ws = None
+    if skip == "linear":
+        ws = torch.randn(Co, Ci, generator=g) / Ci ** 0.5
+    elif skip == "soft-gating":
+        ws = torch.rand(Co, generator=g) + 0.5
+    d = lambda t: None if t is None else t.to(cuda_device)
+    with torch.no_grad():
+        y = Fh.spectral_block(d(x), d(w), d(bias), [m], kind, d(ws), nat.ACT_GELU, fft_norm=norm)
+    torch.cuda.synchronize()
+    ref = R.spectral_conv_forward(x.double(), w.to(torch.complex128), bias.double().view(-1, 1),
+                                  [m], [m], fft_norm=norm)
+    if skip == "linear":
+        ref = ref + R.linear_skip(x.double(), ws.double())
+    elif skip == "soft-gating":
+        ref = ref + ws.double().view(1, -1, 1) * x.double()
+    elif skip == "identity":
+        ref = ref + x.double()
+    ref = R.gelu(ref)
+    err = rel_err(y, ref)
+    assert err <= TOL, err
