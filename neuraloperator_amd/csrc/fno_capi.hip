@@ -91,7 +91,8 @@ const char* fno_last_error(void) { return last_error_cstr(); }
 
 size_t fno_rfft_window_workspace_bytes(int64_t planes, int32_t ndim, const int32_t* sizes,
                                        const int32_t* modes) {
-  if (!sizes || !modes || ndim < 1 || ndim > 4) return 0;
+  if (validate_window(ndim, sizes, modes) != FNO_OK || bounded_elems(planes, ndim, sizes) < 0)
+    return 0;
   return rfft_window_ws(planes, ndim, sizes, modes);
 }
 
@@ -103,6 +104,8 @@ int fno_rfft_window_f32(const float* x, void* xhat, int64_t planes, int32_t ndim
   FNO_CHECK_ARG(planes >= 1, "planes must be positive");
   int rc = validate_window(ndim, sizes, modes);
   if (rc) return rc;
+  FNO_CHECK_ARG(bounded_elems(planes, ndim, sizes) > 0, "planes x sizes exceeds %lld elements",
+                (long long)kMaxElems);
   rc = check_norm(norm);
   if (rc) return rc;
   return rfft_window(x, reinterpret_cast<float2*>(xhat), planes, ndim, sizes, modes, norm, workspace,
@@ -116,6 +119,9 @@ int fno_contract_dense_c64(const void* xhat, const void* w, void* yhat, int32_t 
   FNO_CHECK_ARG(xhat && w && yhat, "xhat/w/yhat must not be NULL");
   FNO_CHECK_ARG(batch >= 1 && in_channels >= 1 && out_channels >= 1 && n_modes >= 1,
                 "batch/channels/modes must be positive");
+  FNO_CHECK_ARG(extent_ok({batch, in_channels > out_channels ? in_channels : out_channels, n_modes}) &&
+                    extent_ok({in_channels, out_channels, n_modes}),
+                "contraction operands exceed %lld elements", (long long)kMaxElems);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const float2* X = reinterpret_cast<const float2*>(xhat);
   const float2* W = reinterpret_cast<const float2*>(w);
@@ -130,7 +136,12 @@ int fno_contract_dense_c64(const void* xhat, const void* w, void* yhat, int32_t 
 
 size_t fno_contract_tucker_workspace_bytes(int32_t batch, int32_t ndim, const int32_t* modes,
                                            const int32_t* ranks) {
-  if (!modes || !ranks || ndim < 1 || ndim > 4) return 0;
+  if (!modes || !ranks || ndim < 1 || ndim > 4 || batch < 1) return 0;
+  for (int d = 0; d < ndim + 2; ++d)
+    if (ranks[d] < 1) return 0;
+  if (bounded_elems((int64_t)batch * (ranks[0] > ranks[1] ? ranks[0] : ranks[1]), ndim, modes) < 0 ||
+      bounded_elems((int64_t)ranks[0] * ranks[1], ndim, modes, ranks + 2) < 0)
+    return 0;
   const int64_t M = mode_count(ndim, modes);
   int64_t big = (int64_t)ranks[0] * ranks[1];
   for (int d = 0; d < ndim; ++d) big *= (modes[d] > ranks[2 + d] ? modes[d] : ranks[2 + d]);
@@ -151,6 +162,11 @@ int fno_contract_tucker_c64(const void* xhat, const void* core, const void* cons
     FNO_CHECK_ARG(ranks[d] >= 1, "rank %d must be positive", d);
   }
   FNO_CHECK_ARG(batch >= 1 && in_channels >= 1 && out_channels >= 1, "bad batch/channels");
+  for (int d = 0; d < ndim; ++d) FNO_CHECK_ARG(modes[d] >= 1, "modes[%d] must be positive", d);
+  FNO_CHECK_ARG(bounded_elems((int64_t)batch * (in_channels > out_channels ? in_channels : out_channels),
+                              ndim, modes) > 0 &&
+                    fno_contract_tucker_workspace_bytes(batch, ndim, modes, ranks) > 0,
+                "tucker contraction operands exceed %lld elements", (long long)kMaxElems);
   const size_t need = fno_contract_tucker_workspace_bytes(batch, ndim, modes, ranks);
   if (workspace_bytes < need || !workspace) {
     set_error("tucker contraction: workspace %zu < %zu bytes", workspace_bytes, need);
@@ -196,6 +212,9 @@ int fno_contract_tucker_c64(const void* xhat, const void* core, const void* cons
 size_t fno_irfft_window_workspace_bytes(int64_t planes, int32_t ndim, const int32_t* out_sizes,
                                         const int32_t* modes) {
   if (!out_sizes || !modes || ndim < 1 || ndim > 4) return 0;
+  for (int d = 0; d < ndim; ++d)
+    if (out_sizes[d] < 1 || out_sizes[d] > 4096 || modes[d] < 1) return 0;
+  if (bounded_elems(planes, ndim, out_sizes, modes) < 0) return 0;
   return irfft_window_ws(planes, ndim, out_sizes, modes);
 }
 
@@ -214,6 +233,9 @@ int fno_irfft_window_f32(const void* yhat, const float* bias, float* y, int64_t 
     FNO_CHECK_ARG(out_sizes[d] >= 1 && out_sizes[d] <= 4096, "out size %d outside [1, 4096]",
                   out_sizes[d]);
   }
+  FNO_CHECK_ARG(extent_ok({batch, channels}) &&
+                    bounded_elems(batch * channels, ndim, out_sizes, in_sizes) > 0,
+                "batch x channels x sizes exceeds %lld elements", (long long)kMaxElems);
   rc = check_norm(norm);
   if (rc) return rc;
   return irfft_window(reinterpret_cast<const float2*>(yhat), bias, y, batch, channels, ndim,
@@ -235,7 +257,9 @@ static int validate_complex_window(int32_t ndim, const int32_t* sizes, const int
 
 size_t fno_fft_window_workspace_bytes(int64_t planes, int32_t ndim, const int32_t* sizes,
                                       const int32_t* modes) {
-  if (!sizes || !modes || ndim < 1 || ndim > 4) return 0;
+  if (validate_complex_window(ndim, sizes, modes) != FNO_OK ||
+      bounded_elems(planes, ndim, sizes) < 0)
+    return 0;
   return fft_window_c2c_ws(planes, ndim, sizes, modes);
 }
 
@@ -247,6 +271,8 @@ int fno_fft_window_c64(const void* x, void* xhat, int64_t planes, int32_t ndim,
   FNO_CHECK_ARG(planes >= 1, "planes must be positive");
   int rc = validate_complex_window(ndim, sizes, modes);
   if (rc) return rc;
+  FNO_CHECK_ARG(bounded_elems(planes, ndim, sizes) > 0, "planes x sizes exceeds %lld elements",
+                (long long)kMaxElems);
   rc = check_norm(norm);
   if (rc) return rc;
   return fft_window_c2c(reinterpret_cast<const float2*>(x), reinterpret_cast<float2*>(xhat), planes,
@@ -257,6 +283,9 @@ int fno_fft_window_c64(const void* x, void* xhat, int64_t planes, int32_t ndim,
 size_t fno_ifft_window_workspace_bytes(int64_t planes, int32_t ndim, const int32_t* out_sizes,
                                        const int32_t* modes) {
   if (!out_sizes || !modes || ndim < 1 || ndim > 4) return 0;
+  for (int d = 0; d < ndim; ++d)
+    if (out_sizes[d] < 1 || out_sizes[d] > 4096 || modes[d] < 1) return 0;
+  if (bounded_elems(planes, ndim, out_sizes, modes) < 0) return 0;
   return ifft_window_c2c_ws(planes, ndim, out_sizes, modes);
 }
 
@@ -274,6 +303,9 @@ int fno_ifft_window_c64(const void* yhat, const float* bias, void* y, int64_t ba
     FNO_CHECK_ARG(out_sizes[d] >= 1 && out_sizes[d] <= 4096, "out size %d outside [1, 4096]",
                   out_sizes[d]);
   }
+  FNO_CHECK_ARG(extent_ok({batch, channels}) &&
+                    bounded_elems(batch * channels, ndim, out_sizes, in_sizes) > 0,
+                "batch x channels x sizes exceeds %lld elements", (long long)kMaxElems);
   rc = check_norm(norm);
   if (rc) return rc;
   return ifft_window_c2c(reinterpret_cast<const float2*>(yhat), bias, reinterpret_cast<float2*>(y),
@@ -289,6 +321,8 @@ int fno_block_epilogue_f32(const float* spec, const float* x, const float* skip_
   FNO_CHECK_ARG(skip_kind == FNO_SKIP_NONE || x, "x must not be NULL with a skip");
   FNO_CHECK_ARG(batch >= 1 && in_channels >= 1 && out_channels >= 1 && points >= 1,
                 "bad batch/channels/points");
+  FNO_CHECK_ARG(extent_ok({batch, in_channels > out_channels ? in_channels : out_channels, points}),
+                "batch x channels x points exceeds %lld elements", (long long)kMaxElems);
   int rc = check_skip(skip_kind, act, in_channels, out_channels, skip_weight);
   if (rc) return rc;
   return block_epilogue(spec, x, skip_weight, y, batch, in_channels, out_channels, points,
@@ -312,6 +346,8 @@ int fno_channel_mlp_f32(const float* x, const float* w1, const float* b1, const 
   FNO_CHECK_ARG(batch >= 1 && in_channels >= 1 && hidden_channels >= 1 && out_channels >= 1 &&
                     points >= 1,
                 "bad batch/channels/points");
+  FNO_CHECK_ARG(extent_ok({batch, in_channels > out_channels ? in_channels : out_channels, points}),
+                "batch x channels x points exceeds %lld elements", (long long)kMaxElems);
   FNO_CHECK_ARG(skip_kind == FNO_SKIP_NONE || skip_kind == FNO_SKIP_SOFT_GATING ||
                     skip_kind == FNO_SKIP_IDENTITY,
                 "channel MLP skip must be none, soft-gating or identity (got %d)", skip_kind);
@@ -357,7 +393,11 @@ int fno_spectral_block_is_fused(int32_t batch, int32_t in_channels, int32_t out_
 size_t fno_spectral_block_workspace_bytes(int32_t batch, int32_t in_channels,
                                           int32_t out_channels, int32_t ndim,
                                           const int32_t* sizes, const int32_t* modes) {
-  if (!sizes || !modes || ndim < 1 || ndim > 4) return 0;
+  if (batch < 1 || in_channels < 1 || out_channels < 1 ||
+      validate_window(ndim, sizes, modes) != FNO_OK ||
+      bounded_elems((int64_t)batch * (in_channels > out_channels ? in_channels : out_channels), ndim,
+                    sizes) < 0)
+    return 0;
   size_t fused = 0;
   if (ndim == 2) fused = fast2d_workspace(batch, in_channels, out_channels, sizes, modes);
   // shapes the row-synthesis epilogue covers take the fused path for every skip kind
@@ -385,6 +425,13 @@ int spectral_block_check(const float* x, const void* w, float* y, int32_t batch,
   FNO_CHECK_ARG(batch >= 1 && in_channels >= 1 && out_channels >= 1, "bad batch/channels");
   int rc = validate_window(ndim, sizes, modes);
   if (rc) return rc;
+  const int64_t cmax = in_channels > out_channels ? in_channels : out_channels;
+  const int64_t elems = bounded_elems((int64_t)batch * cmax, ndim, sizes);
+  FNO_CHECK_ARG(elems > 0, "batch x channels x sizes exceeds %lld elements", (long long)kMaxElems);
+  const int64_t points = elems / ((int64_t)batch * cmax);
+  FNO_CHECK_ARG(!ranges_overlap(x, (size_t)batch * in_channels * points * sizeof(float), y,
+                                (size_t)batch * out_channels * points * sizeof(float)),
+                "spectral block: y must not overlap x");
   rc = check_norm(norm);
   if (rc) return rc;
   return check_skip(skip_kind, act, in_channels, out_channels, skip_weight);

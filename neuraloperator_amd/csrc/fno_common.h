@@ -3,6 +3,7 @@
 // the same memory layout as torch.complex64.
 #pragma once
 
+#include <initializer_list>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stddef.h>
@@ -93,6 +94,32 @@ int launch_status(const char* what);
 // FFT scaling for a transform direction given torch's norm= convention.
 double forward_scale(int norm, const int32_t* in_sizes, int ndim);
 double inverse_scale(int norm, const int32_t* out_sizes, int ndim);
+
+// Largest element count of any operand or intermediate the entry points
+// accept (2^40: 8 TiB of complex64, beyond any device), so that every byte
+// and offset computed from a validated shape fits int64 and size_t.
+constexpr int64_t kMaxElems = (int64_t)1 << 40;
+
+// True when every factor is positive and their product stays within
+// kMaxElems.
+inline bool extent_ok(std::initializer_list<int64_t> factors) {
+  int64_t e = 1;
+  for (int64_t v : factors)
+    if (v < 1 || __builtin_mul_overflow(e, v, &e) || e > kMaxElems) return false;
+  return true;
+}
+
+// planes * prod(max(a[d], b[d])) for d < n (b may be NULL), or -1 when a
+// factor is not positive or the product passes kMaxElems.
+inline int64_t bounded_elems(int64_t planes, int n, const int32_t* a, const int32_t* b = nullptr) {
+  if (planes < 1 || planes > kMaxElems) return -1;
+  int64_t e = planes;
+  for (int d = 0; d < n; ++d) {
+    const int64_t f = b && b[d] > a[d] ? b[d] : a[d];
+    if (f < 1 || __builtin_mul_overflow(e, f, &e) || e > kMaxElems) return -1;
+  }
+  return e;
+}
 
 }  // namespace fno
 

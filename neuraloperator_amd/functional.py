@@ -24,7 +24,14 @@ def _require_gpu(*tensors):
 
 
 def _ptr(t: Optional[torch.Tensor]):
-    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+    """Device address of a tensor's data for the C-ABI.  The kernels read the
+    storage as it is, so a lazily conjugated or negated view (torch's conj /
+    neg bits, which leave the storage untouched) must have been resolved."""
+    if t is None:
+        return ctypes.c_void_p(0)
+    if t.is_conj() or t.is_neg():
+        raise RuntimeError("internal: a conjugate / negative view reached the C-ABI unresolved")
+    return ctypes.c_void_p(t.data_ptr())
 
 
 def _stream(device):
@@ -36,11 +43,15 @@ def _workspace(nbytes: int, device):
 
 
 def _f32(t):
-    return t.contiguous() if t.dtype == torch.float32 else t.float().contiguous()
+    t = t if t.dtype == torch.float32 else t.float()
+    return t.resolve_neg().contiguous()
 
 
 def _c64(t):
-    return t.contiguous() if t.dtype == torch.complex64 else t.to(torch.complex64).contiguous()
+    # resolve_conj: w.conj() is a view with the conjugate bit set over the
+    # same storage, and .contiguous() keeps it so when the view is contiguous
+    t = t if t.dtype == torch.complex64 else t.to(torch.complex64)
+    return t.resolve_conj().resolve_neg().contiguous()
 
 
 def rfft_window(x: torch.Tensor, modes: Sequence[int], fft_norm: str = "forward") -> torch.Tensor:

@@ -17,10 +17,10 @@ complex_data=True runs fno_fft_window_c64 -> contraction -> fno_ifft_window_c64.
 
 Autograd: when gradients are required (training), the forward runs as
 _SpectralConvFn, whose backward is built from the same library calls (window
-transforms under the dual norm and the dense contraction) for output size ==
-input size and non-separable weights; a factorized weight gets its gradient
-through the torch reconstruction of its dense window.  Other configurations
-raise on backward.
+transforms under the dual norm and the mode-wise contraction), for dense and
+separable weights and for outputs on the input grid or resized; a factorized
+weight gets its gradient through the torch reconstruction of its dense
+window; complex_data=True likewise.
 """
 from __future__ import annotations
 
@@ -77,8 +77,10 @@ def get_contract_fun(weight, implementation="reconstructed", separable=False):
 
 
 class _NoGradThroughHip(torch.autograd.Function):
-    """Attaches a HIP forward result to the graph with a backward that
-    raises: for the cases the gradient functions do not cover."""
+    """Attaches the result of a forward-only fused kernel (spectral block with
+    skip / activation, fused channel MLP) to the graph with a backward that
+    raises.  The modules take those kernels only when no gradient is needed;
+    with gradients they run their autograd paths."""
 
     @staticmethod
     def forward(ctx, y, *inputs):
@@ -87,8 +89,8 @@ class _NoGradThroughHip(torch.autograd.Function):
     @staticmethod
     def backward(ctx, *grads):
         raise NotImplementedError(
-            "gradients of the HIP spectral path cover output size == input size and "
-            "non-separable weights")
+            "this fused forward kernel has no backward; call the module with gradients "
+            "enabled so that it takes its autograd path")
 
 
 _DUAL_NORM = {"forward": "backward", "backward": "forward", "ortho": "ortho"}
@@ -104,28 +106,112 @@ def _hermitian_weights(m_last: int, n_last: int, ndim: int, device) -> torch.Ten
     return c.view(*([1] * (ndim + 1)), m_last)
 
 
+def _landing_index(kept: List[int], in_sizes: List[int], out_sizes: List[int], device):
+    """Where each kept window mode lands in the output grid's rfft layout.
+
+    The reference's inverse (spectral_convolution.py:531-564) places the
+    window in the input grid's spectrum (non-last axes centred, frequency
+    q - m//2 at window position q; last axis bins 0..m-1), ifftshifts, and
+    lets ifftn(s=out) / irfft(n=out) trim or zero-pad every axis at its end:
+    a mode at standard index i of axis d survives when i < N'_d (last axis:
+    i < N'_last//2 + 1) and then meets the output basis e^{2 pi i i n / N'_d}.
+    Returns, per axis, the position of that index in the output grid's full
+    window (non-last axes in the same centred order) and a mask of the modes
+    that survive."""
+    nd = len(kept)
+    pos, mask = [], []
+    for d in range(nd):
+        q = torch.arange(kept[d], device=device)
+        if d < nd - 1:
+            i = (q - kept[d] // 2) % in_sizes[d]
+            ok = i < out_sizes[d]
+            p = (i + out_sizes[d] // 2) % out_sizes[d]
+        else:
+            ok = q < out_sizes[d] // 2 + 1
+            p = torch.where(ok, q, torch.zeros_like(q))
+        pos.append(torch.where(ok, p, torch.zeros_like(p)))
+        mask.append(ok)
+    return pos, mask
+
+
+def _inverse_adjoint(gy: torch.Tensor, kept: List[int], in_sizes: List[int],
+                     out_sizes: List[int], dual: str, enforce: bool = True) -> torch.Tensor:
+    """Adjoint of the window inverse (window spectrum [B, C, *kept] ->
+    real field [B, C, *out_sizes]): the output grid's forward transform of gy
+    under the dual norm (so it carries the inverse's scaling), read at the
+    output index of every surviving mode, times the output grid's Hermitian
+    weight of its last-axis bin; modes that do not survive get zero.
+
+    With enforce_hermitian_symmetry and an even output length the reference
+    zeroes the imaginary part of the input grid's last rfft bin N//2 after
+    the non-last inverse transforms (spectral_convolution.py:555-556).  On a
+    resized grid that bin is not the output Nyquist bin, so the output sees
+    only the real part of that column: its adjoint keeps the Hermitian-even
+    part over the non-last output frequencies, (G[j] + conj(G[-j])) / 2 (the
+    real part in 1D).  On the input grid it is the Nyquist bin, whose
+    imaginary part the real inverse ignores anyway."""
+    nd = len(kept)
+    if list(out_sizes) == list(in_sizes):
+        c = _hermitian_weights(kept[-1], out_sizes[-1], nd, gy.device)
+        return Fh.rfft_window(gy, kept, dual) * c
+    full = list(out_sizes[:-1]) + [out_sizes[-1] // 2 + 1]
+    G = Fh.rfft_window(gy, full, dual)                      # [B, C, *full]
+    bz = in_sizes[-1] // 2
+    if enforce and out_sizes[-1] % 2 == 0 and bz < kept[-1] and bz < full[-1]:
+        col = G[..., bz]
+        neg = []
+        for d in range(nd - 1):
+            n = out_sizes[d]
+            p = torch.arange(n, device=gy.device)
+            j = (p - n // 2) % n                             # standard index at position p
+            neg.append(((-j) % n + n // 2) % n)              # position of -j
+        flipped = col[(slice(None), slice(None)) + tuple(torch.meshgrid(*neg, indexing="ij"))] \
+            if nd > 1 else col
+        G = G.clone()
+        G[..., bz] = 0.5 * (col + flipped.conj())
+    pos, mask = _landing_index(kept, in_sizes, out_sizes, gy.device)
+    idx = torch.meshgrid(*pos, indexing="ij")
+    ok = torch.ones((), dtype=torch.bool, device=gy.device)
+    for d, m in enumerate(mask):
+        ok = ok & m.view(*([1] * d), -1, *([1] * (nd - d - 1)))
+    gY = G[(slice(None), slice(None)) + tuple(idx)]
+    c = _hermitian_weights(kept[-1], out_sizes[-1], nd, gy.device)
+    return torch.where(ok, gY * c, torch.zeros((), dtype=gY.dtype, device=gy.device))
+
+
 class _SpectralConvFn(torch.autograd.Function):
-    """Dense spectral convolution y = s_i I(W . s_f F(x)) + bias with the
-    gradients of SpectralConv.forward (spectral_convolution.py:417-570), for
-    output size == input size.  With F the window of the forward transform
-    (bins e^{-i phi_k(n)}) and I the real inverse (y = sum_k c_k Re(Y_k
-    e^{i phi_k(n)}), c_k = 2 for bins that stand for a conjugate pair):
+    """Spectral convolution y = s_i I(W . s_f F(x)) + bias with the gradients
+    of SpectralConv.forward (spectral_convolution.py:417-570), dense or
+    separable (_contract_dense / _contract_dense_separable, :25-52), output on
+    the input grid or resized (output_shape / resolution_scaling_factor,
+    :524-528).  With F the window of the forward transform (bins e^{-i
+    phi_k(n)}) and I the real inverse onto the output grid (y = sum_k c'_k
+    Re(Y_k e^{i phi'_k(n')}), c' = 2 for bins that stand for a conjugate pair
+    of the output grid, modes the output grid trims away dropped):
 
-        gY = s_i c_k . F_unscaled(gy)      gX = gY . conj(W)^T
-        gW = conj(X)^T . gY               gx = s_f Re(sum_k gX_k e^{i phi_k})
-                                              = s_f I_unscaled(gX / c_k)
+        gY = I^H gy  (_inverse_adjoint)      gX = gY . conj(W)^T   (gY * conj(W))
+        gW = conj(X)^T . gY  (sum_b conj(X) gY)
+        gx = s_f Re(sum_k gX_k e^{i phi_k}) = s_f I_unscaled(gX / c_k)
 
-    so both transforms are the library's own window transforms under the dual
-    norm (forward <-> backward scaling), and both contractions its dense
-    mode-wise contraction."""
+    (separable forms in brackets), so both transforms are the library's own
+    window transforms under the dual norm (forward <-> backward scaling) and
+    the dense contractions its mode-wise contraction; the separable weight
+    gradient is a batch sum of window-sized products."""
 
     @staticmethod
-    def forward(ctx, x, w, bias, kept, fft_norm):
+    def forward(ctx, x, w, bias, kept, fft_norm, out_sizes=None, separable=False, enforce=True):
         sizes = list(x.shape[2:])
+        out_sizes = sizes if out_sizes is None else list(out_sizes)
         b = bias.reshape(-1) if bias is not None else None
-        y = Fh.spectral_block(x, w, b, kept, nat.SKIP_NONE, None, nat.ACT_NONE, fft_norm)
+        if out_sizes == sizes and not separable:
+            y = Fh.spectral_block(x, w, b, kept, nat.SKIP_NONE, None, nat.ACT_NONE, fft_norm)
+        else:
+            xhat = Fh.rfft_window(x, kept, fft_norm)
+            yhat = Fh.contract_dense(xhat, w, separable=separable)
+            y = Fh.irfft_window(yhat, sizes, out_sizes, b, fft_norm, enforce)
         ctx.save_for_backward(x, w)
-        ctx.kept, ctx.fft_norm, ctx.sizes = list(kept), fft_norm, sizes
+        ctx.kept, ctx.fft_norm, ctx.sizes, ctx.out_sizes = list(kept), fft_norm, sizes, out_sizes
+        ctx.separable, ctx.enforce = bool(separable), bool(enforce)
         ctx.bias_shape = None if bias is None else bias.shape
         return y
 
@@ -135,21 +221,27 @@ class _SpectralConvFn(torch.autograd.Function):
         kept, norm, sizes = ctx.kept, ctx.fft_norm, ctx.sizes
         gy = gy.contiguous().float()
         dual = _DUAL_NORM[norm]
-        c = _hermitian_weights(kept[-1], sizes[-1], len(sizes), gy.device)
-        gY = Fh.rfft_window(gy, kept, dual) * c
+        gY = _inverse_adjoint(gy, kept, sizes, ctx.out_sizes, dual, ctx.enforce)
         gx = gw = gb = None
         if ctx.needs_input_grad[0]:
-            wt = w.conj().transpose(0, 1).contiguous()              # [Co, Ci, *m]
-            gX = Fh.contract_dense(gY, wt)                          # [B, Ci, *m]
+            if ctx.separable:
+                gX = Fh.contract_dense(gY.contiguous(), w.conj().contiguous(), separable=True)
+            else:
+                wt = w.conj().transpose(0, 1).contiguous()          # [Co, Ci, *m]
+                gX = Fh.contract_dense(gY.contiguous(), wt)         # [B, Ci, *m]
+            c = _hermitian_weights(kept[-1], sizes[-1], len(sizes), gy.device)
             gx = Fh.irfft_window(gX / c, sizes, sizes, None, dual, False)
         if ctx.needs_input_grad[1]:
             X = Fh.rfft_window(x, kept, norm)                       # [B, Ci, *m]
-            xt = X.conj().transpose(0, 1).contiguous()              # [Ci, B, *m]
-            gw = Fh.contract_dense(xt, gY.contiguous())             # [Ci, Co, *m]
+            if ctx.separable:
+                gw = (X.conj() * gY).sum(dim=0)                     # [C, *m]
+            else:
+                xt = X.conj().transpose(0, 1).contiguous()          # [Ci, B, *m]
+                gw = Fh.contract_dense(xt, gY.contiguous())         # [Ci, Co, *m]
         if ctx.bias_shape is not None and ctx.needs_input_grad[2]:
             dims = [0] + list(range(2, gy.ndim))
             gb = gy.sum(dim=dims).reshape(ctx.bias_shape)
-        return gx, gw, gb, None, None
+        return gx, gw, gb, None, None, None, None, None
 
 
 def _last_axis_phase(n: int, ndim: int, device) -> torch.Tensor:
@@ -163,25 +255,58 @@ def _last_axis_phase(n: int, ndim: int, device) -> torch.Tensor:
     return torch.polar(torch.ones_like(t), -2.0 * math.pi * (n // 2) * t / n).to(torch.complex64)
 
 
+def _complex_inverse_adjoint(gy: torch.Tensor, kept: List[int], in_sizes: List[int],
+                             out_sizes: List[int], dual: str) -> torch.Tensor:
+    """Adjoint of the complex-data window inverse onto a resized grid
+    (spectral_convolution.py:531-538: ifftshift of the non-last axes when
+    there are several, then ifftn(s=out), which trims or zero-pads each axis
+    at its end).  On a non-last axis the window's position q sits at shifted
+    position N//2 - m//2 + q, i.e. at standard index i = (q - m//2) mod N; on
+    the last axis (sliced [:m] and never shifted back) at i = q.  A mode
+    survives when i < N'_d and meets the output basis e^{2 pi i i n / N'_d}.
+    The adjoint reads the output grid's full forward window of gy under the
+    dual norm (every axis centred when there are several, none in 1D) at
+    those indices; modes that do not survive get zero."""
+    nd = len(kept)
+    G = Fh.fft_window(gy, list(out_sizes), dual)            # [B, C, *out_sizes]
+    pos, oks = [], []
+    for d in range(nd):
+        n, n2, m = in_sizes[d], out_sizes[d], kept[d]
+        q = torch.arange(m, device=gy.device)
+        i = (q - m // 2) % n if d < nd - 1 else q
+        p = (i + n2 // 2) % n2 if nd > 1 else i
+        ok = i < n2
+        pos.append(torch.where(ok, p, torch.zeros_like(p)))
+        oks.append(ok)
+    ok = torch.ones((), dtype=torch.bool, device=gy.device)
+    for d, m in enumerate(oks):
+        ok = ok & m.view(*([1] * d), -1, *([1] * (nd - d - 1)))
+    gY = G[(slice(None), slice(None)) + tuple(torch.meshgrid(*pos, indexing="ij"))]
+    return torch.where(ok, gY, torch.zeros((), dtype=gY.dtype, device=gy.device))
+
+
 class _SpectralConvComplexFn(torch.autograd.Function):
     """complex_data=True spectral convolution y = I(W . F(x)) + bias with
-    its gradients, output size == input size.  F (windowed fftn) and I
-    (zero-filled ifftn) are C-linear, so with psi from _last_axis_phase and
-    the dual norm:
+    its gradients, dense or separable, output on the input grid or resized.
+    F (windowed fftn) and I (zero-filled ifftn) are C-linear, so with psi from
+    _last_axis_phase and the dual norm:
 
-        gY = I^H gy = F_dual(gy . psi)      gX = gY . conj(W)^T
-        gW = conj(X)^T . gY                gx = F^H gX = I_dual(gX) . psi
-        gbias = sum Re(gy)   (the real bias is added to the real part)"""
+        gY = I^H gy = F_dual(gy . psi)  (resized: _complex_inverse_adjoint)
+        gX = gY . conj(W)^T  (gY * conj(W))      gW = conj(X)^T . gY  (sum_b conj(X) gY)
+        gx = F^H gX = I_dual(gX) . psi           gbias = sum Re(gy)
+    (separable forms in brackets; the real bias is added to the real part)"""
 
     @staticmethod
-    def forward(ctx, x, w, bias, kept, fft_norm):
+    def forward(ctx, x, w, bias, kept, fft_norm, out_sizes=None, separable=False):
         sizes = list(x.shape[2:])
+        out_sizes = sizes if out_sizes is None else list(out_sizes)
         xhat = Fh.fft_window(x, kept, fft_norm)
-        yhat = Fh.contract_dense(xhat, w)
+        yhat = Fh.contract_dense(xhat, w, separable=separable)
         b = bias.reshape(-1) if bias is not None else None
-        y = Fh.ifft_window(yhat, sizes, sizes, b, fft_norm)
+        y = Fh.ifft_window(yhat, sizes, out_sizes, b, fft_norm)
         ctx.save_for_backward(xhat, w)
-        ctx.kept, ctx.fft_norm, ctx.sizes = list(kept), fft_norm, sizes
+        ctx.kept, ctx.fft_norm, ctx.sizes, ctx.out_sizes = list(kept), fft_norm, sizes, out_sizes
+        ctx.separable = bool(separable)
         ctx.bias_shape = None if bias is None else bias.shape
         return y
 
@@ -192,19 +317,28 @@ class _SpectralConvComplexFn(torch.autograd.Function):
         dual = _DUAL_NORM[ctx.fft_norm]
         gy = gy.contiguous().to(torch.complex64)
         psi = _last_axis_phase(sizes[-1], len(sizes), gy.device)
-        gY = Fh.fft_window((gy * psi).contiguous(), kept, dual)          # [B, Co, *m]
+        if ctx.out_sizes == sizes:
+            gY = Fh.fft_window((gy * psi).contiguous(), kept, dual)      # [B, Co, *m]
+        else:
+            gY = _complex_inverse_adjoint(gy, kept, sizes, ctx.out_sizes, dual)
         gx = gw = gb = None
         if ctx.needs_input_grad[0]:
-            wt = w.conj().transpose(0, 1).contiguous()                   # [Co, Ci, *m]
-            gX = Fh.contract_dense(gY, wt)                               # [B, Ci, *m]
+            if ctx.separable:
+                gX = Fh.contract_dense(gY.contiguous(), w.conj().contiguous(), separable=True)
+            else:
+                wt = w.conj().transpose(0, 1).contiguous()               # [Co, Ci, *m]
+                gX = Fh.contract_dense(gY.contiguous(), wt)              # [B, Ci, *m]
             gx = Fh.ifft_window(gX, sizes, sizes, None, dual) * psi
         if ctx.needs_input_grad[1]:
-            xt = xhat.conj().transpose(0, 1).contiguous()                # [Ci, B, *m]
-            gw = Fh.contract_dense(xt, gY)                               # [Ci, Co, *m]
+            if ctx.separable:
+                gw = (xhat.conj() * gY).sum(dim=0)                       # [C, *m]
+            else:
+                xt = xhat.conj().transpose(0, 1).contiguous()            # [Ci, B, *m]
+                gw = Fh.contract_dense(xt, gY.contiguous())              # [Ci, Co, *m]
         if ctx.bias_shape is not None and ctx.needs_input_grad[2]:
             dims = [0] + list(range(2, gy.ndim))
             gb = gy.real.sum(dim=dims).reshape(ctx.bias_shape)
-        return gx, gw, gb, None, None
+        return gx, gw, gb, None, None, None, None
 
 
 def _attach(y, *params):
@@ -376,16 +510,15 @@ class SpectralConv(BaseSpectralConv):
     def _forward_complex(self, x, output_shape=None):
         """complex_data=True: fftn / window / contraction / ifftn on complex
         fields (spectral_convolution.py:436-449, :500-538), output complex.
-        With gradients (output size == input size, non-separable) through
-        _SpectralConvComplexFn on the dense window weight; other cases run
-        the same forward and raise if a backward reaches them."""
+        With gradients through _SpectralConvComplexFn on the dense window
+        weight."""
         sizes = list(x.shape[2:])
         kept, sl = self.window(sizes)
         out_sizes = self.output_sizes(sizes, output_shape)
-        if (torch.is_grad_enabled() and out_sizes == sizes and not self.separable and
+        if (torch.is_grad_enabled() and
                 (x.requires_grad or any(p.requires_grad for p in self.parameters()))):
             return _SpectralConvComplexFn.apply(x, self.dense_window_weight(sl), self.bias, kept,
-                                                self.fft_norm)
+                                                self.fft_norm, out_sizes, self.separable)
         xhat = Fh.fft_window(x.detach(), kept, self.fft_norm)
         if self._contract == "tucker" and not self.separable:
             wv = self.weight[sl]
@@ -400,15 +533,13 @@ class SpectralConv(BaseSpectralConv):
     def _forward_autograd(self, x, output_shape=None):
         """Forward with gradients for x, the weight (through its dense window,
         so factorized weights get theirs through the reconstruction) and the
-        bias; output size == input size, non-separable.  Other cases run the
-        plain forward, whose backward raises."""
+        bias, on the input grid or resized, dense or separable."""
         sizes = list(x.shape[2:])
         out_sizes = self.output_sizes(sizes, output_shape)
-        if out_sizes != sizes or self.separable:
-            return self._forward_hip(x, output_shape)
         kept, sl = self.window(sizes)
         w = self.dense_window_weight(sl)
-        return _SpectralConvFn.apply(x, w, self.bias, kept, self.fft_norm)
+        return _SpectralConvFn.apply(x, w, self.bias, kept, self.fft_norm, out_sizes,
+                                     self.separable, self.enforce_hermitian_symmetry)
 
     def _forward_hip(self, x, output_shape=None, skip_kind=nat.SKIP_NONE, skip_weight=None,
                      act=nat.ACT_NONE):

@@ -32,8 +32,14 @@ def test_validation_errors_without_device():
                                  None, 0, None)
     assert rc == 1 and "modes[1]" in nat.last_error()
     rc = lib.fno_spectral_block_f32(ctypes.c_void_p(16), ctypes.c_void_p(16), None, None,
-                                    ctypes.c_void_p(16), 1, 3, 4, 2, sz, md, 1, 3, 0, None, 0, None)
+                                    ctypes.c_void_p(1 << 40), 1, 3, 4, 2, sz, md, 1, 3, 0, None, 0,
+                                    None)
     assert rc == 1 and "in_channels == out_channels" in nat.last_error()
+    # y over x: rejected (the block reads x again for the skip after writing y)
+    rc = lib.fno_spectral_block_f32(ctypes.c_void_p(16), ctypes.c_void_p(16), None, None,
+                                    ctypes.c_void_p(16 + 64), 1, 4, 4, 2, sz, md, 1, 0, 0, None, 0,
+                                    None)
+    assert rc == 1 and "overlap" in nat.last_error()
     big = nat.i32_array([8192, 8])
     rc = lib.fno_rfft_window_f32(ctypes.c_void_p(16), ctypes.c_void_p(16), 1, 2, big,
                                  nat.i32_array([4, 4]), 1, None, 0, None)
@@ -100,8 +106,9 @@ def test_noalloc_block_rejects_samples_larger_than_its_scratch():
     sz, md = nat.i32_array([4096, 4096]), nat.i32_array([64, 33])
     one = lib.fno_spectral_block_workspace_bytes(1, 64, 64, 2, sz, md)
     assert one > 64 << 20
-    v = ctypes.c_void_p(1 << 24)
-    rc = lib.fno_spectral_block_f32_noalloc(v, v, None, v, v, 2, 64, 64, 2, sz, md, 1, 1, 1, None)
+    v, out = ctypes.c_void_p(1 << 24), ctypes.c_void_p(1 << 44)   # stand-ins, never dereferenced
+    rc = lib.fno_spectral_block_f32_noalloc(v, v, None, v, out, 2, 64, 64, 2, sz, md, 1, 1, 1, None)
     assert rc == 2 and "scratch" in nat.last_error()
-    rc = lib.fno_spectral_block_f32_noalloc(None, v, None, v, v, 2, 64, 64, 2, sz, md, 1, 1, 1, None)
+    rc = lib.fno_spectral_block_f32_noalloc(None, v, None, v, out, 2, 64, 64, 2, sz, md, 1, 1, 1,
+                                            None)
     assert rc == 1

@@ -521,6 +521,48 @@ def test_spectral_conv_gradients(dim, sizes, nm, norm, cuda_device):
     assert rel_err(conv.bias.grad, bd.grad) <= TOL
 
 
+@pytest.mark.parametrize("sizes,nm,kw", [
+    ((32,), (9,), dict(output_shape=(64,))),                 # every bin incl. N//2, upsampled
+    ((30,), (8,), dict(resolution_scaling_factor=0.5)),
+    ((16, 16), (8, 9), dict(output_shape=(32, 32))),         # zeroed column lands inside
+    ((16, 20), (8, 10), dict(resolution_scaling_factor=[2, 1.5])),
+    ((12, 9), (6, 5), dict(output_shape=(7, 10))),
+    ((16, 16), (8, 8), dict(separable=True)),
+    ((16, 16), (8, 9), dict(separable=True, output_shape=(24, 32))),
+    ((8, 12, 16), (4, 6, 8), dict(resolution_scaling_factor=2)),
+])
+@pytest.mark.parametrize("enforce", [True, False])
+def test_resized_and_separable_gradients(sizes, nm, kw, enforce, cuda_device):
+    """Gradients through output_shape / resolution_scaling_factor and
+    separable weights (spectral_convolution.py:49-52, 524-568) against torch
+    autograd through the float64 oracle."""
+    print(f"grad resized/separable {sizes} {nm} {kw} enforce={enforce}", flush=True)
+    torch.manual_seed(21)
+    C, B = 3, 2
+    out_shape = kw.get("output_shape")
+    conv = na.SpectralConv(C, C, nm, enforce_hermitian_symmetry=enforce,
+                           **{k: v for k, v in kw.items() if k != "output_shape"}).to(cuda_device)
+    with torch.no_grad():
+        conv.bias.normal_()
+    x = torch.randn(B, C, *sizes)
+    xg = x.to(cuda_device).requires_grad_(True)
+    y = conv(xg, output_shape=out_shape)
+    g = torch.randn(*y.shape)
+    (y * g.to(cuda_device)).sum().backward()
+    xd = x.double().requires_grad_(True)
+    wd = conv.weight.to_tensor().detach().cpu().to(torch.complex128).requires_grad_(True)
+    bd = conv.bias.detach().cpu().double().requires_grad_(True)
+    rsf = conv.resolution_scaling_factor
+    yd = R.spectral_conv_forward(xd, wd, bd, conv.n_modes, conv.max_n_modes,
+                                 separable=conv.separable, enforce_hermitian_symmetry=enforce,
+                                 output_shape=out_shape, resolution_scaling_factor=rsf)
+    assert tuple(yd.shape) == tuple(y.shape)
+    (yd * g.double()).sum().backward()
+    assert rel_err(xg.grad, xd.grad) <= TOL
+    assert rel_err(torch.view_as_real(conv.weight.to_tensor().grad), torch.view_as_real(wd.grad)) <= TOL
+    assert rel_err(conv.bias.grad, bd.grad) <= TOL
+
+
 def test_tucker_spectral_conv_gradients(cuda_device):
     """A Tucker weight gets its gradients through the reconstruction of its
     dense window: compare the reconstructed-weight gradient path against the
@@ -638,6 +680,45 @@ def test_complex_spectral_conv_gradients(sizes, nm, norm, cuda_device):
     bd = conv.bias.detach().cpu().double().requires_grad_(True)
     yd = R.spectral_conv_forward(xd, wd, bd, conv.n_modes, conv.max_n_modes, fft_norm=norm,
                                  complex_data=True)
+    (yd * g.to(torch.complex128)).real.sum().backward()
+    assert rel_err(torch.view_as_real(xg.grad), torch.view_as_real(xd.grad)) <= TOL
+    assert rel_err(torch.view_as_real(conv.weight.to_tensor().grad), torch.view_as_real(wd.grad)) <= TOL
+    assert rel_err(conv.bias.grad, bd.grad) <= TOL
+
+
+@pytest.mark.parametrize("sizes,nm,kw", [
+    ((32,), (12,), dict(output_shape=(64,))),
+    ((37,), (12,), dict(resolution_scaling_factor=0.5, separable=True)),
+    ((16, 20), (8, 10), dict(output_shape=(32, 15))),
+    ((12, 9), (12, 9), dict(resolution_scaling_factor=[2, 3])),     # every mode
+    ((16, 16), (8, 8), dict(separable=True)),
+    ((8, 12, 16), (4, 6, 8), dict(output_shape=(16, 6, 16), separable=True)),
+])
+def test_complex_resized_and_separable_gradients(sizes, nm, kw, cuda_device):
+    """complex_data=True gradients through output_shape /
+    resolution_scaling_factor and separable weights against torch autograd
+    through the float64 oracle."""
+    print(f"complex grad resized/separable {sizes} {nm} {kw}", flush=True)
+    torch.manual_seed(23)
+    C, B = 3, 2
+    out_shape = kw.get("output_shape")
+    conv = na.SpectralConv(C, C, nm, complex_data=True, fft_norm="backward",
+                           **{k: v for k, v in kw.items() if k != "output_shape"}).to(cuda_device)
+    with torch.no_grad():
+        conv.bias.normal_()
+    x = torch.randn(B, C, *sizes, dtype=torch.complex64)
+    xg = x.to(cuda_device).requires_grad_(True)
+    y = conv(xg, output_shape=out_shape)
+    g = torch.randn(*y.shape, dtype=torch.complex64)
+    (y * g.to(cuda_device)).real.sum().backward()
+    xd = x.to(torch.complex128).requires_grad_(True)
+    wd = conv.weight.to_tensor().detach().cpu().to(torch.complex128).requires_grad_(True)
+    bd = conv.bias.detach().cpu().double().requires_grad_(True)
+    yd = R.spectral_conv_forward(xd, wd, bd, conv.n_modes, conv.max_n_modes, fft_norm="backward",
+                                 complex_data=True, separable=conv.separable,
+                                 output_shape=out_shape,
+                                 resolution_scaling_factor=conv.resolution_scaling_factor)
+    assert tuple(yd.shape) == tuple(y.shape)
     (yd * g.to(torch.complex128)).real.sum().backward()
     assert rel_err(torch.view_as_real(xg.grad), torch.view_as_real(xd.grad)) <= TOL
     assert rel_err(torch.view_as_real(conv.weight.to_tensor().grad), torch.view_as_real(wd.grad)) <= TOL
@@ -1018,15 +1099,13 @@ def test_errors_raise(cuda_device):
         conv(torch.randn(1, 3, 8, 8))            # CPU input
     with pytest.raises(RuntimeError, match="4096"):
         conv(torch.randn(1, 3, 8, 8200, device=cuda_device))
-    # gradients cover output size == input size, non-separable weights: other
-    # forwards run with gradients enabled and raise if a backward reaches them
+    # the fused forward-only kernels (block with skip / activation) have no
+    # backward: the modules take them only without gradients, and a direct
+    # call on a tensor that needs one raises when the backward reaches it
     x = torch.randn(1, 3, 8, 8, device=cuda_device, requires_grad=True)
-    y = conv(x, output_shape=(16, 16))
-    assert list(y.shape[2:]) == [16, 16]
-    with pytest.raises(NotImplementedError):
-        y.sum().backward()
-    y = na.SpectralConv(3, 3, (4, 4), separable=True).to(cuda_device)(x)
-    with pytest.raises(NotImplementedError):
+    sq = na.SpectralConv(3, 3, (4, 4)).to(cuda_device)
+    y = sq._forward_hip(x, None, nat.SKIP_IDENTITY, None, nat.ACT_GELU)
+    with pytest.raises(NotImplementedError, match="no backward"):
         y.sum().backward()
 
 

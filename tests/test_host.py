@@ -228,3 +228,157 @@ def test_ada_in_norm_closed_form():
                           channel_mlp_skip="linear", complex_data=True)
     cblock.set_ada_in_embeddings(e)
     assert torch.equal(cblock.norm[0].fi.embedding, e)
+
+
+# ---- backward algebra of the spectral convolution, on the CPU -------------
+# _SpectralConvFn's backward (index maps of resized outputs, the zeroed
+# column's symmetrisation, separable products, dual-norm scaling) with the
+# library's window transforms restated in torch.fft (float64), against
+# autograd through the same restated forward: checks the host-side gradient
+# logic without a GPU; the GPU tests check the transforms themselves.
+def _fft_size(sizes):
+    f = list(sizes)
+    f[-1] = f[-1] // 2 + 1
+    return f
+
+
+def _rfft_window(x, modes, norm="forward"):
+    nd = len(modes)
+    dims = list(range(-nd, 0))
+    xf = torch.fft.rfftn(x.to(torch.float64), norm=norm, dim=dims)
+    if nd > 1:
+        xf = torch.fft.fftshift(xf, dim=dims[:-1])
+    return xf[R.x_slices(_fft_size(x.shape[2:]), list(modes))]
+
+
+def _irfft_window(yhat, in_sizes, out_sizes, bias=None, norm="forward", enforce=True):
+    B, C, *m = yhat.shape
+    nd = len(m)
+    dims = list(range(-nd, 0))
+    fs = _fft_size(in_sizes)
+    out = torch.zeros(B, C, *fs, dtype=torch.complex128)
+    out[R.x_slices(fs, m)] = yhat
+    if nd > 1:
+        out = torch.fft.ifftshift(out, dim=dims[:-1])
+    ms = list(out_sizes)
+    if enforce:
+        out = torch.fft.ifftn(out, s=ms[:-1], dim=dims[:-1], norm=norm) if nd > 1 else out.clone()
+        out[..., 0].imag.zero_()
+        if ms[-1] % 2 == 0:
+            out[..., -1].imag.zero_()
+        y = torch.fft.irfft(out, n=ms[-1], dim=dims[-1], norm=norm)
+    else:
+        y = torch.fft.irfftn(out, s=ms, dim=dims, norm=norm)
+    return y if bias is None else y + bias.view(1, -1, *([1] * nd))
+
+
+def _contract(x, w, separable=False):
+    return R.contract_dense_separable(x, w) if separable else R.contract_dense(x, w)
+
+
+@pytest.mark.parametrize("sizes,kept,outs,sep", [
+    ((16,), (9,), (32,), False), ((16,), (9,), (8,), False), ((15,), (8,), (30,), False),
+    ((8, 8), (6, 5), (16, 16), False), ((8, 8), (8, 5), (4, 6), False),
+    ((12, 10), (6, 6), (24, 20), True), ((9, 7), (8, 4), (18, 14), False),
+    ((6, 8, 10), (6, 8, 6), (3, 16, 20), True), ((8, 8), (6, 5), (8, 8), True),
+])
+@pytest.mark.parametrize("norm", ["forward", "ortho"])
+@pytest.mark.parametrize("enforce", [True, False])
+def test_spectral_conv_backward_algebra(sizes, kept, outs, sep, norm, enforce, monkeypatch):
+    from neuraloperator_amd import functional as Fh
+    from neuraloperator_amd import spectral_convolution as S
+    monkeypatch.setattr(Fh, "rfft_window", _rfft_window)
+    monkeypatch.setattr(Fh, "irfft_window", _irfft_window)
+    monkeypatch.setattr(Fh, "contract_dense", _contract)
+    torch.manual_seed(0)
+    C, B = 3, 2
+    x = torch.randn(B, C, *sizes, dtype=torch.float64)
+    wshape = (C, *kept) if sep else (C, C, *kept)
+    w = torch.complex(torch.randn(*wshape, dtype=torch.float64),
+                      torch.randn(*wshape, dtype=torch.float64))
+    bias = torch.randn(1, C, *([1] * len(sizes)), dtype=torch.float64)
+    g = torch.randn(B, C, *outs, dtype=torch.float64)
+    leaves = [t.clone().requires_grad_(True) for t in (x, w, bias)]
+    y = S._SpectralConvFn.apply(*leaves, list(kept), norm, list(outs), sep, enforce)
+    got = torch.autograd.grad((y * g).sum(), leaves)
+    ref_leaves = [t.clone().requires_grad_(True) for t in (x, w, bias)]
+    xr, wr, br = ref_leaves
+    yr = _irfft_window(_contract(_rfft_window(xr, kept, norm), wr, sep), sizes, outs, None, norm,
+                       enforce) + br
+    want = torch.autograd.grad((yr * g).sum(), ref_leaves)
+    # the backward runs in float32 (as on the GPU)
+    for a, b in zip(got, want):
+        assert ((a - b).abs().max() / b.abs().max()).item() < 1e-5
+
+
+def _fft_window(x, modes, norm="forward"):
+    nd = len(modes)
+    dims = list(range(-nd, 0))
+    xf = torch.fft.fftn(x.to(torch.complex128), norm=norm, dim=dims)
+    if nd > 1:
+        xf = torch.fft.fftshift(xf, dim=dims)
+    return xf[R.x_slices(list(x.shape[2:]), list(modes))]
+
+
+def _ifft_window(yhat, in_sizes, out_sizes, bias=None, norm="forward"):
+    B, C, *m = yhat.shape
+    nd = len(m)
+    dims = list(range(-nd, 0))
+    out = torch.zeros(B, C, *in_sizes, dtype=torch.complex128)
+    out[R.x_slices(list(in_sizes), m)] = yhat
+    if nd > 1:   # the reference un-shifts the non-last axes only (:531-532)
+        out = torch.fft.ifftshift(out, dim=dims[:-1])
+    y = torch.fft.ifftn(out, s=list(out_sizes), dim=dims, norm=norm)
+    return y if bias is None else y + bias.view(1, -1, *([1] * nd))
+
+
+@pytest.mark.parametrize("sizes,kept,outs,sep", [
+    ((16,), (7,), (16,), False), ((16,), (7,), (32,), False), ((15,), (9,), (8,), True),
+    ((8, 8), (6, 5), (8, 8), False), ((8, 8), (6, 5), (16, 12), False),
+    ((8, 10), (8, 10), (5, 20), True), ((9, 7), (5, 7), (18, 6), False),
+    ((6, 8, 10), (4, 6, 6), (12, 4, 20), True),
+])
+@pytest.mark.parametrize("norm", ["backward", "ortho"])
+def test_complex_spectral_conv_backward_algebra(sizes, kept, outs, sep, norm, monkeypatch):
+    from neuraloperator_amd import functional as Fh
+    from neuraloperator_amd import spectral_convolution as S
+    monkeypatch.setattr(Fh, "fft_window", _fft_window)
+    monkeypatch.setattr(Fh, "ifft_window", _ifft_window)
+    monkeypatch.setattr(Fh, "contract_dense", _contract)
+    torch.manual_seed(1)
+    C, B = 3, 2
+    cplx = lambda *s: torch.complex(torch.randn(*s, dtype=torch.float64),
+                                    torch.randn(*s, dtype=torch.float64))
+    x = cplx(B, C, *sizes)
+    w = cplx(*((C, *kept) if sep else (C, C, *kept)))
+    bias = torch.randn(1, C, *([1] * len(sizes)), dtype=torch.float64)
+    g = cplx(B, C, *outs)
+    leaves = [t.clone().requires_grad_(True) for t in (x, w, bias)]
+    y = S._SpectralConvComplexFn.apply(*leaves, list(kept), norm, list(outs), sep)
+    got = torch.autograd.grad((y * g).real.sum(), leaves)
+    ref_leaves = [t.clone().requires_grad_(True) for t in (x, w, bias)]
+    xr, wr, br = ref_leaves
+    yr = _ifft_window(_contract(_fft_window(xr, kept, norm), wr, sep), sizes, outs, None, norm)
+    yr = yr + br
+    want = torch.autograd.grad((yr * g).real.sum(), ref_leaves)
+    for a, b in zip(got, want):
+        assert ((a - b).abs().max() / b.abs().max()).item() < 1e-5
+
+
+def test_boundary_resolves_lazy_conjugates():
+    """w.conj() is a view with torch's conjugate bit over w's storage, and
+    .contiguous() keeps it when the view is already contiguous: the C-ABI
+    would read w itself.  The boundary helpers resolve the bit (so the data
+    handed over is conj(w)), and the pointer helper refuses an unresolved
+    view."""
+    from neuraloperator_amd import functional as Fh
+    w = torch.randn(3, 4, dtype=torch.complex64)
+    v = w.conj().contiguous()
+    assert v.is_conj() and v.data_ptr() == w.data_ptr()
+    r = Fh._c64(v)
+    assert not r.is_conj()
+    assert torch.equal(torch.view_as_real(r), torch.view_as_real(w.conj().resolve_conj()))
+    assert torch.equal(torch.view_as_real(Fh._c64(-w.conj())),
+                       torch.view_as_real((-w.conj()).resolve_conj().resolve_neg()))
+    with pytest.raises(RuntimeError, match="conjugate"):
+        Fh._ptr(v)
