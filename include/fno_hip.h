@@ -211,6 +211,37 @@ int fno_spectral_block_is_fused(int32_t batch, int32_t in_channels, int32_t out_
                                 int32_t skip_kind);
 
 /*
+ * One FNO layer in post-activation form, for the autocast (bfloat16)
+ * forward.  Replaces FNOBlocks.forward_with_postactivation with a two-layer
+ * channel MLP, neuralop/layers/fno_block.py:331-379 (SpectralConv, the fno
+ * skip, activation, ChannelMLP.forward of channel_mlp.py:82-119, the
+ * channel-MLP skip of skip_connections.py:88-93, activation):
+ *     y1 = act(SpectralConv(x) + skip(x))                 (as fno_spectral_block_f32)
+ *     y  = act(W2 gelu(W1 y1 + b1) + b2 + mlp_skip(x))
+ *   channels in == out; mlp_w1 [hidden, C], mlp_b1 [hidden] or NULL,
+ *   mlp_w2 [C, hidden], mlp_b2 [C] or NULL; mlp_skip_kind FNO_SKIP_NONE,
+ *   FNO_SKIP_SOFT_GATING (gate_weight [C], gate_bias [C] or NULL) or
+ *   FNO_SKIP_IDENTITY.  The two MLP products take y1, W1, h and W2 rounded to
+ *   bfloat16 (nearest even) with fp32 accumulation, as the Conv1d layers run
+ *   under torch.autocast(dtype=torch.bfloat16); everything else is fp32.
+ *   One pass: the MLP runs in the spectral block's row epilogue, so y1 never
+ *   reaches memory.  Covered where fno_layer_is_fused says so (2D, 64
+ *   channels, 32 hidden, a skip, the fused block's shapes); otherwise
+ *   FNO_ERR_UNSUPPORTED, nothing enqueued (compose fno_spectral_block_f32 and
+ *   fno_channel_mlp_f32).  Workspace: fno_spectral_block_workspace_bytes.
+ */
+int fno_layer_f32(const float* x, const void* w, const float* bias, const float* skip_weight,
+                  const float* mlp_w1, const float* mlp_b1, const float* mlp_w2,
+                  const float* mlp_b2, const float* gate_weight, const float* gate_bias, float* y,
+                  int32_t batch, int32_t channels, int32_t hidden_channels, int32_t ndim,
+                  const int32_t* sizes, const int32_t* modes, int32_t norm, int32_t skip_kind,
+                  int32_t mlp_skip_kind, int32_t act, void* workspace, size_t workspace_bytes,
+                  void* stream);
+int fno_layer_is_fused(int32_t batch, int32_t channels, int32_t hidden_channels, int32_t ndim,
+                       const int32_t* sizes, const int32_t* modes, int32_t skip_kind,
+                       int32_t mlp_skip_kind);
+
+/*
  * fno_spectral_block_f32 without a workspace argument and without any device
  * allocation.  No counterpart in the reference: it is for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,

@@ -49,7 +49,10 @@ int fast1d_block(const float* x, const float2* w, const float* bias, const float
                  hipStream_t st);
 int fast2d_block(const float* x, const float2* w, const float* bias, const float* skip_w, float* y,
                  int B, int Ci, int Co, const int32_t* sizes, const int32_t* modes, int norm,
-                 int skip_kind, int act, void* ws, size_t ws_bytes, hipStream_t st);
+                 int skip_kind, int act, void* ws, size_t ws_bytes, hipStream_t st,
+                 const LayerMlp* mlp = nullptr);
+bool rowsynth_mlp_covers(int H, int W, int Ci, int Co, int m1, int m2h, int hidden,
+                         int skip_kind);
 }  // namespace fno
 
 using namespace fno;
@@ -497,6 +500,75 @@ int fno_spectral_block_f32(const float* x, const void* w, const float* bias,
   return spectral_block_run(x, w, bias, skip_weight, y, batch, in_channels, out_channels, ndim,
                             sizes, modes, norm, skip_kind, act, workspace, workspace_bytes,
                             reinterpret_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------- FNO layer
+static bool layer_fused(int32_t batch, int32_t channels, int32_t hidden, int32_t ndim,
+                        const int32_t* sizes, const int32_t* modes, int32_t skip_kind,
+                        int32_t mlp_skip_kind) {
+  if (!sizes || !modes || ndim != 2 || batch < 1) return false;
+  if (!(mlp_skip_kind == FNO_SKIP_NONE || mlp_skip_kind == FNO_SKIP_SOFT_GATING ||
+        mlp_skip_kind == FNO_SKIP_IDENTITY))
+    return false;
+  return fast2d_supported(batch, channels, channels, ndim, sizes, modes, skip_kind) &&
+         rowsynth_mlp_covers(sizes[0], sizes[1], channels, channels, modes[0], modes[1], hidden,
+                             skip_kind);
+}
+
+extern "C" {
+
+int fno_layer_is_fused(int32_t batch, int32_t channels, int32_t hidden_channels, int32_t ndim,
+                       const int32_t* sizes, const int32_t* modes, int32_t skip_kind,
+                       int32_t mlp_skip_kind) {
+  return layer_fused(batch, channels, hidden_channels, ndim, sizes, modes, skip_kind,
+                     mlp_skip_kind)
+             ? 1
+             : 0;
+}
+
+int fno_layer_f32(const float* x, const void* w, const float* bias, const float* skip_weight,
+                  const float* mlp_w1, const float* mlp_b1, const float* mlp_w2,
+                  const float* mlp_b2, const float* gate_weight, const float* gate_bias, float* y,
+                  int32_t batch, int32_t channels, int32_t hidden_channels, int32_t ndim,
+                  const int32_t* sizes, const int32_t* modes, int32_t norm, int32_t skip_kind,
+                  int32_t mlp_skip_kind, int32_t act, void* workspace, size_t workspace_bytes,
+                  void* stream) {
+  clear_error();
+  int rc = spectral_block_check(x, w, y, batch, channels, channels, ndim, sizes, modes, norm,
+                                skip_kind, act, skip_weight);
+  if (rc) return rc;
+  FNO_CHECK_ARG(mlp_w1 && mlp_w2, "mlp_w1/mlp_w2 must not be NULL");
+  FNO_CHECK_ARG(hidden_channels >= 1, "hidden_channels must be positive");
+  FNO_CHECK_ARG(mlp_skip_kind == FNO_SKIP_NONE || mlp_skip_kind == FNO_SKIP_SOFT_GATING ||
+                    mlp_skip_kind == FNO_SKIP_IDENTITY,
+                "channel MLP skip must be none, soft-gating or identity (got %d)", mlp_skip_kind);
+  FNO_CHECK_ARG(mlp_skip_kind != FNO_SKIP_SOFT_GATING || gate_weight,
+                "soft-gating needs a gate weight");
+  if (!layer_fused(batch, channels, hidden_channels, ndim, sizes, modes, skip_kind,
+                   mlp_skip_kind)) {
+    set_error("FNO layer: this shape has no one-pass kernel (compose fno_spectral_block_f32 and "
+              "fno_channel_mlp_f32)");
+    return FNO_ERR_UNSUPPORTED;
+  }
+  const size_t need = fno_spectral_block_workspace_bytes(batch, channels, channels, ndim, sizes,
+                                                         modes);
+  if (!workspace || workspace_bytes < need) {
+    set_error("FNO layer: workspace %zu < %zu bytes", workspace_bytes, need);
+    return FNO_ERR_WORKSPACE;
+  }
+  LayerMlp mlp;
+  mlp.w1 = mlp_w1;
+  mlp.b1 = mlp_b1;
+  mlp.w2 = mlp_w2;
+  mlp.b2 = mlp_b2;
+  mlp.gate_w = gate_weight;
+  mlp.gate_b = mlp_skip_kind == FNO_SKIP_SOFT_GATING ? gate_bias : nullptr;
+  mlp.gate_kind = mlp_skip_kind;
+  return fast2d_block(x, reinterpret_cast<const float2*>(w), bias, skip_weight, y, batch, channels,
+                      channels, sizes, modes, norm, skip_kind, act, workspace, workspace_bytes,
+                      reinterpret_cast<hipStream_t>(stream), &mlp);
 }
 
 }  // extern "C"

@@ -86,6 +86,20 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
                                            0x00020000);
 }
 
+// The channel MLP of an FNO layer folded into the fused 2D block's row
+// epilogue (64 channels, 32 hidden):
+//   y = act(W2 gelu(W1 y1 + b1) + b2 + gate(x)),  y1 = act(spectral + skip)
+// gate: soft-gating g * x + gb, the identity x, or nothing.
+struct LayerMlp {
+  const float* w1 = nullptr;       // [32, 64]
+  const float* b1 = nullptr;       // [32] or NULL
+  const float* w2 = nullptr;       // [64, 32]
+  const float* b2 = nullptr;       // [64] or NULL
+  const float* gate_w = nullptr;   // [64] (soft-gating)
+  const float* gate_b = nullptr;   // [64] or NULL
+  int gate_kind = 0;               // FNO_SKIP_NONE / SOFT_GATING / IDENTITY
+};
+
 // ------------------------------------------------------------------ host side
 void set_error(const char* fmt, ...);
 int hip_status(hipError_t e, const char* what);

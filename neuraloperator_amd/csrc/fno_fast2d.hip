@@ -876,6 +876,11 @@ bool rowsynth_covers(int H, int W, int Ci, int Co, int m1, int m2h);
 int rowsynth_epilogue(const float* x, const float2* yhat, const float* skip_w, const float* bias,
                       float* y, int B, int Ci, int H, int W, int m1, int m2h, int skip_kind,
                       int act, float s, hipStream_t st);
+bool rowsynth_mlp_covers(int H, int W, int Ci, int Co, int m1, int m2h, int hidden,
+                         int skip_kind);
+int rowsynth_mlp_epilogue(const float* x, const float2* yhat, const float* skip_w,
+                          const float* bias, float* y, int B, int H, int W, int m1, int m2h,
+                          int skip_kind, int act, float s, const LayerMlp& mlp, hipStream_t st);
 int contract_dense(const float2* X, const float2* W, float2* Y, int B, int Ci, int Co, int64_t M,
                    int64_t sWi, int64_t sWo, int64_t sWk, hipStream_t st);
 int rfft_window(const float* x, float2* xhat, int64_t planes, int32_t ndim, const int32_t* sizes,
@@ -1160,7 +1165,8 @@ static int dispatch_epi(int W, int Co, int Ci, const float* x, const float2* z,
 
 int fast2d_block(const float* x, const float2* w, const float* bias, const float* skip_w, float* y,
                  int B, int Ci, int Co, const int32_t* sizes, const int32_t* modes, int norm,
-                 int skip_kind, int act, void* ws, size_t ws_bytes, hipStream_t st) {
+                 int skip_kind, int act, void* ws, size_t ws_bytes, hipStream_t st,
+                 const LayerMlp* mlp) {
   const int H = sizes[0], W = sizes[1], m1 = modes[0], m2h = modes[1];
   const int64_t M = (int64_t)m1 * m2h;
   const size_t need = fast2d_workspace(B, Ci, Co, sizes, modes);
@@ -1186,6 +1192,9 @@ int fast2d_block(const float* x, const float2* w, const float* bias, const float
   if (rc) return rc;
   rc = contract_dense(xhat, w, yhat, B, Ci, Co, M, (int64_t)Co * M, M, 1, st);
   if (rc) return rc;
+  if (mlp)
+    return rowsynth_mlp_epilogue(x, yhat, skip_w, bias, y, B, H, W, m1, m2h, skip_kind, act,
+                                 iscale, *mlp, st);
   if (!uses_z(Ci, Co, sizes, modes))
     return rowsynth_epilogue(x, yhat, skip_w, bias, y, B, Ci, H, W, m1, m2h, skip_kind, act,
                              iscale, st);

@@ -95,17 +95,19 @@ __device__ __forceinline__ float synth_entry(int j, int col, int W, int m2h, flo
 // in the XCD's L2.  Otherwise blocks are dealt out in a stride.
 namespace rs {
 constexpr int R = 8;                     // rows per block
+constexpr int kHidden = 32;              // hidden units of a folded channel MLP
 }  // namespace rs
+static constexpr int kSynthMaxM1 = 128;   // window rows of the LDS twiddle table
 #ifndef SYN_BATCH
 #define SYN_BATCH 8                      // window rows whose loads are issued together
 #endif
 
-template <int W, int CI, int KSZ, bool XSKIP>
+template <int W, int CI, int KSZ, bool XSKIP, bool MLP>
 __global__ void __launch_bounds__(rg::kThreads)
 k_row_synth(const float* __restrict__ x, const float2* __restrict__ yhat,
             const float* __restrict__ skip_w, const float* __restrict__ bias,
             float* __restrict__ y, int B, int H, int m1, int m2h, int skip_kind, int act,
-            float s, int xcd_map) {
+            float s, int xcd_map, LayerMlp mlp) {
   constexpr int R = rs::R;
   constexpr int ROWS = rg::kStepPx / W;          // rows per step
   constexpr int WPR = rg::kWaves / ROWS;         // waves per row
@@ -120,6 +122,13 @@ k_row_synth(const float* __restrict__ x, const float2* __restrict__ yhat,
   v8bf* wf = zf + R * ZROW;                                    // [WFRAG]
   float* cinit = reinterpret_cast<float*>(wf + WFRAG);         // [R][64]
   float2* twl = reinterpret_cast<float2*>(cinit + R * rg::kCo);  // [m1] block twiddles
+  // channel MLP (MLP only): W1 / W2 as bf16 A fragments, b1, b2 (+ gate
+  // bias) and the gate weights
+  v8bf* w1f = reinterpret_cast<v8bf*>(twl + kSynthMaxM1);    // [2 ht][2 ks][64]
+  v8bf* w2f = w1f + 2 * 2 * 64;                              // [4 ot][64]
+  float* mb1 = reinterpret_cast<float*>(w2f + 4 * 64);       // [32]
+  float* mseed = mb1 + rs::kHidden;                          // [64] b2 + gate bias
+  float* mgate = mseed + rg::kCo;                            // [64] gate weight (0: none)
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int G = lane >> 4, n = lane & 15;
@@ -161,6 +170,38 @@ k_row_synth(const float* __restrict__ x, const float2* __restrict__ yhat,
       }
       wf[((ot * KSX + ks) * 2) * 64 + ln] = hi;
       wf[((ot * KSX + ks) * 2 + 1) * 64 + ln] = lo;
+    }
+  }
+  if constexpr (MLP) {
+    // The accumulators of a 16-row tile hold rows 4G + r (r < 4) in lane
+    // group G, so the bf16 B operand of the next product, 8 rows per lane
+    // group, takes rows 4G + r of two consecutive tiles: K slot (G, i) of
+    // k-step ks is channel 32 ks + 16 (i / 4) + 4 G + i % 4 of y1 (W1
+    // product) and hidden unit 16 (i / 4) + 4 G + i % 4 of h (W2 product).
+    // The A fragments take their columns in the same order.
+    for (int f = tid; f < 2 * 2 * 64 + 4 * 64; f += rg::kThreads) {
+      const int ln = f & 63, m = ln & 15, g = ln >> 4;
+      v8bf a;
+      if (f < 2 * 2 * 64) {
+        const int ks = (f >> 6) & 1, ht = f >> 7;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          a[i] = (__bf16)mlp.w1[(16 * ht + m) * rg::kCo + 32 * ks + 16 * (i >> 2) + 4 * g + (i & 3)];
+        w1f[f] = a;
+      } else {
+        const int ot = (f - 2 * 2 * 64) >> 6;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          a[i] = (__bf16)mlp.w2[(16 * ot + m) * rs::kHidden + 16 * (i >> 2) + 4 * g + (i & 3)];
+        w2f[f - 2 * 2 * 64] = a;
+      }
+    }
+    for (int o = tid; o < rg::kCo; o += rg::kThreads) {
+      if (o < rs::kHidden) mb1[o] = mlp.b1 ? mlp.b1[o] : 0.f;
+      mseed[o] = (mlp.b2 ? mlp.b2[o] : 0.f) + (mlp.gate_b ? mlp.gate_b[o] : 0.f);
+      mgate[o] = mlp.gate_kind == FNO_SKIP_SOFT_GATING ? mlp.gate_w[o]
+                 : mlp.gate_kind == FNO_SKIP_IDENTITY  ? 1.f
+                                                       : 0.f;
     }
   }
   v8bf th[2][KSZ], tl[2][KSZ];
@@ -246,6 +287,92 @@ k_row_synth(const float* __restrict__ x, const float2* __restrict__ yhat,
           acc[ot][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, th[u][ks], acc[ot][u], 0, 0, 0);
         }
       }
+    if constexpr (MLP) {
+      // compiler barrier: the MLP's LDS operands are read again in every
+      // step rather than kept in registers across the unrolled steps
+      __asm__ volatile("" ::: "memory");
+      // y1 = act(acc), rounded to bf16, as the B fragments of the W1 product
+      // (K slot (G, i) of k-step ks: channel 32 ks + 16 (i / 4) + 4 G + i % 4)
+      v8bf yb[2][2];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            float v = acc[2 * ks + (i >> 2)][u][i & 3];
+            v = act_select(gelu_erf(v), v, gmask);
+            yb[ks][u][i] = (__bf16)v;
+          }
+      // h = gelu(W1 y1 + b1), 2 tiles of 16 hidden units
+      v4f hacc[2][2];
+#pragma unroll
+      for (int ht = 0; ht < 2; ++ht)
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) hacc[ht][u][r] = mb1[16 * ht + 4 * G + r];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int ht = 0; ht < 2; ++ht) {
+          const v8bf a = w1f[(ht * 2 + ks) * 64 + lane];
+#pragma unroll
+          for (int u = 0; u < 2; ++u)
+            hacc[ht][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, yb[ks][u], hacc[ht][u], 0, 0, 0);
+        }
+      v8bf hb[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) hb[u][i] = (__bf16)gelu_erf(hacc[i >> 2][u][i & 3]);
+      // y = act(W2 h + b2 + g x): the accumulators seeded with b2 (+ gate
+      // bias); g x as the product diag(g) . x on the x fragments of the skip
+      // (three-term splits, like the skip); the store applies the activation
+#pragma unroll
+      for (int ot = 0; ot < 4; ++ot)
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[ot][u][r] = mseed[16 * ot + 4 * G + r];
+      // diag(g) fragment of tile ot in k-step ks = ot / 2: lane (G, m) holds
+      // g[16 ot + m] in slot m % 8 when 8 G + m % 8 == 16 (ot % 2) + m
+      const int m16 = lane & 15;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          v8bf bh, bl;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const bf16x2 p = split_bf16(u ? xc[ks][i].y : xc[ks][i].x);
+            bh[i] = p.hi;
+            bl[i] = p.lo;
+          }
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            const int ot = 2 * ks + t;
+            const bool mine = G == 2 * t + (m16 >> 3);
+            const bf16x2 g = split_bf16(mine ? mgate[16 * ot + m16] : 0.f);
+            v8bf gh, gl;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              gh[i] = (i == (m16 & 7)) ? g.hi : (__bf16)0.f;
+              gl[i] = (i == (m16 & 7)) ? g.lo : (__bf16)0.f;
+            }
+            acc[ot][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(gh, bl, acc[ot][u], 0, 0, 0);
+            acc[ot][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(gl, bh, acc[ot][u], 0, 0, 0);
+            acc[ot][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(gh, bh, acc[ot][u], 0, 0, 0);
+          }
+        }
+#pragma unroll
+      for (int ot = 0; ot < 4; ++ot) {
+        const v8bf a = w2f[ot * 64 + lane];
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+          acc[ot][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, hb[u], acc[ot][u], 0, 0, 0);
+      }
+    }
     const __amdgpu_buffer_rsrc_t ry = make_rsrc(y + (int64_t)b * rg::kCo * HW,
                                                 (uint32_t)rg::kCo * HW * 4u);
     const uint32_t yvoff =
@@ -417,11 +544,11 @@ static int device_cus() {
 }
 
 // ---- row products with the column synthesis from yhat
-static constexpr int kSynthMaxM1 = 128;   // window rows of the LDS twiddle table
 
-static size_t rowsynth_lds_bytes(int ksz, int ksx) {
+static size_t rowsynth_lds_bytes(int ksz, int ksx, bool mlp = false) {
   return (size_t)rs::R * ksz * 4 * 2 * 64 * 16 + (size_t)4 * (ksx > 0 ? ksx : 1) * 2 * 64 * 16 +
-         (size_t)rs::R * rg::kCo * sizeof(float) + (size_t)kSynthMaxM1 * 8;
+         (size_t)rs::R * rg::kCo * sizeof(float) + (size_t)kSynthMaxM1 * 8 +
+         (mlp ? (size_t)(2 * 2 * 64 + 4 * 64) * 16 + (size_t)(rs::kHidden + 2 * rg::kCo) * 4 : 0);
 }
 
 // Shapes k_row_synth covers for every skip kind: 64 output channels, 32 or
@@ -434,12 +561,13 @@ bool rowsynth_covers(int H, int W, int Ci, int Co, int m1, int m2h) {
   return rowsynth_lds_bytes(rowgemm_ksz(m2h), 2) <= 160 * 1024;
 }
 
-template <int W, int CI, int KSZ, bool XSKIP>
+template <int W, int CI, int KSZ, bool XSKIP, bool MLP = false>
 static int launch_rowsynth(const float* x, const float2* yhat, const float* skip_w,
                            const float* bias, float* y, int B, int H, int m1, int m2h,
-                           int skip_kind, int act, float s, hipStream_t st) {
-  const size_t lds = rowsynth_lds_bytes(KSZ, XSKIP ? CI / 32 : 0);
-  auto kern = k_row_synth<W, CI, KSZ, XSKIP>;
+                           int skip_kind, int act, float s, hipStream_t st,
+                           const LayerMlp& mlp = LayerMlp{}) {
+  const size_t lds = rowsynth_lds_bytes(KSZ, XSKIP ? CI / 32 : 0, MLP);
+  auto kern = k_row_synth<W, CI, KSZ, XSKIP, MLP>;
   if (lds > 64 * 1024) {
     int rc = hip_status(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
@@ -454,7 +582,7 @@ static int launch_rowsynth(const float* x, const float2* yhat, const float* skip
   const bool xcd = (B % 8 == 0) && (8 * NR == cus);
   const int64_t grid = xcd ? 8 * NR : (nblocks < cus ? nblocks : cus);
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(rg::kThreads), lds, st, x, yhat, skip_w,
-                     bias, y, B, H, m1, m2h, skip_kind, act, s, xcd ? 1 : 0);
+                     bias, y, B, H, m1, m2h, skip_kind, act, s, xcd ? 1 : 0, mlp);
   return launch_status("k_row_synth");
 }
 
@@ -478,6 +606,31 @@ static int dispatch_rowsynth_w(const float* x, const float2* yhat, const float* 
     return launch_rowsynth<W, 64, 2, false>(x, yhat, skip_w, bias, y, B, H, m1, m2h, skip_kind,
                                             act, s, st);
   set_error("row synthesis epilogue: unsupported Ci=%d m2h=%d", Ci, m2h);
+  return FNO_ERR_UNSUPPORTED;
+}
+
+// Shapes the row epilogue can also fold a layer's channel MLP into: 64
+// input channels (the gate adds the layer input), 64 hidden-row bins at most
+// two k-steps, a skip, and room in LDS for the MLP's weights.
+bool rowsynth_mlp_covers(int H, int W, int Ci, int Co, int m1, int m2h, int hidden,
+                         int skip_kind) {
+  if (!rowsynth_covers(H, W, Ci, Co, m1, m2h) || Ci != rg::kCo || hidden != rs::kHidden)
+    return false;
+  if (skip_kind == FNO_SKIP_NONE) return false;
+  return rowsynth_lds_bytes(rowgemm_ksz(m2h), 2, true) <= 160 * 1024;
+}
+
+int rowsynth_mlp_epilogue(const float* x, const float2* yhat, const float* skip_w,
+                          const float* bias, float* y, int B, int H, int W, int m1, int m2h,
+                          int skip_kind, int act, float s, const LayerMlp& mlp, hipStream_t st) {
+  const int ksz = rowgemm_ksz(m2h);
+#define FNO_RSM(w, k)                                                                              \
+  if (W == w && ksz == k)                                                                          \
+    return launch_rowsynth<w, 64, k, true, true>(x, yhat, skip_w, bias, y, B, H, m1, m2h,         \
+                                                 skip_kind, act, s, st, mlp);
+  FNO_RSM(128, 1) FNO_RSM(128, 2) FNO_RSM(256, 1) FNO_RSM(256, 2)
+#undef FNO_RSM
+  set_error("row epilogue with channel MLP: unsupported W=%d m2h=%d", W, m2h);
   return FNO_ERR_UNSUPPORTED;
 }
 

@@ -300,10 +300,51 @@ class FNOBlocks(nn.Module):
             return nat.SKIP_IDENTITY, None
         return None
 
+    def _fused_layer(self, x, index, fused_mlp):
+        """The whole layer (spectral block, its skip and activation, the
+        channel MLP, its skip and the second activation) as one fno_layer_f32
+        call, for the bf16-autocast forward; None where that kernel does not
+        cover the layer."""
+        conv = self.convs[index]
+        if (conv.separable or conv.complex_data or conv._contract not in ("dense", "cp", "tt")
+                or conv.in_channels != conv.out_channels):
+            return None
+        if not Fh.autocast_bf16(x.device.type) or x.dtype != torch.float32:
+            return None
+        kind, sw = self._fused_skip(index)
+        mkind, gate = fused_mlp
+        mlp = self.channel_mlp[index]
+        sizes = list(x.shape[2:])
+        kept, sl = conv.window(sizes)
+        C, Ch = conv.out_channels, mlp.hidden_channels
+        if not Fh.layer_is_fused(x.shape[0], C, Ch, sizes, kept, kind, mkind):
+            return None
+        fc0, fc1 = mlp.fcs
+        d = lambda t: None if t is None else t.detach()
+        act = nat.ACT_GELU if index < (self.n_layers - 1) else nat.ACT_NONE
+        y = Fh.fno_layer(x.detach(), conv.dense_window_weight(sl).detach(),
+                         None if conv.bias is None else conv.bias.detach().reshape(-1), kept, kind,
+                         d(sw), fc0.weight.detach().reshape(Ch, C), d(fc0.bias),
+                         fc1.weight.detach().reshape(C, Ch), d(fc1.bias), mkind,
+                         None if gate is None else gate.weight.detach().reshape(-1),
+                         None if gate is None or gate.bias is None else gate.bias.detach().reshape(-1),
+                         act, conv.fft_norm)
+        params = [x] + list(conv.parameters()) + list(mlp.parameters())
+        if self.fno_skips is not None:
+            params += list(self.fno_skips[index].parameters())
+        if gate is not None:
+            params += list(gate.parameters())
+        return _attach(y, *params)
+
     def forward_with_postactivation(self, x, index=0, output_shape=None):
         profiler = get_active_profiler()
         prefix = f"fno_blocks/{index}"
         fused_mlp = self._fused_mlp(x, index, output_shape)
+        if fused_mlp is not None and self._can_fuse(x, index, output_shape):
+            with maybe_profile(profiler, f"{prefix}/fno_layer", x.device):
+                y = self._fused_layer(x, index, fused_mlp)
+            if y is not None:
+                return y
         x_in = x
         if self.use_channel_mlp and self.channel_mlp_skips is not None and fused_mlp is None:
             with maybe_profile(profiler, f"{prefix}/channel_mlp_skip", x.device):

@@ -265,3 +265,39 @@ def spectral_block(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.T
                                          wsb, _stream(x.device)),
               "fno_spectral_block_f32")
     return y
+
+
+def layer_is_fused(B, C, hidden, sizes, modes, skip_kind, mlp_skip_kind) -> bool:
+    lib = nat.load()
+    return bool(lib.fno_layer_is_fused(B, C, hidden, len(sizes), nat.i32_array(sizes),
+                                       nat.i32_array(modes), skip_kind, mlp_skip_kind))
+
+
+def fno_layer(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor],
+              modes: Sequence[int], skip_kind: int, skip_weight: Optional[torch.Tensor],
+              w1: torch.Tensor, b1: Optional[torch.Tensor], w2: torch.Tensor,
+              b2: Optional[torch.Tensor], mlp_skip_kind: int, gate_weight: Optional[torch.Tensor],
+              gate_bias: Optional[torch.Tensor], act: int, fft_norm: str = "forward") -> torch.Tensor:
+    """One FNO layer in one pass (fno_layer_f32): act(W2 gelu(W1 y1 + b1) +
+    b2 + mlp_skip(x)) with y1 = act(SpectralConv(x) + skip(x)); the MLP
+    products on bf16-rounded operands (the autocast forward)."""
+    _require_gpu(x, weight, bias, skip_weight, w1, w2, gate_weight)
+    lib = nat.load()
+    x = _f32(x)
+    weight = _c64(weight)
+    B, C, *S = x.shape
+    nd = len(S)
+    hidden = w1.shape[0]
+    y = torch.empty((B, C, *S), dtype=torch.float32, device=x.device)
+    flat = [(_f32(t.reshape(-1)) if t is not None else None)
+            for t in (bias, skip_weight, w1, b1, w2, b2, gate_weight, gate_bias)]
+    b, sw, w1f, b1f, w2f, b2f, gw, gb = flat
+    sz, md = nat.i32_array(S), nat.i32_array(modes)
+    wsb = lib.fno_spectral_block_workspace_bytes(B, C, C, nd, sz, md)
+    ws = _workspace(wsb, x.device)
+    nat.check(lib.fno_layer_f32(_ptr(x), _ptr(weight), _ptr(b), _ptr(sw), _ptr(w1f), _ptr(b1f),
+                                _ptr(w2f), _ptr(b2f), _ptr(gw), _ptr(gb), _ptr(y), B, C, hidden, nd,
+                                sz, md, nat.NORMS[fft_norm], skip_kind, mlp_skip_kind, act,
+                                _ptr(ws), wsb, _stream(x.device)),
+              "fno_layer_f32")
+    return y

@@ -1265,6 +1265,77 @@ def test_channel_mlp_bf16_products(Ci, Ch, Co, P, skip, cuda_device):
     assert rel_err(y, refs[1]) <= 2e-2
 
 
+_LAYER_CASES = [
+    # (B, H, W, n_modes, block skip, MLP skip, activation)
+    (2, 256, 256, (64, 64), "linear", "soft-gating", True),      # a layer of the bf16 FNO
+    (2, 256, 256, (64, 64), "linear", "soft-gating", False),     # its last layer
+    (3, 128, 128, (32, 32), "linear", "identity", True),
+    (2, 128, 128, (32, 32), "soft-gating", "none", True),
+    (3, 64, 128, (16, 16), "identity", "soft-gating", True),
+    (2, 64, 128, (16, 16), "linear", "none", False),
+    (2, 48, 256, (20, 22), "soft-gating", "identity", True),     # one k-step of row bins
+]
+
+
+@pytest.mark.parametrize("B,H,W,nm,skip,gate,act", _LAYER_CASES)
+def test_fused_fno_layer(B, H, W, nm, skip, gate, act, cuda_device):
+    """One-pass FNO layer (fno_layer_f32: spectral block + skip + GELU +
+    channel MLP 64 -> 32 -> 64 with bf16 products + MLP skip + GELU,
+    fno_block.py:331-379) against the composed kernels (the block, then the
+    bf16-product channel MLP) and against the bf16-rounding oracle layer."""
+    print(f"fno layer B{B} {H}x{W} {nm} skip={skip} gate={gate} act={act}", flush=True)
+    C, Ch = 64, 32
+    torch.manual_seed(41)
+    conv = na.SpectralConv(C, C, nm).to(cuda_device)
+    with torch.no_grad():
+        conv.bias.normal_(0, 0.1)
+    kept, sl = conv.window([H, W])
+    wwin = conv.dense_window_weight(sl).detach()
+    g = torch.Generator().manual_seed(42)
+    kinds = {"linear": nat.SKIP_LINEAR, "soft-gating": nat.SKIP_SOFT_GATING,
+             "identity": nat.SKIP_IDENTITY, "none": nat.SKIP_NONE}
+    ws = {"linear": torch.randn(C, C, generator=g) / 8, "soft-gating": torch.rand(C, generator=g) + 0.5,
+          "identity": None}[skip]
+    w1, b1 = torch.randn(Ch, C, generator=g) / 8, torch.randn(Ch, generator=g) / 4
+    w2, b2 = torch.randn(C, Ch, generator=g) / 6, torch.randn(C, generator=g) / 4
+    gw, gb = torch.rand(C, generator=g) + 0.5, torch.randn(C, generator=g) / 4
+    x = gaussian_random_field((B, C, H, W), seed=43)
+    dev = lambda t: None if t is None else t.to(cuda_device)
+    a = nat.ACT_GELU if act else nat.ACT_NONE
+    gkind = kinds[gate]
+    gwt, gbt = (gw, gb) if gate == "soft-gating" else (None, None)
+    assert Fh.layer_is_fused(B, C, Ch, [H, W], kept, kinds[skip], gkind)
+    bias = conv.bias.detach().reshape(-1)
+    with torch.no_grad():
+        y = Fh.fno_layer(dev(x), wwin, bias, kept, kinds[skip], dev(ws), dev(w1), dev(b1), dev(w2),
+                         dev(b2), gkind, dev(gwt), dev(gbt), a)
+        y1 = Fh.spectral_block(dev(x), wwin, bias, kept, kinds[skip], dev(ws), a)
+        yc = Fh.channel_mlp(y1, dev(w1), dev(b1), dev(w2), dev(b2), gkind,
+                            dev(x) if gate != "none" else None, dev(gwt), dev(gbt), a,
+                            bf16_products=True)
+    torch.cuda.synchronize()
+    err_c = rel_err(y, yc)
+    if skip == "linear":
+        skip_d = {"type": "linear", "w": ws.double()}
+    elif skip == "soft-gating":
+        skip_d = {"type": "soft-gating", "w": ws.double().view(1, C, 1, 1)}
+    else:
+        skip_d = {"type": "identity"}
+    gate_d = {"soft-gating": {"type": "soft-gating", "w": gw.double().view(1, C, 1, 1),
+                              "b": gb.double().view(1, C, 1, 1)},
+              "identity": {"type": "identity"}, "none": None}[gate]
+    convd = dict(weight=conv.weight.to_tensor().detach().cpu().to(torch.complex128),
+                 bias=conv.bias.detach().cpu().double(), n_modes=conv.n_modes,
+                 max_n_modes=conv.max_n_modes)
+    mlpd = {"weights": [w1.double(), w2.double()], "biases": [b1.double(), b2.double()]}
+    ref = R.fno_block_forward(x.double(), 0 if act else 1, 2, convd, skip_d, mlpd, gate_d,
+                              bf16_products=True)
+    err = rel_err(y, ref)
+    print(f"  vs composed {err_c:.2e}, vs rounded oracle {err:.2e}", flush=True)
+    assert err_c <= 2e-3
+    assert err <= 2e-2
+
+
 def test_fno_autocast_bf16(cuda_device):
     """FNO forward under torch.autocast(dtype=bfloat16): lifting, block and
     projection MLPs take the bf16-product kernel, the spectral path stays
