@@ -147,6 +147,29 @@ size_t fno_ifft_window_workspace_bytes(int64_t planes, int32_t ndim, const int32
                                        const int32_t* modes);
 
 /*
+ * Inverse window transform with the bias, skip and activation, output on the
+ * input grid:  y = act(irfft(yhat) + bias + skip(x)).  Replaces the inverse
+ * of SpectralConv.forward (ifftshift, ifftn over the non-last axes, Hermitian
+ * fix-up, irfft, bias: spectral_convolution.py:531-568) followed by the skip
+ * add and first activation of FNOBlocks.forward_with_postactivation
+ * (fno_block.py:331-361, skips of skip_connections.py:88-130).
+ *   yhat  complex64 [batch, out_channels, m_1..m_ndim] window order
+ *   x     float32 [batch, in_channels, N_1..N_ndim] (NULL without a skip);
+ *         y float32 [batch, out_channels, N_1..N_ndim], not overlapping x
+ * Lines of 64 points with at most 15 kept bins and 32 / 64 channels take the
+ * last axis, bias, skip and activation in one pass over the non-last
+ * transforms' output (the spectral field never reaches memory); other shapes
+ * run fno_irfft_window_f32 then fno_block_epilogue_f32.  Workspace:
+ * fno_irfft_window_workspace_bytes(batch * out_channels, ndim, sizes, modes).
+ */
+int fno_irfft_window_epilogue_f32(const void* yhat, const float* bias, const float* x,
+                                  const float* skip_weight, float* y, int32_t batch,
+                                  int32_t in_channels, int32_t out_channels, int32_t ndim,
+                                  const int32_t* sizes, const int32_t* modes, int32_t norm,
+                                  int32_t skip_kind, int32_t act, void* workspace,
+                                  size_t workspace_bytes, void* stream);
+
+/*
  * Block epilogue: y = act(spec + skip(x)).  Replaces the skip, add and first
  * activation of FNOBlocks.forward_with_postactivation, fno_block.py:331-361,
  * with the skips of skip_connections.py:88-130.  spec may alias y.

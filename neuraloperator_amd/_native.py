@@ -56,6 +56,9 @@ _SIGNATURES = {
                                      _c_i64, _c_i32, _c_i32, _c_i32, _c_i64, _c_i32, _c_i32, _c_i32,
                                      _c_vp]),
     "fno_channel_mlp_is_supported": (_c_i32, [_c_i32, _c_i32, _c_i32, _c_i64]),
+    "fno_irfft_window_epilogue_f32": (_c_i32, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i32, _c_i32,
+                                               _c_i32, _c_i32, _c_i32p, _c_i32p, _c_i32, _c_i32,
+                                               _c_i32, _c_vp, _c_size, _c_vp]),
     "fno_layer_is_fused": (_c_i32, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32p, _c_i32p, _c_i32,
                                     _c_i32]),
     "fno_layer_f32": (_c_i32, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,

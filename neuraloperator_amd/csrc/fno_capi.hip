@@ -32,6 +32,10 @@ int contract_separable(const float2* X, const float2* W, float2* Y, int B, int C
                        hipStream_t st);
 int axis_matmul(const float2* in, const float2* mat, float2* out, int64_t outer, int A, int J,
                 int64_t inner, hipStream_t st);
+int irfft_epilogue(const float2* yhat, const float* bias, const float* x, const float* skip_w,
+                   float* y, int B, int Ci, int Co, int32_t ndim, const int32_t* sizes,
+                   const int32_t* modes, int32_t norm, int32_t skip_kind, int32_t act, void* ws,
+                   size_t ws_bytes, hipStream_t st);
 int block_epilogue(const float* spec, const float* x, const float* ws, float* y, int B, int Ci,
                    int Co, int64_t P, int skip_kind, int act, hipStream_t st);
 bool channel_mlp_supported(int Ci, int Ch, int Co, int64_t P);
@@ -53,6 +57,11 @@ int fast2d_block(const float* x, const float2* w, const float* bias, const float
                  const LayerMlp* mlp = nullptr);
 bool rowsynth_mlp_covers(int H, int W, int Ci, int Co, int m1, int m2h, int hidden,
                          int skip_kind);
+bool tucker_fused_supported(int B, int Ci, int Co, int ndim, const int32_t* modes,
+                            const int32_t* ranks);
+int tucker_fused(const float2* X, const float2* core, const float2* const* factors,
+                 const int32_t* ranks, float2* Y, int B, int Ci, int Co, int ndim,
+                 const int32_t* modes, float2* Kbuf, hipStream_t st);
 }  // namespace fno
 
 using namespace fno;
@@ -181,6 +190,13 @@ int fno_contract_tucker_c64(const void* xhat, const void* core, const void* cons
   int64_t big = (int64_t)rin * rout;
   for (int d = 0; d < ndim; ++d) big *= (modes[d] > ranks[2 + d] ? modes[d] : ranks[2 + d]);
   float2* Kt = reinterpret_cast<float2*>(workspace);
+  // two launches (mode factors into the core, then the mode-wise products)
+  // where their LDS stages fit; the chain of one launch per factor otherwise
+  if (tucker_fused_supported(batch, in_channels, out_channels, ndim, modes, ranks))
+    return tucker_fused(reinterpret_cast<const float2*>(xhat), reinterpret_cast<const float2*>(core),
+                        reinterpret_cast<const float2* const*>(factors), ranks,
+                        reinterpret_cast<float2*>(yhat), batch, in_channels, out_channels, ndim,
+                        modes, Kt, st);
   float2* e1 = Kt + (int64_t)rin * rout * M;
   float2* e2 = e1 + big;
   float2* t1 = e2 + big;
@@ -314,6 +330,35 @@ int fno_ifft_window_c64(const void* yhat, const float* bias, void* y, int64_t ba
   return ifft_window_c2c(reinterpret_cast<const float2*>(yhat), bias, reinterpret_cast<float2*>(y),
                          batch, channels, ndim, in_sizes, out_sizes, modes, norm, workspace,
                          workspace_bytes, reinterpret_cast<hipStream_t>(stream));
+}
+
+int fno_irfft_window_epilogue_f32(const void* yhat, const float* bias, const float* x,
+                                  const float* skip_weight, float* y, int32_t batch,
+                                  int32_t in_channels, int32_t out_channels, int32_t ndim,
+                                  const int32_t* sizes, const int32_t* modes, int32_t norm,
+                                  int32_t skip_kind, int32_t act, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  clear_error();
+  FNO_CHECK_ARG(yhat && y, "yhat/y must not be NULL");
+  FNO_CHECK_ARG(skip_kind == FNO_SKIP_NONE || x, "x must not be NULL with a skip");
+  FNO_CHECK_ARG(batch >= 1 && in_channels >= 1 && out_channels >= 1, "bad batch/channels");
+  int rc = validate_window(ndim, sizes, modes);
+  if (rc) return rc;
+  const int64_t cmax = in_channels > out_channels ? in_channels : out_channels;
+  const int64_t elems = bounded_elems((int64_t)batch * cmax, ndim, sizes);
+  FNO_CHECK_ARG(elems > 0, "batch x channels x sizes exceeds %lld elements", (long long)kMaxElems);
+  const int64_t points = elems / ((int64_t)batch * cmax);
+  FNO_CHECK_ARG(skip_kind == FNO_SKIP_NONE ||
+                    !ranges_overlap(x, (size_t)batch * in_channels * points * sizeof(float), y,
+                                    (size_t)batch * out_channels * points * sizeof(float)),
+                "inverse + epilogue: y must not overlap x");
+  rc = check_norm(norm);
+  if (rc) return rc;
+  rc = check_skip(skip_kind, act, in_channels, out_channels, skip_weight);
+  if (rc) return rc;
+  return irfft_epilogue(reinterpret_cast<const float2*>(yhat), bias, x, skip_weight, y, batch,
+                        in_channels, out_channels, ndim, sizes, modes, norm, skip_kind, act,
+                        workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
 }
 
 int fno_block_epilogue_f32(const float* spec, const float* x, const float* skip_weight, float* y,
@@ -468,14 +513,10 @@ int spectral_block_run(const float* x, const void* w, const float* bias, const f
   rc = contract_dense(xhat, reinterpret_cast<const float2*>(w), yhat, batch, in_channels,
                       out_channels, M, (int64_t)out_channels * M, M, 1, st);
   if (rc) return rc;
-  rc = irfft_window(yhat, bias, y, batch, out_channels, ndim, sizes, sizes, modes, norm, 1, rest,
-                    rest_bytes, st);
-  if (rc) return rc;
-  int64_t P = 1;
-  for (int d = 0; d < ndim; ++d) P *= sizes[d];
-  if (skip_kind == FNO_SKIP_NONE && act == FNO_ACT_NONE) return FNO_OK;
-  return block_epilogue(y, x, skip_weight, y, batch, in_channels, out_channels, P, skip_kind, act,
-                        st);
+  // inverse + bias + skip + activation (one pass over the last axis where
+  // the line epilogue covers it)
+  return irfft_epilogue(yhat, bias, x, skip_weight, y, batch, in_channels, out_channels, ndim,
+                        sizes, modes, norm, skip_kind, act, rest, rest_bytes, st);
 }
 
 }  // namespace fno

@@ -1008,19 +1008,13 @@ size_t ifft_window_c2c_ws(int64_t planes, int32_t ndim, const int32_t* out_sizes
          sizeof(float2);
 }
 
-int irfft_window(const float2* yhat, const float* bias, float* y, int64_t batch, int32_t channels,
-                 int32_t ndim, const int32_t* in_sizes, const int32_t* out_sizes,
-                 const int32_t* modes, int32_t norm, int32_t enforce, void* ws, size_t ws_bytes,
-                 hipStream_t st) {
-  const int64_t planes = batch * channels;
-  const double scale = inverse_scale(norm, out_sizes, ndim);
-  // stage d (d < ndim-1) expands axis d to out_sizes[d] into bufs[d % 2]
-  const int64_t eb = inv_buffer_elems(planes, ndim, out_sizes, modes);
-  const size_t need = (size_t)stage_buffers(ndim) * eb * sizeof(float2);
-  if (ws_bytes < need) {
-    set_error("irfft_window: workspace %zu < %zu bytes", ws_bytes, need);
-    return FNO_ERR_WORKSPACE;
-  }
+// The inverse transforms of every axis but the last (unscaled), from the
+// window spectrum into the workspace's stage buffers (eb elements each):
+// *out ends as [planes][out_0 .. out_{ndim-2}][m_last] (yhat itself in 1D).
+static int inverse_nonlast(const float2* yhat, int64_t planes, int32_t ndim,
+                           const int32_t* in_sizes, const int32_t* out_sizes,
+                           const int32_t* modes, void* ws, int64_t eb, const float2** out,
+                           hipStream_t st) {
   float2* bufs[2] = {reinterpret_cast<float2*>(ws), reinterpret_cast<float2*>(ws) + eb};
   const float2* src = yhat;
   for (int d = 0; d < ndim - 1; ++d) {
@@ -1034,6 +1028,26 @@ int irfft_window(const float2* yhat, const float* bias, float* y, int64_t batch,
     if (rc) return rc;
     src = dst;
   }
+  *out = src;
+  return FNO_OK;
+}
+
+int irfft_window(const float2* yhat, const float* bias, float* y, int64_t batch, int32_t channels,
+                 int32_t ndim, const int32_t* in_sizes, const int32_t* out_sizes,
+                 const int32_t* modes, int32_t norm, int32_t enforce, void* ws, size_t ws_bytes,
+                 hipStream_t st) {
+  const int64_t planes = batch * channels;
+  const double scale = inverse_scale(norm, out_sizes, ndim);
+  // stage d (d < ndim-1) expands axis d to out_sizes[d] into bufs[d % 2]
+  const int64_t eb = inv_buffer_elems(planes, ndim, out_sizes, modes);
+  const size_t need = (size_t)stage_buffers(ndim) * eb * sizeof(float2);
+  if (ws_bytes < need) {
+    set_error("irfft_window: workspace %zu < %zu bytes", ws_bytes, need);
+    return FNO_ERR_WORKSPACE;
+  }
+  const float2* src = yhat;
+  int rc0 = inverse_nonlast(yhat, planes, ndim, in_sizes, out_sizes, modes, ws, eb, &src, st);
+  if (rc0) return rc0;
   {
     int64_t rows = planes;
     for (int a = 0; a < ndim - 1; ++a) rows *= out_sizes[a];
@@ -1077,6 +1091,49 @@ int irfft_window(const float2* yhat, const float* bias, float* y, int64_t batch,
     }
   }
   return FNO_OK;
+}
+
+bool line_epilogue_supported(int W, int Ci, int Co, int m2h, int skip_kind);
+int line_epilogue(const float2* z, const float* x, const float* skip_w, const float* bias,
+                  float* y, int B, int Ci, int Co, int64_t L, int m2h, int skip_kind, int act,
+                  float scale, hipStream_t st);
+int block_epilogue(const float* spec, const float* x, const float* ws, float* y, int B, int Ci,
+                   int Co, int64_t P, int skip_kind, int act, hipStream_t st);
+
+// The inverse window transform (output on the input grid) with the bias, the
+// skip and the activation: y = act(irfft(yhat) + bias + skip(x)).  Lines the
+// line epilogue covers take the last axis, bias, skip and activation in one
+// kernel from the non-last stages' output (no spectral field in memory);
+// otherwise the inverse transform writes y and the block epilogue finishes it
+// in place.  Workspace: irfft_window_ws(batch * out_channels, ...).
+int irfft_epilogue(const float2* yhat, const float* bias, const float* x, const float* skip_w,
+                   float* y, int B, int Ci, int Co, int32_t ndim, const int32_t* sizes,
+                   const int32_t* modes, int32_t norm, int32_t skip_kind, int32_t act, void* ws,
+                   size_t ws_bytes, hipStream_t st) {
+  const int64_t planes = (int64_t)B * Co;
+  const int W = sizes[ndim - 1], m2h = modes[ndim - 1];
+  const bool aligned = (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) % 16 == 0;
+  if (aligned && line_epilogue_supported(W, Ci, Co, m2h, skip_kind)) {
+    const int64_t eb = inv_buffer_elems(planes, ndim, sizes, modes);
+    const size_t need = (size_t)stage_buffers(ndim) * eb * sizeof(float2);
+    if (ws_bytes < need) {
+      set_error("inverse + epilogue: workspace %zu < %zu bytes", ws_bytes, need);
+      return FNO_ERR_WORKSPACE;
+    }
+    const float2* z = yhat;
+    int rc = inverse_nonlast(yhat, planes, ndim, sizes, sizes, modes, ws, eb, &z, st);
+    if (rc) return rc;
+    int64_t L = 1;
+    for (int d = 0; d + 1 < ndim; ++d) L *= sizes[d];
+    return line_epilogue(z, x, skip_w, bias, y, B, Ci, Co, L, m2h, skip_kind, act,
+                         (float)inverse_scale(norm, sizes, ndim), st);
+  }
+  int rc = irfft_window(yhat, bias, y, B, Co, ndim, sizes, sizes, modes, norm, 1, ws, ws_bytes, st);
+  if (rc) return rc;
+  if (skip_kind == FNO_SKIP_NONE && act == FNO_ACT_NONE) return FNO_OK;
+  int64_t P = 1;
+  for (int d = 0; d < ndim; ++d) P *= sizes[d];
+  return block_epilogue(y, x, skip_w, y, B, Ci, Co, P, skip_kind, act, st);
 }
 
 bool contract_mfma_supported(int B, int Ci, int Co, int64_t M, int64_t sWi, int64_t sWo,

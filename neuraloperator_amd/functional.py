@@ -133,6 +133,32 @@ def irfft_window(yhat: torch.Tensor, in_sizes: Sequence[int], out_sizes: Sequenc
     return y
 
 
+def irfft_window_epilogue(yhat: torch.Tensor, sizes: Sequence[int], bias: Optional[torch.Tensor],
+                          x: Optional[torch.Tensor], skip_kind: int,
+                          skip_weight: Optional[torch.Tensor], act: int,
+                          fft_norm: str = "forward") -> torch.Tensor:
+    """act(irfft(yhat) + bias + skip(x)) on the input grid (see
+    fno_irfft_window_epilogue_f32)."""
+    _require_gpu(yhat, bias, x, skip_weight)
+    lib = nat.load()
+    yhat = _c64(yhat)
+    B, Co, *modes = yhat.shape
+    nd = len(modes)
+    xx = _f32(x) if x is not None else None
+    Ci = xx.shape[1] if xx is not None else Co
+    y = torch.empty((B, Co, *sizes), dtype=torch.float32, device=yhat.device)
+    b = _f32(bias.reshape(-1)) if bias is not None else None
+    w = _f32(skip_weight.reshape(-1)) if skip_weight is not None else None
+    sz, md = nat.i32_array(sizes), nat.i32_array(modes)
+    wsb = lib.fno_irfft_window_workspace_bytes(B * Co, nd, sz, md)
+    ws = _workspace(wsb, yhat.device)
+    nat.check(lib.fno_irfft_window_epilogue_f32(_ptr(yhat), _ptr(b), _ptr(xx), _ptr(w), _ptr(y), B,
+                                                Ci, Co, nd, sz, md, nat.NORMS[fft_norm], skip_kind,
+                                                act, _ptr(ws), wsb, _stream(yhat.device)),
+              "fno_irfft_window_epilogue_f32")
+    return y
+
+
 def fft_window(x: torch.Tensor, modes: Sequence[int], fft_norm: str = "forward") -> torch.Tensor:
     """Kept-mode window of fftn(x) for complex data (see fno_fft_window_c64).
     x complex [B, C, *S] -> complex64 [B, C, *modes]."""

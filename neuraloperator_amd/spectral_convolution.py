@@ -566,11 +566,16 @@ class SpectralConv(BaseSpectralConv):
         else:
             w = self.dense_window_weight(sl).detach()
             yhat = Fh.contract_dense(xhat, w, separable=self.separable)
-        y = Fh.irfft_window(yhat, sizes, out_sizes, None if bias is None else bias.detach(),
-                            self.fft_norm, self.enforce_hermitian_symmetry)
+        b = None if bias is None else bias.detach()
         if skip_kind != nat.SKIP_NONE or act != nat.ACT_NONE:
             if not same_size:
                 raise RuntimeError("fused skip requires output size == input size")
-            y = Fh.block_epilogue(y, x.detach(), skip_kind,
-                                  None if skip_weight is None else skip_weight.detach(), act)
+            # inverse, bias, skip and activation in one call (on the input
+            # grid the Hermitian fix-up is implied by the real inverse)
+            y = Fh.irfft_window_epilogue(yhat, sizes, b, x.detach(), skip_kind,
+                                         None if skip_weight is None else skip_weight.detach(),
+                                         act, self.fft_norm)
+        else:
+            y = Fh.irfft_window(yhat, sizes, out_sizes, b, self.fft_norm,
+                                self.enforce_hermitian_symmetry)
         return _attach(y, x, *params)

@@ -1336,6 +1336,81 @@ def test_fused_fno_layer(B, H, W, nm, skip, gate, act, cuda_device):
     assert err <= 2e-2
 
 
+_EPI_CASES = [
+    # (B, Ci, Co, sizes, window, skip, act); lines of 64 with <= 15 bins and
+    # 32 / 64 channels take the one-pass line epilogue, the rest the composed path
+    (2, 32, 32, (16, 16, 64), (8, 8, 9), "linear", True),
+    (2, 64, 32, (32, 64), (16, 15), "linear", True),
+    (2, 32, 64, (8, 12, 64), (4, 6, 12), "linear", False),
+    (2, 32, 32, (24, 64), (12, 9), "soft-gating", False),
+    (3, 64, 64, (64,), (9,), "identity", True),
+    (2, 32, 32, (8, 64), (8, 5), "none", True),
+    (2, 48, 40, (16, 64), (8, 9), "linear", True),      # 40 channels: composed
+    (2, 32, 32, (16, 32), (8, 9), "linear", True),      # 32-point lines: composed
+    (2, 32, 32, (16, 64), (8, 20), "linear", True),     # 20 bins: composed
+]
+
+
+@pytest.mark.parametrize("B,Ci,Co,S,m,skip,act", _EPI_CASES)
+@pytest.mark.parametrize("norm", ["forward", "ortho"])
+def test_irfft_window_epilogue(B, Ci, Co, S, m, skip, act, norm, cuda_device):
+    """fno_irfft_window_epilogue_f32 (inverse + bias + skip + activation in
+    one call) against the same steps as separate calls: fno_irfft_window_f32
+    then fno_block_epilogue_f32."""
+    print(f"irfft+epilogue B{B} {Ci}->{Co} {S} {m} {skip} act={act} {norm}", flush=True)
+    g = torch.Generator().manual_seed(51)
+    yhat = torch.complex(torch.randn(B, Co, *m, generator=g), torch.randn(B, Co, *m, generator=g))
+    x = torch.randn(B, Ci, *S, generator=g)
+    kind = {"linear": nat.SKIP_LINEAR, "soft-gating": nat.SKIP_SOFT_GATING,
+            "identity": nat.SKIP_IDENTITY, "none": nat.SKIP_NONE}[skip]
+    ws = {"linear": torch.randn(Co, Ci, generator=g) / Ci ** 0.5,
+          "soft-gating": torch.rand(Co, generator=g) + 0.5}.get(skip)
+    bias = torch.randn(Co, generator=g)
+    a = nat.ACT_GELU if act else nat.ACT_NONE
+    dev = lambda t: None if t is None else t.to(cuda_device)
+    with torch.no_grad():
+        y = Fh.irfft_window_epilogue(dev(yhat), list(S), dev(bias), dev(x), kind, dev(ws), a, norm)
+        ref = Fh.irfft_window(dev(yhat), list(S), list(S), dev(bias), norm)
+        ref = Fh.block_epilogue(ref, dev(x), kind, dev(ws), a)
+    torch.cuda.synchronize()
+    assert rel_err(y, ref) <= TOL
+
+
+@pytest.mark.parametrize("S,nm,skip", [((16, 16, 64), (8, 8, 16), "linear"),
+                                       ((32, 64), (16, 16), "soft-gating"),
+                                       ((12, 64), (12, 20), "identity")])
+def test_block_with_line_epilogue_matches_oracle(S, nm, skip, cuda_device):
+    """Spectral blocks whose last axis is a 64-point line (the generic path's
+    one-pass line epilogue), dense weight, skip + GELU, against the float64
+    oracle."""
+    print(f"block with line epilogue {S} {nm} {skip}", flush=True)
+    torch.manual_seed(52)
+    C, B = 32, 2
+    conv = na.SpectralConv(C, C, nm).to(cuda_device)
+    with torch.no_grad():
+        conv.bias.normal_(0, 0.1)
+    g = torch.Generator().manual_seed(53)
+    x = torch.randn(B, C, *S, generator=g)
+    kind = {"linear": nat.SKIP_LINEAR, "soft-gating": nat.SKIP_SOFT_GATING,
+            "identity": nat.SKIP_IDENTITY}[skip]
+    ws = {"linear": torch.randn(C, C, generator=g) / C ** 0.5,
+          "soft-gating": torch.rand(C, generator=g) + 0.5}.get(skip)
+    with torch.no_grad():
+        y = conv._forward_hip(x.to(cuda_device), None, kind,
+                              None if ws is None else ws.to(cuda_device), nat.ACT_GELU)
+    torch.cuda.synchronize()
+    w = conv.weight.to_tensor().detach().cpu().to(torch.complex128)
+    ref = R.spectral_conv_forward(x.double(), w, conv.bias.detach().cpu().double(), conv.n_modes,
+                                  conv.max_n_modes)
+    if skip == "linear":
+        ref = ref + R.linear_skip(x.double(), ws.double())
+    elif skip == "soft-gating":
+        ref = ref + R.soft_gating(x.double(), ws.double().view(1, C, *([1] * len(S))))
+    else:
+        ref = ref + x.double()
+    assert rel_err(y, R.gelu(ref)) <= TOL
+
+
 def test_fno_autocast_bf16(cuda_device):
     """FNO forward under torch.autocast(dtype=bfloat16): lifting, block and
     projection MLPs take the bf16-product kernel, the spectral path stays
