@@ -790,6 +790,10 @@ int c2c_fft_fwd(const float2* in, float2* out, int64_t outer, int64_t inner, int
 int c2c_fft_inv(const float2* in, float2* out, int64_t outer, int64_t inner, int N, int Np, int m,
                 int off, float scale, hipStream_t st);
 
+bool slab_fwd64_supported(int N1, int N2, int m1, int m2h);
+int slab_fwd64(const float* x, float2* out, int64_t slabs, int m1, int m2h, float scale,
+               hipStream_t st);
+
 int rfft_window(const float* x, float2* xhat, int64_t planes, int32_t ndim, const int32_t* sizes,
                 const int32_t* modes, int32_t norm, void* ws, size_t ws_bytes, hipStream_t st) {
   // stage s transforms axis (ndim-1-s); stage outputs go to the workspace
@@ -803,6 +807,30 @@ int rfft_window(const float* x, float2* xhat, int64_t planes, int32_t ndim, cons
   }
   float2* bufs[2] = {reinterpret_cast<float2*>(ws), reinterpret_cast<float2*>(ws) + eb};
   float2* bufA = bufs[0];
+  // 64 x 64 trailing slabs: the last two axes in one pass (stages 0 and 1,
+  // written where stage 1 writes), then the remaining axes as below
+  if (ndim >= 2 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+      slab_fwd64_supported(sizes[ndim - 2], sizes[ndim - 1], modes[ndim - 2], modes[ndim - 1])) {
+    int64_t slabs = planes;
+    for (int d = 0; d + 2 < ndim; ++d) slabs *= sizes[d];
+    float2* dst = ndim == 2 ? xhat : bufs[1];
+    int rc = slab_fwd64(x, dst, slabs, modes[ndim - 2], modes[ndim - 1],
+                        ndim == 2 ? (float)scale : 1.f, st);
+    if (rc) return rc;
+    const float2* src = dst;
+    for (int d = ndim - 3; d >= 0; --d) {
+      int64_t outer = planes;
+      for (int a = 0; a < d; ++a) outer *= sizes[a];
+      int64_t inner = 1;
+      for (int a = d + 1; a < ndim; ++a) inner *= modes[a];
+      float2* out = (d == 0) ? xhat : bufs[(ndim - 1 - d) % 2];
+      rc = c2c_axis_fwd(src, out, outer, sizes[d], inner, modes[d], -(modes[d] / 2),
+                        d == 0 ? (float)scale : 1.f, st);
+      if (rc) return rc;
+      src = out;
+    }
+    return FNO_OK;
+  }
   // last axis
   {
     const int N = sizes[ndim - 1], m = modes[ndim - 1];

@@ -1,0 +1,190 @@
+// Forward window transform of the last two axes of 64 x 64 slabs in one pass:
+//
+//   X[k1, k2] = s sum_{d1, d2} x[d1, d2] e^{-2 pi i ((k1 - m1/2) d1 + k2 d2) / 64},
+//               k1 < m1 <= 16 (window rows of the next-to-last axis, centred),
+//               k2 < m2h <= 16 (rfft bins of the last axis),
+//
+// the first two stages of the window transform (torch.fft.rfftn + fftshift +
+// window slice over those two axes, neuralop/layers/spectral_convolution.py
+// :443-449, :500-521), so the last-axis spectrum of the whole field never
+// goes through memory.  One wave per slab, two products on
+// v_mfma_f32_16x16x32_bf16 (three-term bf16 splits, fp32 accumulation):
+//   1. A1[d1, c] = sum_d2 x[d1, d2] F[d2, c]: columns c < 16 the real parts
+//      (cos) of bins c, columns 16 + c the imaginary parts (-sin), so a
+//      lane's two column tiles hold Re and Im of the same bin;
+//   2. [Xr; Xi][k1, k2] = sum over (d1, part) of A2 . A1: the accumulators
+//      of step 1 are the B operand as they stand, K slot (G, i) of k-step ks
+//      being row d1 = 16 ks + 4 G + i % 4 of part i / 4 (Re / Im), and A2 the
+//      window's twiddles (cos / sin) in that slot order, scaled by s.
+// The twiddle fragments of both products are built once per workgroup in LDS.
+#include "fno_common.h"
+#include "fno_twiddle.h"
+
+namespace fno {
+
+namespace sl {
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+constexpr int kN = 64, kWaves = 4, kThreads = 64 * kWaves;
+struct bf2 {
+  __bf16 hi, lo;
+};
+__device__ __forceinline__ bf2 split(float v) {
+  const __bf16 h = (__bf16)v;
+  return {h, (__bf16)(v - (float)h)};
+}
+__device__ __forceinline__ v4f mma3(v8bf ah, v8bf al, v8bf bh, v8bf bl, v4f acc) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
+}
+}  // namespace sl
+
+__global__ void __launch_bounds__(sl::kThreads)
+k_slab_fwd64(const float* __restrict__ x, float2* __restrict__ out, int64_t slabs, int m1,
+             int m2h, float scale) {
+  using namespace sl;
+  // F fragments [ks 2][nt 2][hi|lo][64]; A2 fragments [rt 2][ks 4][hi|lo][64]
+  __shared__ v8bf ff[2 * 2 * 2 * 64];
+  __shared__ v8bf af[2 * 4 * 2 * 64];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int G = lane >> 4, n = lane & 15;
+  for (int f = tid; f < 2 * 2 * 64; f += kThreads) {
+    const int ln = f & 63, nt = (f >> 6) & 1, ks = f >> 7;
+    const int c = ln & 15, g = ln >> 4;
+    v8bf h, l;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int d2 = 32 * ks + 8 * g + i;
+      float v = 0.f;
+      if (c < m2h) {
+        const float2 t = twiddle_any((c * d2) & (kN - 1), kN);
+        v = nt ? -t.y : t.x;
+      }
+      const bf2 q = split(v);
+      h[i] = q.hi;
+      l[i] = q.lo;
+    }
+    ff[((ks * 2 + nt) * 2) * 64 + ln] = h;
+    ff[((ks * 2 + nt) * 2 + 1) * 64 + ln] = l;
+  }
+  for (int f = tid; f < 2 * 4 * 64; f += kThreads) {
+    const int ln = f & 63, ks = (f >> 6) & 3, rt = f >> 8;
+    const int k1 = ln & 15, g = ln >> 4;
+    v8bf h, l;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int d1 = 16 * ks + 4 * g + (i & 3), part = i >> 2;
+      float v = 0.f;
+      if (k1 < m1) {
+        // e^{-i theta} (a + i b): Re = cos a + sin b, Im = cos b - sin a
+        const int f1 = k1 - m1 / 2;
+        const float2 t = twiddle_any(((f1 * d1) % kN + kN) % kN, kN);
+        v = rt == 0 ? (part == 0 ? t.x : t.y) : (part == 0 ? -t.y : t.x);
+        v *= scale;
+      }
+      const bf2 q = split(v);
+      h[i] = q.hi;
+      l[i] = q.lo;
+    }
+    af[((rt * 4 + ks) * 2) * 64 + ln] = h;
+    af[((rt * 4 + ks) * 2 + 1) * 64 + ln] = l;
+  }
+  __syncthreads();
+
+  const int64_t nwaves = (int64_t)gridDim.x * kWaves;
+#pragma unroll 1
+  for (int64_t s = (int64_t)blockIdx.x * kWaves + (tid >> 6); s < slabs; s += nwaves) {
+    // rows 16 mt + m of the slab, columns 32 ks + 8 G .. + 7
+    const float* xs = x + s * (kN * kN);
+    float4 xv[4][2][2];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const float* p = xs + (16 * mt + n) * kN + 32 * ks + 8 * G;
+        xv[mt][ks][0] = *reinterpret_cast<const float4*>(p);
+        xv[mt][ks][1] = *reinterpret_cast<const float4*>(p + 4);
+      }
+    v4f a1[4][2];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      a1[mt][0] = (v4f)0.f;
+      a1[mt][1] = (v4f)0.f;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const float v[8] = {xv[mt][ks][0].x, xv[mt][ks][0].y, xv[mt][ks][0].z, xv[mt][ks][0].w,
+                            xv[mt][ks][1].x, xv[mt][ks][1].y, xv[mt][ks][1].z, xv[mt][ks][1].w};
+        v8bf ah, al;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const bf2 q = split(v[i]);
+          ah[i] = q.hi;
+          al[i] = q.lo;
+        }
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+          a1[mt][nt] = mma3(ah, al, ff[((ks * 2 + nt) * 2) * 64 + lane],
+                            ff[((ks * 2 + nt) * 2 + 1) * 64 + lane], a1[mt][nt]);
+      }
+    }
+    // step 2: k-step ks of the window product is row tile ks of step 1
+    v4f a2[2] = {(v4f)0.f, (v4f)0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      v8bf bh, bl;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const bf2 q = split(a1[ks][i >> 2][i & 3]);
+        bh[i] = q.hi;
+        bl[i] = q.lo;
+      }
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+        a2[rt] = mma3(af[((rt * 4 + ks) * 2) * 64 + lane], af[((rt * 4 + ks) * 2 + 1) * 64 + lane],
+                      bh, bl, a2[rt]);
+    }
+    // row k1 = 4 G + r, column k2 = n of both tiles
+    float2* os = out + s * m1 * m2h;
+    if (n < m2h) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int k1 = 4 * G + r;
+        if (k1 < m1) os[k1 * m2h + n] = make_float2(a2[0][r], a2[1][r]);
+      }
+    }
+  }
+}
+
+// ============================================================== host side
+bool slab_fwd64_supported(int N1, int N2, int m1, int m2h) {
+  return N1 == sl::kN && N2 == sl::kN && m1 >= 1 && m1 <= 16 && m2h >= 1 && m2h <= 16;
+}
+
+// slabs of 64 x 64 floats at x (16-byte aligned) -> [slabs][m1][m2h] window
+static int slab_cus() {
+  static int cus = 0;
+  if (!cus) {
+    int dev = 0, n = 0;
+    cus = (hipGetDevice(&dev) == hipSuccess &&
+           hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+           n > 0)
+              ? n
+              : 256;
+  }
+  return cus;
+}
+
+int slab_fwd64(const float* x, float2* out, int64_t slabs, int m1, int m2h, float scale,
+               hipStream_t st) {
+  // as many workgroups as are resident at once (two per CU by registers);
+  // the waves loop over the slabs, so each workgroup builds its twiddle
+  // fragments once
+  int64_t grid = (slabs + sl::kWaves - 1) / sl::kWaves;
+  if (grid > 2 * slab_cus()) grid = 2 * slab_cus();
+  hipLaunchKernelGGL(k_slab_fwd64, dim3((unsigned)grid), dim3(sl::kThreads), 0, st, x, out, slabs,
+                     m1, m2h, scale);
+  return launch_status("k_slab_fwd64");
+}
+
+}  // namespace fno

@@ -1057,6 +1057,28 @@ def test_rfft_window_matrix_core_dft(shape, modes, cuda_device):
     assert rel_err(torch.view_as_real(y), torch.view_as_real(torch.from_numpy(X))) <= TOL
 
 
+@pytest.mark.parametrize("shape,modes", [((2, 3, 64, 64), (16, 9)), ((2, 3, 64, 64), (5, 16)),
+                                         ((1, 4, 8, 64, 64), (4, 16, 16)),
+                                         ((2, 2, 64, 64, 64), (16, 16, 9)),
+                                         ((3, 2, 64, 64), (1, 1)), ((2, 5, 64, 64), (16, 15))])
+@pytest.mark.parametrize("norm", ["forward", "backward", "ortho"])
+def test_rfft_window_slabs(shape, modes, norm, cuda_device):
+    """Trailing 64 x 64 slabs with at most 16 kept rows and bins take both
+    axes in one pass (the slab kernel): the window against float64 numpy
+    (rfftn, centred rows of every non-last axis)."""
+    print(f"rfft window slabs {shape} {modes} {norm}", flush=True)
+    x = torch.randn(*shape, generator=torch.Generator().manual_seed(45))
+    with torch.no_grad():
+        y = Fh.rfft_window(x.to(cuda_device), list(modes), norm)
+    spatial = shape[2:]
+    X = np.fft.rfftn(x.double().numpy(), axes=tuple(range(2, x.ndim)), norm=norm)
+    for d, (n, m) in enumerate(zip(spatial[:-1], modes[:-1])):
+        X = np.fft.fftshift(X, axes=2 + d)
+        X = np.take(X, range(n // 2 - m // 2, n // 2 - m // 2 + m), axis=2 + d)
+    X = X[..., :modes[-1]]
+    assert rel_err(torch.view_as_real(y), torch.view_as_real(torch.from_numpy(X))) <= TOL
+
+
 @pytest.mark.parametrize("B,sizes,nm,out", [(4, (128, 421), (16, 32), None),
                                             (4, (128, 210), (16, 32), (128, 421)),
                                             (512, (421,), (30,), None),
