@@ -930,8 +930,16 @@ static int c2c_axis_fwd(const float2* src, float2* dst, int64_t outer, int N, in
   return launch_status("k_c2c_fwd_direct");
 }
 
+bool axis_inv64_supported(int N, int Np, int m, int64_t inner);
+int axis_inv64(const float2* src, float2* dst, int64_t slabs, int m, int inner, float scale,
+               hipStream_t st);
+
 static int c2c_axis_inv(const float2* src, float2* dst, int64_t outer, int N, int Np, int64_t inner,
                         int m, int off, float sc, hipStream_t st) {
+  // 64-point axis, a window of at most 16 rows (centred: off = -(m / 2)) and
+  // at most 16 columns: one matrix-core product per slab
+  if (off == -(m / 2) && axis_inv64_supported(N, Np, m, inner))
+    return axis_inv64(src, dst, outer, m, (int)inner, sc, st);
   if (inner < 16 && c2c_mfma_ok(outer, inner, m, Np))
     return launch_c2c_mfma<1, 4>(src, dst, outer, inner, N, Np, m, off, sc, st);
   if (c2c_fft_supported(Np, outer, inner))

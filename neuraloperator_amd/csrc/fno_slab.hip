@@ -156,6 +156,78 @@ k_slab_fwd64(const float* __restrict__ x, float2* __restrict__ out, int64_t slab
   }
 }
 
+// ----------------------------------------------------------------------------
+// Inverse along one 64-point axis from a window of m <= 16 rows (frequency
+// j - m/2 at window row j), for inner <= 16 columns:
+//
+//   Z[s, d, c] = t sum_{j < m} U[s, j, c] e^{2 pi i (j - m/2) d / 64}
+//
+// (an ifftn axis of SpectralConv.forward's inverse, spectral_convolution.py
+// :547-548, zero-padded window to the full axis).  One wave per slab s as one
+// product on the matrix cores: rows (d, Re | Im) in row tiles (16 d, part),
+// K = (j, Re | Im of U) against the constant twiddle fragments, columns c.
+// Three-term bf16 splits, fp32 accumulation.
+__global__ void __launch_bounds__(sl::kThreads)
+k_axis_inv64(const float2* __restrict__ src, float2* __restrict__ dst, int64_t slabs, int m,
+             int inner, float scale) {
+  using namespace sl;
+  // A fragments [row tile 8][hi|lo][64]: row tile rt = 2 t + part, rows
+  // d = 16 t + lane % 16; K slot (G, i) = window row 4 G + i / 2, Re / Im of U
+  __shared__ v8bf af[8 * 2 * 64];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int G = lane >> 4, n = lane & 15;
+  for (int f = tid; f < 8 * 64; f += kThreads) {
+    const int ln = f & 63, rt = f >> 6;
+    const int d = 16 * (rt >> 1) + (ln & 15), part = rt & 1, g = ln >> 4;
+    v8bf h, l;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int j = 4 * g + (i >> 1), cu = i & 1;
+      float v = 0.f;
+      if (j < m) {
+        const float2 t = twiddle_any((((j - m / 2) * d) % kN + kN) % kN, kN);
+        // Re Z = cos Ur - sin Ui, Im Z = sin Ur + cos Ui
+        v = part == 0 ? (cu == 0 ? t.x : -t.y) : (cu == 0 ? t.y : t.x);
+        v *= scale;
+      }
+      const bf2 q = split(v);
+      h[i] = q.hi;
+      l[i] = q.lo;
+    }
+    af[(rt * 2) * 64 + ln] = h;
+    af[(rt * 2 + 1) * 64 + ln] = l;
+  }
+  __syncthreads();
+  const int64_t nwaves = (int64_t)gridDim.x * kWaves;
+#pragma unroll 1
+  for (int64_t s = (int64_t)blockIdx.x * kWaves + (tid >> 6); s < slabs; s += nwaves) {
+    // B: lane (G, n) holds U[s, 4 G + i / 2, n] (Re, Im) for i < 8
+    const float2* us = src + s * m * inner;
+    v8bf bh, bl;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int j = 4 * G + q;
+      const float2 uv = (j < m && n < inner) ? us[j * inner + n] : make_float2(0.f, 0.f);
+      const bf2 a = split(uv.x), c = split(uv.y);
+      bh[2 * q] = a.hi;
+      bl[2 * q] = a.lo;
+      bh[2 * q + 1] = c.hi;
+      bl[2 * q + 1] = c.lo;
+    }
+    float2* zs = dst + s * kN * inner;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      v4f re = (v4f)0.f, im = (v4f)0.f;
+      re = mma3(af[((2 * t) * 2) * 64 + lane], af[((2 * t) * 2 + 1) * 64 + lane], bh, bl, re);
+      im = mma3(af[((2 * t + 1) * 2) * 64 + lane], af[((2 * t + 1) * 2 + 1) * 64 + lane], bh, bl, im);
+      if (n < inner) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) zs[(16 * t + 4 * G + r) * inner + n] = make_float2(re[r], im[r]);
+      }
+    }
+  }
+}
+
 // ============================================================== host side
 bool slab_fwd64_supported(int N1, int N2, int m1, int m2h) {
   return N1 == sl::kN && N2 == sl::kN && m1 >= 1 && m1 <= 16 && m2h >= 1 && m2h <= 16;
@@ -185,6 +257,20 @@ int slab_fwd64(const float* x, float2* out, int64_t slabs, int m1, int m2h, floa
   hipLaunchKernelGGL(k_slab_fwd64, dim3((unsigned)grid), dim3(sl::kThreads), 0, st, x, out, slabs,
                      m1, m2h, scale);
   return launch_status("k_slab_fwd64");
+}
+
+bool axis_inv64_supported(int N, int Np, int m, int64_t inner) {
+  return N == sl::kN && Np == sl::kN && m >= 1 && m <= 16 && inner >= 1 && inner <= 16;
+}
+
+// [slabs][m][inner] window -> [slabs][64][inner], scaled by scale
+int axis_inv64(const float2* src, float2* dst, int64_t slabs, int m, int inner, float scale,
+               hipStream_t st) {
+  int64_t grid = (slabs + sl::kWaves - 1) / sl::kWaves;
+  if (grid > 4 * slab_cus()) grid = 4 * slab_cus();
+  hipLaunchKernelGGL(k_axis_inv64, dim3((unsigned)grid), dim3(sl::kThreads), 0, st, src, dst, slabs,
+                     m, inner, scale);
+  return launch_status("k_axis_inv64");
 }
 
 }  // namespace fno

@@ -1370,6 +1370,13 @@ _EPI_CASES = [
     (2, 48, 40, (16, 64), (8, 9), "linear", True),      # 40 channels: composed
     (2, 32, 32, (16, 32), (8, 9), "linear", True),      # 32-point lines: composed
     (2, 32, 32, (16, 64), (8, 20), "linear", True),     # 20 bins: composed
+    # trailing 64 x 64 slabs (the next-to-last axis' inverse on 64-point lines)
+    (2, 32, 32, (4, 64, 64), (4, 16, 9), "linear", True),
+    (2, 64, 32, (64, 64), (16, 9), "linear", True),
+    (2, 32, 32, (64, 64), (8, 15), "soft-gating", False),
+    (2, 32, 32, (3, 64, 64), (3, 12, 5), "identity", True),
+    (2, 32, 32, (64, 64), (16, 9), "none", True),
+    (1, 32, 32, (2, 64, 64), (2, 1, 1), "linear", True),
 ]
 
 
