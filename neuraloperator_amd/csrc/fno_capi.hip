@@ -27,7 +27,7 @@ int irfft_window(const float2* yhat, const float* bias, float* y, int64_t batch,
                  const int32_t* modes, int32_t norm, int32_t enforce, void* ws, size_t ws_bytes,
                  hipStream_t st);
 int contract_dense(const float2* X, const float2* W, float2* Y, int B, int Ci, int Co, int64_t M,
-                   int64_t sWi, int64_t sWo, int64_t sWk, hipStream_t st);
+                   int64_t sWi, int64_t sWo, int64_t sWk, hipStream_t st, int ymap_w = 0);
 int contract_separable(const float2* X, const float2* W, float2* Y, int B, int C, int64_t M,
                        hipStream_t st);
 int axis_matmul(const float2* in, const float2* mat, float2* out, int64_t outer, int A, int J,

@@ -48,7 +48,7 @@ template <int KB>
 __global__ void __launch_bounds__(contract_threads(KB))
 __attribute__((amdgpu_waves_per_eu(2, 4)))
 k_contract_mfma(const float2* __restrict__ X, const float2* __restrict__ W, float2* __restrict__ Y,
-                int B, int Ci, int Co, int64_t M, int nblocks) {
+                int B, int Ci, int Co, int64_t M, int nblocks, int ymap_w) {
   constexpr int THREADS = contract_threads(KB);
   constexpr int NP = KB / 2;          // float4 (mode pairs) per operand row
   static_assert(KB % 2 == 0 && IC * OH * KB / 2 == WF4 * THREADS && IC * 32 * KB / 2 == XF4 * THREADS,
@@ -212,8 +212,21 @@ k_contract_mfma(const float2* __restrict__ X, const float2* __restrict__ W, floa
       const int b = b0 + 16 * hb + bl;
       const int64_t k = k0 + 2 * part;
       const float4 v = *reinterpret_cast<const float4*>(smem + bl * YB + o * KB * 2 + part * 4);
-      if (b < B && o0 + o < Co && k < M)
-        reinterpret_cast<float4*>(Y)[(((int64_t)b * Co + o0 + o) * M + k) >> 1] = v;
+      if (b < B && o0 + o < Co && k < M) {
+        float2* yp = Y + ((int64_t)b * Co + o0 + o) * M;
+        if (ymap_w) {
+          // rows of AC bins first, the DC column after them (see contract_mfma)
+          const int m1 = Mi / ymap_w;
+          auto map = [&](int kk) {
+            const int j = kk / ymap_w, kw = kk - j * ymap_w;
+            return kw ? j * (ymap_w - 1) + kw - 1 : m1 * (ymap_w - 1) + j;
+          };
+          yp[map((int)k)] = make_float2(v.x, v.y);
+          yp[map((int)k + 1)] = make_float2(v.z, v.w);
+        } else {
+          reinterpret_cast<float4*>(yp)[k >> 1] = v;
+        }
+      }
     }
   }
 }
@@ -231,7 +244,7 @@ bool contract_mfma_supported(int B, int Ci, int Co, int64_t M, int64_t sWi, int6
 
 template <int KB>
 static int launch_contract(const float2* X, const float2* W, float2* Y, int B, int Ci, int Co,
-                           int64_t M, hipStream_t st) {
+                           int64_t M, int ymap_w, hipStream_t st) {
   const int nblocks = (int)((M + KB - 1) / KB);
   const int pairs16 = (nblocks + 7) / 8;              // groups of 8 blocks
   dim3 grid((unsigned)(pairs16 * 16), (unsigned)((B + 31) / 32));
@@ -243,23 +256,28 @@ static int launch_contract(const float2* X, const float2* W, float2* Y, int B, i
     if (rc) return rc;
   }
   hipLaunchKernelGGL(k_contract_mfma<KB>, grid, dim3(contract_threads(KB)), lds, st, X, W, Y, B,
-                     Ci, Co, M, nblocks);
+                     Ci, Co, M, nblocks, ymap_w);
   return launch_status("k_contract_mfma");
 }
 
 // One workgroup per CU (the double-buffered tile takes 136-157 KB of LDS at
 // 16-18 modes); a grid just over the CU count would leave a few CUs a second
 // round, so such grids take the smallest wider block that fits one round.
+// ymap_w = 0: Y [B][Co][M] in the mode order of X and W.  ymap_w = W' > 0
+// (modes = m1 rows of W' bins): each (b, o) plane of Y holds the rows' bins
+// 1 .. W'-1 first, row after row (entry j (W'-1) + kw - 1), then the m1 DC
+// bins (entry m1 (W'-1) + j), so the AC part of every row starts at a
+// multiple of 8 (W'-1) bytes from the plane.
 int contract_mfma(const float2* X, const float2* W, float2* Y, int B, int Ci, int Co, int64_t M,
-                  hipStream_t st) {
+                  hipStream_t st, int ymap_w) {
   const int64_t bt = (B + 31) / 32, cus = 256;
   auto wgs = [&](int kb) { return 2 * ((M + kb - 1) / kb) * bt; };
   if (wgs(16) > cus && wgs(16) <= 2 * cus) {
-    if (wgs(18) <= cus) return launch_contract<18>(X, W, Y, B, Ci, Co, M, st);
+    if (wgs(18) <= cus) return launch_contract<18>(X, W, Y, B, Ci, Co, M, ymap_w, st);
   }
   // few modes (e.g. 32 x 17): halve the block so twice the CUs take part
-  if (2 * wgs(16) <= cus) return launch_contract<8>(X, W, Y, B, Ci, Co, M, st);
-  return launch_contract<16>(X, W, Y, B, Ci, Co, M, st);
+  if (2 * wgs(16) <= cus) return launch_contract<8>(X, W, Y, B, Ci, Co, M, ymap_w, st);
+  return launch_contract<16>(X, W, Y, B, Ci, Co, M, ymap_w, st);
 }
 
 }  // namespace fno

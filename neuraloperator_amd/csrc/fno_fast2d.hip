@@ -882,7 +882,7 @@ int rowsynth_mlp_epilogue(const float* x, const float2* yhat, const float* skip_
                           const float* bias, float* y, int B, int H, int W, int m1, int m2h,
                           int skip_kind, int act, float s, const LayerMlp& mlp, hipStream_t st);
 int contract_dense(const float2* X, const float2* W, float2* Y, int B, int Ci, int Co, int64_t M,
-                   int64_t sWi, int64_t sWo, int64_t sWk, hipStream_t st);
+                   int64_t sWi, int64_t sWo, int64_t sWk, hipStream_t st, int ymap_w);
 int rfft_window(const float* x, float2* xhat, int64_t planes, int32_t ndim, const int32_t* sizes,
                 const int32_t* modes, int32_t norm, void* ws, size_t ws_bytes, hipStream_t st);
 size_t rfft_window_ws(int64_t planes, int32_t ndim, const int32_t* sizes, const int32_t* modes);
@@ -1190,12 +1190,17 @@ int fast2d_block(const float* x, const float2* w, const float* bias, const float
                      ws_bytes - (size_t)((int64_t)B * (Ci + Co) * M) * sizeof(float2), st);
   }
   if (rc) return rc;
-  rc = contract_dense(xhat, w, yhat, B, Ci, Co, M, (int64_t)Co * M, M, 1, st);
+  // The row synthesis reads each window row's AC bins as one run, so for it
+  // the contraction writes every (b, o) plane as the rows' AC bins (m2h - 1
+  // entries each, 128-byte aligned at 17 and 33 bins) followed by the DC
+  // column, instead of in the weight's mode order.
+  const bool rsyn = mlp || !uses_z(Ci, Co, sizes, modes);
+  rc = contract_dense(xhat, w, yhat, B, Ci, Co, M, (int64_t)Co * M, M, 1, st, rsyn ? m2h : 0);
   if (rc) return rc;
   if (mlp)
     return rowsynth_mlp_epilogue(x, yhat, skip_w, bias, y, B, H, W, m1, m2h, skip_kind, act,
                                  iscale, *mlp, st);
-  if (!uses_z(Ci, Co, sizes, modes))
+  if (rsyn)
     return rowsynth_epilogue(x, yhat, skip_w, bias, y, B, Ci, H, W, m1, m2h, skip_kind, act,
                              iscale, st);
   rc = dispatch_inv(H, yhat, zbuf, B, Co, m1, m2h, st);

@@ -527,11 +527,22 @@ k_c2r_mfma(const float2* __restrict__ in, float* __restrict__ out, const float* 
 
 // ----------------------------------------------------------------- contraction
 // y[b, o, k] = sum_i x[b, i, k] * w[i*sWi + o*sWo + k*sWk]     (complex)
+// Output mode index of mode k = j W' + kw of an m1 x W' window when the
+// consumer wants each row's AC bins as one run (ymap_w = W'): AC bins of all
+// rows first (entry j (W' - 1) + kw - 1), then the DC column (m1 (W' - 1) + j).
+// ymap_w = 0 keeps the window order.
+__device__ __forceinline__ int64_t ymap_index(int64_t k, int64_t M, int ymap_w) {
+  if (!ymap_w) return k;
+  const int64_t j = k / ymap_w, kw = k - j * ymap_w;
+  return kw ? j * (ymap_w - 1) + kw - 1 : (M / ymap_w) * (ymap_w - 1) + j;
+}
+
 // One lane per mode k; each thread owns a TB x TO tile of (b, o).
 template <int TB, int TO>
 __global__ void __launch_bounds__(kThreads)
 k_contract_dense(const float2* __restrict__ X, const float2* __restrict__ W, float2* __restrict__ Y,
-                 int B, int Ci, int Co, int64_t M, int64_t sWi, int64_t sWo, int64_t sWk) {
+                 int B, int Ci, int Co, int64_t M, int64_t sWi, int64_t sWo, int64_t sWk,
+                 int ymap_w) {
   const int64_t k = (int64_t)blockIdx.x * 64 + (threadIdx.x & 63);
   const int nOt = (Co + TO - 1) / TO;
   const int nBt = (B + TB - 1) / TB;
@@ -562,7 +573,8 @@ k_contract_dense(const float2* __restrict__ X, const float2* __restrict__ W, flo
   for (int a = 0; a < TB; ++a)
 #pragma unroll
     for (int c = 0; c < TO; ++c)
-      if (b0 + a < B && o0 + c < Co) Y[((int64_t)(b0 + a) * Co + o0 + c) * M + k] = acc[a][c];
+      if (b0 + a < B && o0 + c < Co)
+        Y[((int64_t)(b0 + a) * Co + o0 + c) * M + ymap_index(k, M, ymap_w)] = acc[a][c];
 }
 
 // Small contractions (few modes): 16 lanes per output y[b, o, k], each
@@ -570,7 +582,8 @@ k_contract_dense(const float2* __restrict__ X, const float2* __restrict__ W, flo
 // ordered k fastest, then o, then b.
 __global__ void __launch_bounds__(kThreads)
 k_contract_small(const float2* __restrict__ X, const float2* __restrict__ W, float2* __restrict__ Y,
-                 int B, int Ci, int Co, int64_t M, int64_t sWi, int64_t sWo, int64_t sWk) {
+                 int B, int Ci, int Co, int64_t M, int64_t sWi, int64_t sWo, int64_t sWk,
+                 int ymap_w) {
   constexpr int L = 16;
   const int64_t out = ((int64_t)blockIdx.x * kThreads + threadIdx.x) / L;
   const int sub = threadIdx.x % L;
@@ -588,7 +601,7 @@ k_contract_small(const float2* __restrict__ X, const float2* __restrict__ W, flo
     acc.x += __shfl_xor(acc.x, off, L);
     acc.y += __shfl_xor(acc.y, off, L);
   }
-  if (live && sub == 0) Y[((int64_t)b * Co + o) * M + k] = acc;
+  if (live && sub == 0) Y[((int64_t)b * Co + o) * M + ymap_index(k, M, ymap_w)] = acc;
 }
 
 // y[b, i, k] = x[b, i, k] * w[i, k]
@@ -1175,27 +1188,28 @@ int irfft_epilogue(const float2* yhat, const float* bias, const float* x, const 
 bool contract_mfma_supported(int B, int Ci, int Co, int64_t M, int64_t sWi, int64_t sWo,
                              int64_t sWk);
 int contract_mfma(const float2* X, const float2* W, float2* Y, int B, int Ci, int Co, int64_t M,
-                  hipStream_t st);
+                  hipStream_t st, int ymap_w);
 
+// ymap_w: the output mode order (ymap_index); 0 for the window order.
 int contract_dense(const float2* X, const float2* W, float2* Y, int B, int Ci, int Co, int64_t M,
-                   int64_t sWi, int64_t sWo, int64_t sWk, hipStream_t st) {
+                   int64_t sWi, int64_t sWo, int64_t sWk, hipStream_t st, int ymap_w) {
   // few modes: the MFMA kernel's grid (a workgroup per 8+ modes and 32
   // output channels) would leave most CUs idle; spread the outputs instead
   const int64_t outs = (int64_t)B * Co * M;
   if (M <= 64 && outs <= (int64_t(1) << 20)) {
     const int64_t blocks = (outs * 16 + kThreads - 1) / kThreads;
     hipLaunchKernelGGL(k_contract_small, dim3((unsigned)blocks), dim3(kThreads), 0, st, X, W, Y, B,
-                       Ci, Co, M, sWi, sWo, sWk);
+                       Ci, Co, M, sWi, sWo, sWk, ymap_w);
     return launch_status("k_contract_small");
   }
   if (contract_mfma_supported(B, Ci, Co, M, sWi, sWo, sWk))
-    return contract_mfma(X, W, Y, B, Ci, Co, M, st);
+    return contract_mfma(X, W, Y, B, Ci, Co, M, st, ymap_w);
   constexpr int TB = 4, TO = 8;
   const int nTiles = ((B + TB - 1) / TB) * ((Co + TO - 1) / TO);
   const int wavesPerBlock = kThreads / 64;
   dim3 grid((unsigned)((M + 63) / 64), (unsigned)((nTiles + wavesPerBlock - 1) / wavesPerBlock));
   hipLaunchKernelGGL((k_contract_dense<TB, TO>), grid, dim3(kThreads), 0, st, X, W, Y, B, Ci, Co, M,
-                     sWi, sWo, sWk);
+                     sWi, sWo, sWk, ymap_w);
   return launch_status("k_contract_dense");
 }
 

@@ -72,8 +72,9 @@ __device__ __forceinline__ float synth_entry(int j, int col, int W, int m2h, flo
 
 // ------------------------------------------------------------------------
 // The inverse column transform is done here, from the window spectrum
-// yhat[b][o][j][kw] (j < m1 window rows, frequency j - m1/2), so no H x m2h
-// intermediate goes through memory.  A workgroup takes blocks
+// yhat[b][o] (j < m1 window rows, frequency j - m1/2; per channel the rows'
+// AC bins kw >= 1 as runs of m2h - 1 entries, then the m1 DC entries), so no
+// H x m2h intermediate goes through memory.  A workgroup takes blocks
 // of R = 8 rows of one sample, h_t = r + (H / R) t (one residue class r of
 // H / R), for which
 //   Z[o, h_t, kw] = sum_j yhat[o, j, kw] w_H^(f_j h_t)
@@ -411,9 +412,13 @@ k_row_synth(const float* __restrict__ x, const float2* __restrict__ yhat,
     // over the distinct channels of the wave); the channel goes in the offset
     const __amdgpu_buffer_rsrc_t ryh = make_rsrc(yhat + (int64_t)b * rg::kCo * m1 * m2h,
                                                  (uint32_t)(rg::kCo * m1 * m2h * 8));
+    // a channel's plane (m1 x m2h entries) holds the window rows' AC bins
+    // kw = 1 .. m2h-1 first (row j at j (m2h - 1) + kw - 1), then the DC
+    // column (row j at m1 (m2h - 1) + j)
+    const int ac = m2h - 1;
     const uint32_t cstride = (uint32_t)(16 * m1 * m2h) * 8u;   // 16 channels
-    const uint32_t boff = kwt < m2h ? (uint32_t)(ot0 * m1 * m2h + kwt) * 8u : 0x80000000u;
-    const uint32_t dbase = (uint32_t)(so * m1 * m2h) * 8u;
+    const uint32_t boff = kwt < m2h ? (uint32_t)(ot0 * m1 * m2h + kwt - 1) * 8u : 0x80000000u;
+    const uint32_t dbase = (uint32_t)(so * m1 * m2h + m1 * ac) * 8u;
     float2 P[R][4];
 #pragma unroll
     for (int c = 0; c < R; ++c)
@@ -429,7 +434,7 @@ k_row_synth(const float* __restrict__ x, const float2* __restrict__ yhat,
       const int jd = j0 + sq;
       const float2 vd = __builtin_bit_cast(
           float2, __builtin_amdgcn_raw_buffer_load_b64(
-                      ryh, (int)(jd < m1 ? dbase + (uint32_t)(jd * m2h) * 8u : 0x80000000u), 0, 0));
+                      ryh, (int)(jd < m1 ? dbase + (uint32_t)jd * 8u : 0x80000000u), 0, 0));
 #pragma unroll
       for (int hc = 0; hc < R; hc += SYN_BATCH) {
         float2 v[SYN_BATCH][4];
@@ -439,7 +444,7 @@ k_row_synth(const float* __restrict__ x, const float2* __restrict__ yhat,
           const uint32_t bo = j < m1 ? boff : 0x80000000u;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int soff = __builtin_amdgcn_readfirstlane((int)(i * cstride + j * m2h * 8));
+            const int soff = __builtin_amdgcn_readfirstlane((int)(i * cstride + j * ac * 8));
             v[cc][i] = __builtin_bit_cast(
                 float2, __builtin_amdgcn_raw_buffer_load_b64(ryh, (int)bo, soff, 0));
           }
