@@ -409,10 +409,12 @@ def module_workload(name, dev):
                   "layers": [_oracle_layer(blk, i) for i in range(blk.n_layers)]}
         xs = x[:1].float().cpu().double()
         return lambda: R.fno_forward(xs, params), 1, B
-    # bf16 mixed precision as torch.autocast defines it: the 1x1 layers (lifting,
-    # channel MLPs, projection) take bf16-rounded operands with fp32
-    # accumulation; activations, skips and the complex64 spectral path stay
-    # fp32 (the bf16 input is widened on entry)
+    # bf16 mixed precision: under torch.autocast(bfloat16) the 1x1 layers
+    # (lifting, channel MLPs, projection) take bf16-rounded operands with fp32
+    # accumulation, and the activations between the lifting, the layers and
+    # the projection are stored in bf16; the complex64 spectral path, the
+    # skips and every accumulation are fp32 (the bf16 input is widened on
+    # entry)
     def step():
         with torch.autocast("cuda", dtype=torch.bfloat16):
             return model(x.float())
@@ -421,7 +423,8 @@ def module_workload(name, dev):
         with torch.autocast("cuda", dtype=torch.bfloat16):
             return torch_rocm_fno(model, x.float())
     return dict(step=step, nbytes=nbytes,
-                dtype="bf16 1x1-layer operands (autocast), fp32 accumulation and activations",
+                dtype="bf16 activation storage and 1x1-layer operands (autocast), fp32 "
+                      "accumulation, complex64 spectral path",
                 cpu=cpu,
                 rocm=(rocm, "the same FNO forward in torch ops under the same autocast: "
                             "torch.fft + einsum + Conv1d + gelu (rocFFT, rocBLAS, MIOpen), same GPU"),

@@ -211,6 +211,29 @@ int fno_channel_mlp_is_supported(int32_t in_channels, int32_t hidden_channels,
                                  int32_t out_channels, int64_t points);
 
 /*
+ * The lifting and projection MLPs of the bf16 FNO forward, with bfloat16
+ * activation storage on one side: y = act(W2 gelu(W1 x + b1) + b2), both 1x1
+ * layers on bf16 operands with fp32 accumulation (as fno_channel_mlp_f32 with
+ * bf16_products = 1; ChannelMLP.forward, neuralop/layers/channel_mlp.py
+ * :82-119, under torch.autocast(dtype=bfloat16)), no skip.
+ *   x_bf16 = 1: x is bfloat16 [B, Ci, P] (the projection's input);
+ *   y_bf16 = 1: y is bfloat16 [B, Co, P], rounded to nearest even (the
+ *   lifting's output); the other side is float32.  x and y 16-byte aligned,
+ *   not overlapping.
+ * Covered: Ci <= 4 -> (128, 64) or (64, 32) with y_bf16 (lifting),
+ * (64, 128) or (32, 64) -> Co <= 16 with x_bf16 (projection), P % 4 == 0;
+ * with neither flag every fno_channel_mlp_f32 width.  Otherwise
+ * FNO_ERR_UNSUPPORTED (fno_channel_mlp_io_is_supported tells which).
+ */
+int fno_channel_mlp_io(const void* x, const float* w1, const float* b1, const float* w2,
+                       const float* b2, void* y, int64_t batch, int32_t in_channels,
+                       int32_t hidden_channels, int32_t out_channels, int64_t points, int32_t act,
+                       int32_t x_bf16, int32_t y_bf16, void* stream);
+int fno_channel_mlp_io_is_supported(int32_t in_channels, int32_t hidden_channels,
+                                    int32_t out_channels, int64_t points, int32_t x_bf16,
+                                    int32_t y_bf16);
+
+/*
  * One call for the whole spectral block
  *     y = act(SpectralConv(x) + skip(x))
  * with a dense weight (w [Ci, Co, m_1..m_ndim] window, complex64) and bias
@@ -263,6 +286,29 @@ int fno_layer_f32(const float* x, const void* w, const float* bias, const float*
 int fno_layer_is_fused(int32_t batch, int32_t channels, int32_t hidden_channels, int32_t ndim,
                        const int32_t* sizes, const int32_t* modes, int32_t skip_kind,
                        int32_t mlp_skip_kind);
+
+/*
+ * fno_layer_f32 with bfloat16 activation storage: x and y are bfloat16
+ * [batch, channels, N_1, N_2] (16-byte aligned, not overlapping); the
+ * arithmetic is fno_layer_f32's, on x widened exactly to fp32, and y is
+ * rounded to bfloat16 (nearest even) at the store.  Replaces the same
+ * reference layer (fno_block.py:331-379) in the bf16 FNO forward, where the
+ * activations between layers are kept in bfloat16 (half the bytes of every
+ * layer's reads and writes of the field).  Covered where
+ * fno_layer_bf16_is_fused says so: fno_layer_is_fused's shapes with planes of
+ * 64, 128 or 256 rows by 128 or 256 columns; otherwise FNO_ERR_UNSUPPORTED,
+ * nothing enqueued.  Workspace and errors as fno_layer_f32.
+ */
+int fno_layer_bf16(const void* x, const void* w, const float* bias, const float* skip_weight,
+                   const float* mlp_w1, const float* mlp_b1, const float* mlp_w2,
+                   const float* mlp_b2, const float* gate_weight, const float* gate_bias, void* y,
+                   int32_t batch, int32_t channels, int32_t hidden_channels, int32_t ndim,
+                   const int32_t* sizes, const int32_t* modes, int32_t norm, int32_t skip_kind,
+                   int32_t mlp_skip_kind, int32_t act, void* workspace, size_t workspace_bytes,
+                   void* stream);
+int fno_layer_bf16_is_fused(int32_t batch, int32_t channels, int32_t hidden_channels,
+                            int32_t ndim, const int32_t* sizes, const int32_t* modes,
+                            int32_t skip_kind, int32_t mlp_skip_kind);
 
 /*
  * fno_spectral_block_f32 without a workspace argument and without any device

@@ -56,12 +56,20 @@ _SIGNATURES = {
                                      _c_i64, _c_i32, _c_i32, _c_i32, _c_i64, _c_i32, _c_i32, _c_i32,
                                      _c_vp]),
     "fno_channel_mlp_is_supported": (_c_i32, [_c_i32, _c_i32, _c_i32, _c_i64]),
+    "fno_channel_mlp_io": (_c_i32, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i32, _c_i32,
+                                    _c_i32, _c_i64, _c_i32, _c_i32, _c_i32, _c_vp]),
+    "fno_channel_mlp_io_is_supported": (_c_i32, [_c_i32, _c_i32, _c_i32, _c_i64, _c_i32, _c_i32]),
     "fno_irfft_window_epilogue_f32": (_c_i32, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i32, _c_i32,
                                                _c_i32, _c_i32, _c_i32p, _c_i32p, _c_i32, _c_i32,
                                                _c_i32, _c_vp, _c_size, _c_vp]),
     "fno_layer_is_fused": (_c_i32, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32p, _c_i32p, _c_i32,
                                     _c_i32]),
+    "fno_layer_bf16_is_fused": (_c_i32, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32p, _c_i32p, _c_i32,
+                                         _c_i32]),
     "fno_layer_f32": (_c_i32, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
+                               _c_vp, _c_vp, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32p, _c_i32p,
+                               _c_i32, _c_i32, _c_i32, _c_i32, _c_vp, _c_size, _c_vp]),
+    "fno_layer_bf16": (_c_i32, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                                _c_vp, _c_vp, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32p, _c_i32p,
                                _c_i32, _c_i32, _c_i32, _c_i32, _c_vp, _c_size, _c_vp]),
     "fno_fft_window_c64": (_c_i32, [_c_vp, _c_vp, _c_i64, _c_i32, _c_i32p, _c_i32p, _c_i32, _c_vp,

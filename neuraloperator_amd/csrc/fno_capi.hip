@@ -43,18 +43,23 @@ int channel_mlp(const float* x, const float* w1, const float* b1, const float* w
                 const float* xs, const float* sw, const float* sb, float* y, int64_t B, int Ci,
                 int Ch, int Co, int64_t P, int skip_kind, int act, bool bf16_products,
                 hipStream_t st);
+bool channel_mlp_io_supported(int Ci, int Ch, int Co, int64_t P, bool x_bf16, bool y_bf16);
+int channel_mlp_io(const void* x, const float* w1, const float* b1, const float* w2,
+                   const float* b2, void* y, int64_t B, int Ci, int Ch, int Co, int64_t P, int act,
+                   bool x_bf16, bool y_bf16, hipStream_t st);
 bool fast2d_supported(int B, int Ci, int Co, int ndim, const int32_t* sizes, const int32_t* modes,
                       int skip_kind);
+bool fast2d_bf16_supported(const int32_t* sizes, const int32_t* modes);
 size_t fast2d_workspace(int B, int Ci, int Co, const int32_t* sizes, const int32_t* modes);
 bool rowsynth_covers(int H, int W, int Ci, int Co, int m1, int m2h);
 bool fast1d_supported(int Ci, int Co, int N, int m);
 int fast1d_block(const float* x, const float2* w, const float* bias, const float* skip_w, float* y,
                  int B, int Ci, int Co, int N, int m, int norm, int skip_kind, int act,
                  hipStream_t st);
-int fast2d_block(const float* x, const float2* w, const float* bias, const float* skip_w, float* y,
+int fast2d_block(const void* x, const float2* w, const float* bias, const float* skip_w, void* y,
                  int B, int Ci, int Co, const int32_t* sizes, const int32_t* modes, int norm,
                  int skip_kind, int act, void* ws, size_t ws_bytes, hipStream_t st,
-                 const LayerMlp* mlp = nullptr);
+                 const LayerMlp* mlp = nullptr, bool bf = false);
 bool rowsynth_mlp_covers(int H, int W, int Ci, int Co, int m1, int m2h, int hidden,
                          int skip_kind);
 bool tucker_fused_supported(int B, int Ci, int Co, int ndim, const int32_t* modes,
@@ -431,6 +436,53 @@ int fno_channel_mlp_f32(const float* x, const float* w1, const float* b1, const 
                      reinterpret_cast<hipStream_t>(stream));
 }
 
+int fno_channel_mlp_io_is_supported(int32_t in_channels, int32_t hidden_channels,
+                                    int32_t out_channels, int64_t points, int32_t x_bf16,
+                                    int32_t y_bf16) {
+  return channel_mlp_io_supported(in_channels, hidden_channels, out_channels, points, x_bf16 != 0,
+                                  y_bf16 != 0)
+             ? 1
+             : 0;
+}
+
+int fno_channel_mlp_io(const void* x, const float* w1, const float* b1, const float* w2,
+                       const float* b2, void* y, int64_t batch, int32_t in_channels,
+                       int32_t hidden_channels, int32_t out_channels, int64_t points, int32_t act,
+                       int32_t x_bf16, int32_t y_bf16, void* stream) {
+  clear_error();
+  FNO_CHECK_ARG(x && w1 && w2 && y, "x/w1/w2/y must not be NULL");
+  FNO_CHECK_ARG((x_bf16 == 0 || x_bf16 == 1) && (y_bf16 == 0 || y_bf16 == 1),
+                "x_bf16 / y_bf16 must be 0 or 1 (got %d, %d)", x_bf16, y_bf16);
+  FNO_CHECK_ARG(batch >= 1 && in_channels >= 1 && hidden_channels >= 1 && out_channels >= 1 &&
+                    points >= 1,
+                "bad batch/channels/points");
+  FNO_CHECK_ARG(extent_ok({batch, in_channels > out_channels ? in_channels : out_channels, points}),
+                "batch x channels x points exceeds %lld elements", (long long)kMaxElems);
+  FNO_CHECK_ARG(act == FNO_ACT_NONE || act == FNO_ACT_GELU, "unknown activation %d", act);
+  if (!channel_mlp_io_supported(in_channels, hidden_channels, out_channels, points, x_bf16 != 0,
+                                y_bf16 != 0)) {
+    set_error("channel MLP %d -> %d -> %d over %lld points with %s storage is not covered by the "
+              "kernel", in_channels, hidden_channels, out_channels, (long long)points,
+              x_bf16 ? (y_bf16 ? "bf16 in / bf16 out" : "bf16 in") : (y_bf16 ? "bf16 out" : "fp32"));
+    return FNO_ERR_UNSUPPORTED;
+  }
+  const uintptr_t addr = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y);
+  if (addr % 16 != 0) {
+    set_error("channel MLP: x and y must be 16-byte aligned");
+    return FNO_ERR_UNSUPPORTED;
+  }
+  const size_t ybytes = (size_t)batch * out_channels * points * (y_bf16 ? 2 : 4);
+  const size_t xbytes = (size_t)batch * in_channels * points * (x_bf16 ? 2 : 4);
+  FNO_CHECK_ARG(!ranges_overlap(x, xbytes, y, ybytes), "channel MLP: y must not overlap x");
+  if (!x_bf16 && !y_bf16)
+    return channel_mlp(static_cast<const float*>(x), w1, b1, w2, b2, nullptr, nullptr, nullptr,
+                       static_cast<float*>(y), batch, in_channels, hidden_channels, out_channels,
+                       points, FNO_SKIP_NONE, act, true, reinterpret_cast<hipStream_t>(stream));
+  return channel_mlp_io(x, w1, b1, w2, b2, y, batch, in_channels, hidden_channels, out_channels,
+                        points, act, x_bf16 != 0, y_bf16 != 0,
+                        reinterpret_cast<hipStream_t>(stream));
+}
+
 int fno_spectral_block_is_fused(int32_t batch, int32_t in_channels, int32_t out_channels,
                                 int32_t ndim, const int32_t* sizes, const int32_t* modes,
                                 int32_t skip_kind) {
@@ -465,10 +517,12 @@ size_t fno_spectral_block_workspace_bytes(int32_t batch, int32_t in_channels,
 
 namespace fno {
 
-int spectral_block_check(const float* x, const void* w, float* y, int32_t batch,
+// es: bytes per element of x and y (4: float32, 2: bfloat16)
+int spectral_block_check(const void* x, const void* w, void* y, int32_t batch,
                          int32_t in_channels, int32_t out_channels, int32_t ndim,
                          const int32_t* sizes, const int32_t* modes, int32_t norm,
-                         int32_t skip_kind, int32_t act, const float* skip_weight) {
+                         int32_t skip_kind, int32_t act, const float* skip_weight,
+                         size_t es = sizeof(float)) {
   FNO_CHECK_ARG(x && w && y, "x/w/y must not be NULL");
   FNO_CHECK_ARG(batch >= 1 && in_channels >= 1 && out_channels >= 1, "bad batch/channels");
   int rc = validate_window(ndim, sizes, modes);
@@ -477,8 +531,8 @@ int spectral_block_check(const float* x, const void* w, float* y, int32_t batch,
   const int64_t elems = bounded_elems((int64_t)batch * cmax, ndim, sizes);
   FNO_CHECK_ARG(elems > 0, "batch x channels x sizes exceeds %lld elements", (long long)kMaxElems);
   const int64_t points = elems / ((int64_t)batch * cmax);
-  FNO_CHECK_ARG(!ranges_overlap(x, (size_t)batch * in_channels * points * sizeof(float), y,
-                                (size_t)batch * out_channels * points * sizeof(float)),
+  FNO_CHECK_ARG(!ranges_overlap(x, (size_t)batch * in_channels * points * es, y,
+                                (size_t)batch * out_channels * points * es),
                 "spectral block: y must not overlap x");
   rc = check_norm(norm);
   if (rc) return rc;
@@ -546,16 +600,19 @@ int fno_spectral_block_f32(const float* x, const void* w, const float* bias,
 }  // extern "C"
 
 // ---------------------------------------------------------------- FNO layer
+// bf16: bfloat16 activation storage (fno_layer_bf16)
 static bool layer_fused(int32_t batch, int32_t channels, int32_t hidden, int32_t ndim,
                         const int32_t* sizes, const int32_t* modes, int32_t skip_kind,
-                        int32_t mlp_skip_kind) {
+                        int32_t mlp_skip_kind, bool bf16 = false) {
   if (!sizes || !modes || ndim != 2 || batch < 1) return false;
   if (!(mlp_skip_kind == FNO_SKIP_NONE || mlp_skip_kind == FNO_SKIP_SOFT_GATING ||
         mlp_skip_kind == FNO_SKIP_IDENTITY))
     return false;
-  return fast2d_supported(batch, channels, channels, ndim, sizes, modes, skip_kind) &&
-         rowsynth_mlp_covers(sizes[0], sizes[1], channels, channels, modes[0], modes[1], hidden,
-                             skip_kind);
+  if (!fast2d_supported(batch, channels, channels, ndim, sizes, modes, skip_kind) ||
+      !rowsynth_mlp_covers(sizes[0], sizes[1], channels, channels, modes[0], modes[1], hidden,
+                           skip_kind))
+    return false;
+  return !bf16 || fast2d_bf16_supported(sizes, modes);
 }
 
 extern "C" {
@@ -569,16 +626,26 @@ int fno_layer_is_fused(int32_t batch, int32_t channels, int32_t hidden_channels,
              : 0;
 }
 
-int fno_layer_f32(const float* x, const void* w, const float* bias, const float* skip_weight,
-                  const float* mlp_w1, const float* mlp_b1, const float* mlp_w2,
-                  const float* mlp_b2, const float* gate_weight, const float* gate_bias, float* y,
-                  int32_t batch, int32_t channels, int32_t hidden_channels, int32_t ndim,
-                  const int32_t* sizes, const int32_t* modes, int32_t norm, int32_t skip_kind,
-                  int32_t mlp_skip_kind, int32_t act, void* workspace, size_t workspace_bytes,
-                  void* stream) {
+int fno_layer_bf16_is_fused(int32_t batch, int32_t channels, int32_t hidden_channels,
+                            int32_t ndim, const int32_t* sizes, const int32_t* modes,
+                            int32_t skip_kind, int32_t mlp_skip_kind) {
+  return layer_fused(batch, channels, hidden_channels, ndim, sizes, modes, skip_kind,
+                     mlp_skip_kind, true)
+             ? 1
+             : 0;
+}
+
+// Both layer entry points: es = bytes per element of x and y.
+static int layer_run(const void* x, const void* w, const float* bias, const float* skip_weight,
+                     const float* mlp_w1, const float* mlp_b1, const float* mlp_w2,
+                     const float* mlp_b2, const float* gate_weight, const float* gate_bias, void* y,
+                     int32_t batch, int32_t channels, int32_t hidden_channels, int32_t ndim,
+                     const int32_t* sizes, const int32_t* modes, int32_t norm, int32_t skip_kind,
+                     int32_t mlp_skip_kind, int32_t act, void* workspace, size_t workspace_bytes,
+                     void* stream, size_t es) {
   clear_error();
   int rc = spectral_block_check(x, w, y, batch, channels, channels, ndim, sizes, modes, norm,
-                                skip_kind, act, skip_weight);
+                                skip_kind, act, skip_weight, es);
   if (rc) return rc;
   FNO_CHECK_ARG(mlp_w1 && mlp_w2, "mlp_w1/mlp_w2 must not be NULL");
   FNO_CHECK_ARG(hidden_channels >= 1, "hidden_channels must be positive");
@@ -588,9 +655,11 @@ int fno_layer_f32(const float* x, const void* w, const float* bias, const float*
   FNO_CHECK_ARG(mlp_skip_kind != FNO_SKIP_SOFT_GATING || gate_weight,
                 "soft-gating needs a gate weight");
   if (!layer_fused(batch, channels, hidden_channels, ndim, sizes, modes, skip_kind,
-                   mlp_skip_kind)) {
-    set_error("FNO layer: this shape has no one-pass kernel (compose fno_spectral_block_f32 and "
-              "fno_channel_mlp_f32)");
+                   mlp_skip_kind, es == 2)) {
+    set_error(es == 2 ? "FNO layer: this shape has no one-pass bfloat16 kernel "
+                        "(fno_layer_bf16_is_fused)"
+                      : "FNO layer: this shape has no one-pass kernel (compose "
+                        "fno_spectral_block_f32 and fno_channel_mlp_f32)");
     return FNO_ERR_UNSUPPORTED;
   }
   const size_t need = fno_spectral_block_workspace_bytes(batch, channels, channels, ndim, sizes,
@@ -609,7 +678,31 @@ int fno_layer_f32(const float* x, const void* w, const float* bias, const float*
   mlp.gate_kind = mlp_skip_kind;
   return fast2d_block(x, reinterpret_cast<const float2*>(w), bias, skip_weight, y, batch, channels,
                       channels, sizes, modes, norm, skip_kind, act, workspace, workspace_bytes,
-                      reinterpret_cast<hipStream_t>(stream), &mlp);
+                      reinterpret_cast<hipStream_t>(stream), &mlp, es == 2);
+}
+
+int fno_layer_f32(const float* x, const void* w, const float* bias, const float* skip_weight,
+                  const float* mlp_w1, const float* mlp_b1, const float* mlp_w2,
+                  const float* mlp_b2, const float* gate_weight, const float* gate_bias, float* y,
+                  int32_t batch, int32_t channels, int32_t hidden_channels, int32_t ndim,
+                  const int32_t* sizes, const int32_t* modes, int32_t norm, int32_t skip_kind,
+                  int32_t mlp_skip_kind, int32_t act, void* workspace, size_t workspace_bytes,
+                  void* stream) {
+  return layer_run(x, w, bias, skip_weight, mlp_w1, mlp_b1, mlp_w2, mlp_b2, gate_weight, gate_bias,
+                   y, batch, channels, hidden_channels, ndim, sizes, modes, norm, skip_kind,
+                   mlp_skip_kind, act, workspace, workspace_bytes, stream, sizeof(float));
+}
+
+int fno_layer_bf16(const void* x, const void* w, const float* bias, const float* skip_weight,
+                   const float* mlp_w1, const float* mlp_b1, const float* mlp_w2,
+                   const float* mlp_b2, const float* gate_weight, const float* gate_bias, void* y,
+                   int32_t batch, int32_t channels, int32_t hidden_channels, int32_t ndim,
+                   const int32_t* sizes, const int32_t* modes, int32_t norm, int32_t skip_kind,
+                   int32_t mlp_skip_kind, int32_t act, void* workspace, size_t workspace_bytes,
+                   void* stream) {
+  return layer_run(x, w, bias, skip_weight, mlp_w1, mlp_b1, mlp_w2, mlp_b2, gate_weight, gate_bias,
+                   y, batch, channels, hidden_channels, ndim, sizes, modes, norm, skip_kind,
+                   mlp_skip_kind, act, workspace, workspace_bytes, stream, 2);
 }
 
 }  // extern "C"

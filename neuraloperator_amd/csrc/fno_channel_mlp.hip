@@ -31,6 +31,8 @@
 // the slab swizzle still separates the groups) and hidden row
 // 16 (2 kb + j / 4) + 4 G + j % 4 in GEMM 2 (two of GEMM 1's accumulator
 // tiles per k-step).
+#include <type_traits>
+
 #include "fno_common.h"
 
 namespace fno {
@@ -62,12 +64,22 @@ struct MlpLds {
 
 // TWO = false: a single 1x1 layer y = act(W1 x + b2 + skip) (CH == CO), the
 // linear skip of the block epilogue with the spectral term as identity skip.
-template <int CI, int CH, int CO, bool TWO, bool BF>
+// IO: storage of x (bit 0) and y (bit 1), bfloat16 where set (the lifting's
+// output and the projection's input in the bf16 FNO forward), else float32;
+// x is widened to fp32 in the slab, y rounded to bf16 (nearest even) at the
+// store.
+template <int CI, int CH, int CO, bool TWO, bool BF, int IO = 0>
 __global__ void __launch_bounds__(kMlpThreads) __attribute__((amdgpu_waves_per_eu(CI <= 64 ? 2 : 1)))
-k_channel_mlp(const float* x, const float* __restrict__ w1, const float* __restrict__ b1,
+k_channel_mlp(const void* xv, const float* __restrict__ w1, const float* __restrict__ b1,
               const float* __restrict__ w2, const float* __restrict__ b2, const float* xs,
-              const float* __restrict__ sw, const float* __restrict__ sb, float* y, int64_t P,
+              const float* __restrict__ sw, const float* __restrict__ sb, void* yv, int64_t P,
               int64_t tiles_per_sample, int64_t tiles, int ci, int co, int skip_kind, int act) {
+  constexpr bool XBF = IO & 1, YBF = IO & 2;
+  using XT = std::conditional_t<XBF, __bf16, float>;
+  using YT = std::conditional_t<YBF, __bf16, float>;
+  using XQ = std::conditional_t<XBF, uint2, float4>;   // 4 points of x as loaded
+  const XT* x = static_cast<const XT*>(xv);
+  YT* y = static_cast<YT*>(yv);
   static_assert(CI % 4 == 0 && CH % 16 == 0 && CO % 16 == 0, "channel multiples");
   static_assert(TWO || CH == CO, "one layer: CH == CO");
   // outputs go back through the slab (as [CO][TP]) for 16-byte stores when
@@ -131,19 +143,28 @@ k_channel_mlp(const float* x, const float* __restrict__ w1, const float* __restr
 
   // slab of tile `tile` into registers: float4 q = tid + kMlpThreads j is row
   // q / (TP/4), points 4 (q % (TP/4)) .. +3; points past P read as zero
-  float4 pre[LPT];
+  XQ pre[LPT];
   auto load_slab = [&](int64_t tile) __attribute__((always_inline)) {
     const int64_t b = tile / tiles_per_sample;
     const int64_t p0 = (tile % tiles_per_sample) * kMlpTP;
-    const float* xb = x + b * ci * P;
+    const XT* xb = x + b * ci * P;
 #pragma unroll
     for (int j = 0; j < LPT; ++j) {
       const int q = tid + kMlpThreads * j;
       const int c = q / (kMlpTP / 4);
       const int64_t p = p0 + 4 * (q % (kMlpTP / 4));
-      pre[j] = q < NQ && p < P && c < ci ? *reinterpret_cast<const float4*>(xb + c * P + p)
-                                         : make_float4(0.f, 0.f, 0.f, 0.f);
+      XQ zero;
+      if constexpr (XBF) zero = make_uint2(0u, 0u);
+      else zero = make_float4(0.f, 0.f, 0.f, 0.f);
+      pre[j] = q < NQ && p < P && c < ci ? *reinterpret_cast<const XQ*>(xb + c * P + p) : zero;
     }
+  };
+  auto widen = [](const XQ& v) __attribute__((always_inline)) -> float4 {
+    if constexpr (XBF)
+      return make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
+                         __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u));
+    else
+      return v;
   };
 
   // skip input of the outputs this lane stores for tile `tile`
@@ -171,7 +192,7 @@ k_channel_mlp(const float* x, const float* __restrict__ w1, const float* __restr
       const int q = tid + kMlpThreads * j;
       const int row = q / (kMlpTP / 4);
       if (q < NQ)
-        *reinterpret_cast<float4*>(slab + row * kMlpXS + slab_col(row, 4 * (q % (kMlpTP / 4)))) = pre[j];
+        *reinterpret_cast<float4*>(slab + row * kMlpXS + slab_col(row, 4 * (q % (kMlpTP / 4)))) = widen(pre[j]);
     }
     __syncthreads();
     const int64_t b = tile / tiles_per_sample;
@@ -314,7 +335,15 @@ k_channel_mlp(const float* x, const float* __restrict__ w1, const float* __restr
           v.z = gelu_erf(v.z);
           v.w = gelu_erf(v.w);
         }
-        *reinterpret_cast<float4*>(y + (b * co + c) * P + p) = v;
+        if constexpr (YBF) {
+          auto pk = [](float a, float b) __attribute__((always_inline)) {
+            return (uint32_t)__builtin_bit_cast(unsigned short, (__bf16)a) |
+                   ((uint32_t)__builtin_bit_cast(unsigned short, (__bf16)b) << 16);
+          };
+          *reinterpret_cast<uint2*>(y + (b * co + c) * P + p) = make_uint2(pk(v.x, v.y), pk(v.z, v.w));
+        } else {
+          *reinterpret_cast<float4*>(y + (b * co + c) * P + p) = v;
+        }
       }
       continue;
     }
@@ -333,7 +362,7 @@ k_channel_mlp(const float* x, const float* __restrict__ w1, const float* __restr
           float v = o[mo][n][r] + bos[oc];
           if (has_skip) v = fmaf(gws[oc], sv[n][mo][r], v);
           if (gelu_out) v = gelu_erf(v);
-          y[idx] = v;
+          y[idx] = (YT)v;
         }
     }
   }
@@ -359,13 +388,13 @@ bool channel_mlp_supported(int Ci, int Ch, int Co, int64_t P) {
   return P % 4 == 0 && mlp_variant(Ci, Ch, Co) >= 0;
 }
 
-template <int CI, int CH, int CO, bool TWO, bool BF>
-static int launch_mlp(const float* x, const float* w1, const float* b1, const float* w2,
-                      const float* b2, const float* xs, const float* sw, const float* sb, float* y,
+template <int CI, int CH, int CO, bool TWO, bool BF, int IO = 0>
+static int launch_mlp(const void* x, const float* w1, const float* b1, const float* w2,
+                      const float* b2, const float* xs, const float* sw, const float* sb, void* y,
                       int64_t B, int64_t P, int ci, int co, int skip_kind, int act, hipStream_t st) {
   const size_t lds = MlpLds<CI, CH, CO, TWO, BF>::total;
   if (lds > 48 * 1024) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_channel_mlp<CI, CH, CO, TWO, BF>),
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_channel_mlp<CI, CH, CO, TWO, BF, IO>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) {
       set_error("channel MLP: %s", hipGetErrorString(e));
@@ -380,7 +409,7 @@ static int launch_mlp(const float* x, const float* w1, const float* b1, const fl
   if (per_cu == 0) {
     int n = 0;
     const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-        &n, reinterpret_cast<const void*>(&k_channel_mlp<CI, CH, CO, TWO, BF>), kMlpThreads, lds);
+        &n, reinterpret_cast<const void*>(&k_channel_mlp<CI, CH, CO, TWO, BF, IO>), kMlpThreads, lds);
     per_cu = (e == hipSuccess && n > 0) ? n : 1;
   }
   int dev = 0, cus = 0;
@@ -389,7 +418,7 @@ static int launch_mlp(const float* x, const float* w1, const float* b1, const fl
     cus = 256;
   int64_t grid = (int64_t)cus * per_cu;
   if (grid > tiles) grid = tiles;
-  hipLaunchKernelGGL((k_channel_mlp<CI, CH, CO, TWO, BF>), dim3((unsigned)grid), dim3(kMlpThreads), lds, st,
+  hipLaunchKernelGGL((k_channel_mlp<CI, CH, CO, TWO, BF, IO>), dim3((unsigned)grid), dim3(kMlpThreads), lds, st,
                      x, w1, b1, w2, b2, xs, sw, sb, y, P, tps, tiles, ci, co, skip_kind, act);
   return launch_status("k_channel_mlp");
 }
@@ -416,6 +445,35 @@ int channel_mlp(const float* x, const float* w1, const float* b1, const float* w
   }
 #undef FNO_MLP
   set_error("channel MLP %d -> %d -> %d is not covered by the kernel", Ci, Ch, Co);
+  return FNO_ERR_UNSUPPORTED;
+}
+
+// bfloat16 storage of x (x_bf16) or y (y_bf16), with bf16 products: the
+// lifting widths (Ci <= 4, y bf16) and the projection widths (Co <= 16, x
+// bf16) of the bf16 FNO forward.
+bool channel_mlp_io_supported(int Ci, int Ch, int Co, int64_t P, bool x_bf16, bool y_bf16) {
+  if (!channel_mlp_supported(Ci, Ch, Co, P)) return false;
+  const int v = mlp_variant(Ci, Ch, Co);
+  if (x_bf16 && y_bf16) return false;
+  if (y_bf16) return v == 3 || v == 4;
+  if (x_bf16) return v == 5 || v == 6;
+  return true;
+}
+
+int channel_mlp_io(const void* x, const float* w1, const float* b1, const float* w2,
+                   const float* b2, void* y, int64_t B, int Ci, int Ch, int Co, int64_t P, int act,
+                   bool x_bf16, bool y_bf16, hipStream_t st) {
+#define FNO_MLPIO(ci_, ch_, co_, io)                                                             \
+  launch_mlp<ci_, ch_, co_, true, true, io>(x, w1, b1, w2, b2, nullptr, nullptr, nullptr, y, B, P, \
+                                            Ci, Co, FNO_SKIP_NONE, act, st)
+  const int v = mlp_variant(Ci, Ch, Co);
+  if (y_bf16 && !x_bf16 && v == 3) return FNO_MLPIO(4, 128, 64, 2);
+  if (y_bf16 && !x_bf16 && v == 4) return FNO_MLPIO(4, 64, 32, 2);
+  if (x_bf16 && !y_bf16 && v == 5) return FNO_MLPIO(64, 128, 16, 1);
+  if (x_bf16 && !y_bf16 && v == 6) return FNO_MLPIO(32, 64, 16, 1);
+#undef FNO_MLPIO
+  set_error("channel MLP %d -> %d -> %d with bfloat16 %s is not covered by the kernel", Ci, Ch, Co,
+            x_bf16 ? "input" : "output");
   return FNO_ERR_UNSUPPORTED;
 }
 

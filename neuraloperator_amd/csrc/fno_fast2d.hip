@@ -57,9 +57,11 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 // region, so a wavefront writes them without waiting for the others.  The
 // column stage exchanges its partial DFTs through the spectrum entries it has
 // just read.
-template <int H, int W, int KPR>
+// BF: x is bfloat16 (the activation storage of the bf16 FNO forward), widened
+// to fp32 as it is staged; everything after that is the same.
+template <int H, int W, int KPR, bool BF = false>
 __global__ void __launch_bounds__(16 * LinePlan<W>::T)
-k_fwd_stream(const float* __restrict__ x, float2* __restrict__ xhat, int m1, int m2h, float scale) {
+k_fwd_stream(const void* __restrict__ x, float2* __restrict__ xhat, int m1, int m2h, float scale) {
   using PW = LinePlan<W>;
   constexpr int T = PW::T, R = PW::R, Q = PW::Q;
   constexpr int D = H / 32;
@@ -87,7 +89,8 @@ k_fwd_stream(const float* __restrict__ x, float2* __restrict__ xhat, int m1, int
 
   const int tid = threadIdx.x;
   const int L = tid / T, t = tid % T;     // line of the chunk, lane in the line
-  const float* xp = x + (int64_t)blockIdx.x * H * W;
+  constexpr int ES = BF ? 2 : 4;              // bytes per element of x
+  const char* xp = static_cast<const char*>(x) + (int64_t)blockIdx.x * H * W * ES;
 
   // column stage roles: 4 lanes per kept column
   const int col = tid >> 2, j = tid & 3;
@@ -105,22 +108,23 @@ k_fwd_stream(const float* __restrict__ x, float2* __restrict__ xhat, int m1, int
   // loads 4 float4 of each row (16 lanes x 16 B = 256 contiguous bytes per
   // load instruction) one chunk ahead; at the chunk they are staged in the
   // line's own LDS slice and read back in the FFT's stride-T layout.
-  constexpr int NF4 = W / (4 * T);   // float4 per lane and row
-  static_assert(NF4 * 4 * T == W, "row split");
+  constexpr int EPL = 16 / ES;        // elements per 16-byte load
+  constexpr int NF4 = W / (EPL * T);  // 16-byte loads per lane and row
+  static_assert(NF4 * EPL * T == W, "row split");
   const __amdgpu_buffer_rsrc_t rxp = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float*>(xp), (short)0, H * W * 4, 0x00020000);
+      const_cast<char*>(xp), (short)0, H * W * ES, 0x00020000);
   // cache policy 2 = non-temporal (nt): x streams through once here, and
   // keeping it out of the caches' recent set measured 17 us faster at
   // B32 C64 256^2 (the caches keep what the following kernels reuse)
   constexpr int kNT = 2;
   auto load_rows = [&](uint32_t row, int lt, float4 (&dst)[2 * NF4]) __attribute__((always_inline)) {
-    const uint32_t off = (row * W + 4 * lt) * 4u;
+    const uint32_t off = (row * W + EPL * lt) * (uint32_t)ES;
 #pragma unroll
     for (int k = 0; k < NF4; ++k) {
       dst[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
                                               rxp, (int)(off + 16u * T * k), 0, kNT));
       dst[NF4 + k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                    rxp, (int)(off + 16u * T * k), D * W * 4, kNT));
+                                                    rxp, (int)(off + 16u * T * k), D * W * ES, kNT));
     }
   };
   // Chunk order: workgroups that share an XCD (ids 8 apart) start at
@@ -145,8 +149,21 @@ k_fwd_stream(const float* __restrict__ x, float2* __restrict__ xhat, int m1, int
       float* exf = reinterpret_cast<float*>(exl);   // rows a | b
 #pragma unroll
       for (int k = 0; k < NF4; ++k) {
-        reinterpret_cast<float4*>(exf)[tt + T * k] = xs4[k];
-        reinterpret_cast<float4*>(exf + W)[tt + T * k] = xs4[NF4 + k];
+        if constexpr (BF) {
+          // 8 bf16 of pixels 8 (tt + T k) .. + 7: widen (bits << 16)
+          auto widen = [](float4 p, float4* d) __attribute__((always_inline)) {
+            const uint4 u = __builtin_bit_cast(uint4, p);
+            d[0] = make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                               __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u));
+            d[1] = make_float4(__uint_as_float(u.z << 16), __uint_as_float(u.z & 0xffff0000u),
+                               __uint_as_float(u.w << 16), __uint_as_float(u.w & 0xffff0000u));
+          };
+          widen(xs4[k], reinterpret_cast<float4*>(exf) + 2 * (tt + T * k));
+          widen(xs4[NF4 + k], reinterpret_cast<float4*>(exf + W) + 2 * (tt + T * k));
+        } else {
+          reinterpret_cast<float4*>(exf)[tt + T * k] = xs4[k];
+          reinterpret_cast<float4*>(exf + W)[tt + T * k] = xs4[NF4 + k];
+        }
       }
       if (cs + 1 < D)  // next chunk's rows in flight during this chunk
         load_rows((uint32_t)(((c + 1) & (D - 1)) + D * (2 * Ll)), tt, xs4);
@@ -878,9 +895,10 @@ int rowsynth_epilogue(const float* x, const float2* yhat, const float* skip_w, c
                       int act, float s, hipStream_t st);
 bool rowsynth_mlp_covers(int H, int W, int Ci, int Co, int m1, int m2h, int hidden,
                          int skip_kind);
-int rowsynth_mlp_epilogue(const float* x, const float2* yhat, const float* skip_w,
-                          const float* bias, float* y, int B, int H, int W, int m1, int m2h,
-                          int skip_kind, int act, float s, const LayerMlp& mlp, hipStream_t st);
+int rowsynth_mlp_epilogue(const void* x, const float2* yhat, const float* skip_w,
+                          const float* bias, void* y, int B, int H, int W, int m1, int m2h,
+                          int skip_kind, int act, float s, const LayerMlp& mlp, bool bf,
+                          hipStream_t st);
 int contract_dense(const float2* X, const float2* W, float2* Y, int B, int Ci, int Co, int64_t M,
                    int64_t sWi, int64_t sWo, int64_t sWk, hipStream_t st, int ymap_w);
 int rfft_window(const float* x, float2* xhat, int64_t planes, int32_t ndim, const int32_t* sizes,
@@ -972,6 +990,12 @@ bool fast2d_supported(int B, int Ci, int Co, int ndim, const int32_t* sizes, con
   return epi_supported(H, W, Ci, Co, modes[0], modes[1], skip_kind);
 }
 
+// bfloat16 activation storage (the one-pass layer only) needs the streamed
+// forward, which reads x as stored.
+bool fast2d_bf16_supported(const int32_t* sizes, const int32_t* modes) {
+  return fwd_supported(sizes[0], sizes[1], modes[0], modes[1]);
+}
+
 // The inverse column transform Z [B][Co][H][m2h] lives in the workspace only
 // when the epilogue reads it; the row-synthesis epilogue builds it on chip.
 static bool uses_z(int Ci, int Co, const int32_t* sizes, const int32_t* modes) {
@@ -996,32 +1020,35 @@ static int allow_lds(K kernel, size_t bytes) {
                     "hipFuncSetAttribute(MaxDynamicSharedMemorySize)");
 }
 
-template <int H, int W, int KPR>
-static int launch_fwd(const float* x, float2* xhat, int64_t planes, int m1, int m2h, float scale,
+template <int H, int W, int KPR, bool BF>
+static int launch_fwd(const void* x, float2* xhat, int64_t planes, int m1, int m2h, float scale,
                       hipStream_t st) {
   constexpr int BLOCK = 16 * (W >= 256 ? 16 : 8);
   const size_t lds = fwd_lds_bytes(H, W, m2h);
-  int rc = allow_lds(k_fwd_stream<H, W, KPR>, lds);
+  int rc = allow_lds(k_fwd_stream<H, W, KPR, BF>, lds);
   if (rc) return rc;
-  hipLaunchKernelGGL((k_fwd_stream<H, W, KPR>), dim3((unsigned)planes), dim3(BLOCK), lds, st, x,
-                     xhat, m1, m2h, scale);
+  hipLaunchKernelGGL((k_fwd_stream<H, W, KPR, BF>), dim3((unsigned)planes), dim3(BLOCK), lds, st,
+                     x, xhat, m1, m2h, scale);
   return launch_status("k_fwd_stream");
 }
 
-template <int H, int W>
-static int launch_fwd_k(const float* x, float2* xhat, int64_t planes, int m1, int m2h, float scale,
+template <int H, int W, bool BF>
+static int launch_fwd_k(const void* x, float2* xhat, int64_t planes, int m1, int m2h, float scale,
                         hipStream_t st) {
   switch (fwd_kpr(m1)) {
-    case 1: return launch_fwd<H, W, 1>(x, xhat, planes, m1, m2h, scale, st);
-    case 2: return launch_fwd<H, W, 2>(x, xhat, planes, m1, m2h, scale, st);
-    default: return launch_fwd<H, W, 4>(x, xhat, planes, m1, m2h, scale, st);
+    case 1: return launch_fwd<H, W, 1, BF>(x, xhat, planes, m1, m2h, scale, st);
+    case 2: return launch_fwd<H, W, 2, BF>(x, xhat, planes, m1, m2h, scale, st);
+    default: return launch_fwd<H, W, 4, BF>(x, xhat, planes, m1, m2h, scale, st);
   }
 }
 
-static int dispatch_fwd(int H, int W, const float* x, float2* xhat, int64_t planes, int m1, int m2h,
-                        float scale, hipStream_t st) {
-#define FNO_FWD(h, w) \
-  if (H == h && W == w) return launch_fwd_k<h, w>(x, xhat, planes, m1, m2h, scale, st);
+// bf: x bfloat16 (else float32)
+static int dispatch_fwd(int H, int W, const void* x, float2* xhat, int64_t planes, int m1, int m2h,
+                        float scale, hipStream_t st, bool bf = false) {
+#define FNO_FWD(h, w)                                                                     \
+  if (H == h && W == w)                                                                   \
+    return bf ? launch_fwd_k<h, w, true>(x, xhat, planes, m1, m2h, scale, st)             \
+              : launch_fwd_k<h, w, false>(x, xhat, planes, m1, m2h, scale, st);
   FNO_FWD(64, 128) FNO_FWD(128, 128) FNO_FWD(256, 128)
   FNO_FWD(64, 256) FNO_FWD(128, 256) FNO_FWD(256, 256)
 #undef FNO_FWD
@@ -1163,10 +1190,11 @@ static int dispatch_epi(int W, int Co, int Ci, const float* x, const float2* z,
   return FNO_ERR_UNSUPPORTED;
 }
 
-int fast2d_block(const float* x, const float2* w, const float* bias, const float* skip_w, float* y,
+// bf (with a channel MLP only): x and y are bfloat16.
+int fast2d_block(const void* x, const float2* w, const float* bias, const float* skip_w, void* y,
                  int B, int Ci, int Co, const int32_t* sizes, const int32_t* modes, int norm,
                  int skip_kind, int act, void* ws, size_t ws_bytes, hipStream_t st,
-                 const LayerMlp* mlp) {
+                 const LayerMlp* mlp, bool bf) {
   const int H = sizes[0], W = sizes[1], m1 = modes[0], m2h = modes[1];
   const int64_t M = (int64_t)m1 * m2h;
   const size_t need = fast2d_workspace(B, Ci, Co, sizes, modes);
@@ -1181,12 +1209,16 @@ int fast2d_block(const float* x, const float2* w, const float* bias, const float
   const float fscale = (float)forward_scale(norm, sz, 2);
   const float iscale = (float)inverse_scale(norm, sz, 2);
   int rc;
+  if (bf && (!mlp || !fwd_supported(H, W, m1, m2h))) {
+    set_error("fused 2D block: bfloat16 activations need the one-pass layer's shapes");
+    return FNO_ERR_UNSUPPORTED;
+  }
   if (fwd_supported(H, W, m1, m2h)) {
-    rc = dispatch_fwd(H, W, x, xhat, (int64_t)B * Ci, m1, m2h, fscale, st);
+    rc = dispatch_fwd(H, W, x, xhat, (int64_t)B * Ci, m1, m2h, fscale, st, bf);
   } else {
     // the generic forward's scratch goes where Z lives later
     void* rest = zbuf;
-    rc = rfft_window(x, xhat, (int64_t)B * Ci, 2, sizes, modes, norm, rest,
+    rc = rfft_window(static_cast<const float*>(x), xhat, (int64_t)B * Ci, 2, sizes, modes, norm, rest,
                      ws_bytes - (size_t)((int64_t)B * (Ci + Co) * M) * sizeof(float2), st);
   }
   if (rc) return rc;
@@ -1199,16 +1231,18 @@ int fast2d_block(const float* x, const float2* w, const float* bias, const float
   if (rc) return rc;
   if (mlp)
     return rowsynth_mlp_epilogue(x, yhat, skip_w, bias, y, B, H, W, m1, m2h, skip_kind, act,
-                                 iscale, *mlp, st);
+                                 iscale, *mlp, bf, st);
+  const float* xf = static_cast<const float*>(x);
+  float* yf = static_cast<float*>(y);
   if (rsyn)
-    return rowsynth_epilogue(x, yhat, skip_w, bias, y, B, Ci, H, W, m1, m2h, skip_kind, act,
+    return rowsynth_epilogue(xf, yhat, skip_w, bias, yf, B, Ci, H, W, m1, m2h, skip_kind, act,
                              iscale, st);
   rc = dispatch_inv(H, yhat, zbuf, B, Co, m1, m2h, st);
   if (rc) return rc;
   if (epi_r_supported(H, W, Ci, Co, m2h, skip_kind))
-    return dispatch_epi_r(W, Co, Ci, x, zbuf, skip_w, bias, y, B, H, m2h, skip_kind, act, iscale,
+    return dispatch_epi_r(W, Co, Ci, xf, zbuf, skip_w, bias, yf, B, H, m2h, skip_kind, act, iscale,
                           st);
-  return dispatch_epi(W, Co, Ci, x, zbuf, skip_w, bias, y, B, H, m2h, skip_kind, act, iscale, st);
+  return dispatch_epi(W, Co, Ci, xf, zbuf, skip_w, bias, yf, B, H, m2h, skip_kind, act, iscale, st);
 }
 
 }  // namespace fno

@@ -24,10 +24,10 @@
 
 namespace fno {
 void clear_error();
-int spectral_block_check(const float* x, const void* w, float* y, int32_t batch,
+int spectral_block_check(const void* x, const void* w, void* y, int32_t batch,
                          int32_t in_channels, int32_t out_channels, int32_t ndim,
                          const int32_t* sizes, const int32_t* modes, int32_t norm,
-                         int32_t skip_kind, int32_t act, const float* skip_weight);
+                         int32_t skip_kind, int32_t act, const float* skip_weight, size_t es);
 int spectral_block_run(const float* x, const void* w, const float* bias, const float* skip_weight,
                        float* y, int32_t batch, int32_t in_channels, int32_t out_channels,
                        int32_t ndim, const int32_t* sizes, const int32_t* modes, int32_t norm,
@@ -100,7 +100,7 @@ int fno_spectral_block_f32_noalloc(const float* x, const void* w, const float* b
                                    int32_t skip_kind, int32_t act, void* stream) {
   clear_error();
   int rc = spectral_block_check(x, w, y, batch, in_channels, out_channels, ndim, sizes, modes, norm,
-                                skip_kind, act, skip_weight);
+                                skip_kind, act, skip_weight, sizeof(float));
   if (rc) return rc;
   constexpr size_t cap = FNO_NOALLOC_SCRATCH_BYTES;
   const size_t one = fno_spectral_block_workspace_bytes(1, in_channels, out_channels, ndim, sizes,

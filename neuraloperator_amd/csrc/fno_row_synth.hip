@@ -103,12 +103,28 @@ static constexpr int kSynthMaxM1 = 128;   // window rows of the LDS twiddle tabl
 #define SYN_BATCH 8                      // window rows whose loads are issued together
 #endif
 
-template <int W, int CI, int KSZ, bool XSKIP, bool MLP>
+// BF: x and y are bfloat16 (activation storage of the bf16 FNO forward); x
+// is then exact in one bf16 term, so the skip and gate products take two
+// matrix products instead of three, and y is rounded to bf16 (nearest even)
+// at the store.
+template <bool BF> struct RowIO;
+template <> struct RowIO<false> {
+  typedef float T;        // element
+  typedef float2 Pair;    // the two pixels of a lane
+};
+template <> struct RowIO<true> {
+  typedef __bf16 T;
+  typedef uint32_t Pair;  // two bf16, pixel col0 in the low half
+};
+
+template <int W, int CI, int KSZ, bool XSKIP, bool MLP, bool BF>
 __global__ void __launch_bounds__(rg::kThreads)
-k_row_synth(const float* __restrict__ x, const float2* __restrict__ yhat,
+k_row_synth(const typename RowIO<BF>::T* __restrict__ x, const float2* __restrict__ yhat,
             const float* __restrict__ skip_w, const float* __restrict__ bias,
-            float* __restrict__ y, int B, int H, int m1, int m2h, int skip_kind, int act,
-            float s, int xcd_map, LayerMlp mlp) {
+            typename RowIO<BF>::T* __restrict__ y, int B, int H, int m1, int m2h, int skip_kind,
+            int act, float s, int xcd_map, LayerMlp mlp) {
+  using XPair = typename RowIO<BF>::Pair;
+  constexpr uint32_t ES = sizeof(typename RowIO<BF>::T);   // bytes per element
   constexpr int R = rs::R;
   constexpr int ROWS = rg::kStepPx / W;          // rows per step
   constexpr int WPR = rg::kWaves / ROWS;         // waves per row
@@ -219,12 +235,12 @@ k_row_synth(const float* __restrict__ x, const float2* __restrict__ yhat,
 
   // ---- x operand of rows (h, h + 1 at W = 128): channel 32 ks + 8 G + i,
   //      pixels col0, col0 + 1 of row h + wrow
-  const uint32_t xbytes = (uint32_t)CI * HW * 4u;
-  const uint32_t xvoff = ((uint32_t)(8 * G) * HW + (uint32_t)(wrow * NR * W + col0)) * 4u;
-  float2 xa[KX][8], xb[KX][8];
+  const uint32_t xbytes = (uint32_t)CI * HW * ES;
+  const uint32_t xvoff = ((uint32_t)(8 * G) * HW + (uint32_t)(wrow * NR * W + col0)) * ES;
+  XPair xa[KX][8], xb[KX][8];
   // row of step t of a block: steps pair rows t, t + 1 of the block at W = 128
   auto step_row = [&](int r, int t) __attribute__((always_inline)) { return r + NR * t; };
-  auto load_x = [&](int b, int h, float2 (&dst)[KX][8]) __attribute__((always_inline)) {
+  auto load_x = [&](int b, int h, XPair (&dst)[KX][8]) __attribute__((always_inline)) {
     if constexpr (XSKIP) {
       const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + (int64_t)b * CI * HW, xbytes);
       // rows h (waves of row 0) and h + NR (row 1 of the step at W = 128)
@@ -233,15 +249,26 @@ k_row_synth(const float* __restrict__ x, const float2* __restrict__ yhat,
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           const int soff = __builtin_amdgcn_readfirstlane(
-              (int)(((uint32_t)(32 * ks + i) * HW + (uint32_t)h * W) * 4u));
-          dst[ks][i] = __builtin_bit_cast(
-              float2, __builtin_amdgcn_raw_buffer_load_b64(rx, (int)xvoff, soff, 0));
+              (int)(((uint32_t)(32 * ks + i) * HW + (uint32_t)h * W) * ES));
+          if constexpr (BF)
+            dst[ks][i] = __builtin_amdgcn_raw_buffer_load_b32(rx, (int)xvoff, soff, 0);
+          else
+            dst[ks][i] = __builtin_bit_cast(
+                float2, __builtin_amdgcn_raw_buffer_load_b64(rx, (int)xvoff, soff, 0));
         }
     }
   };
 
   // ---- one step: rows t0 (+1) of the block in zf / cinit
-  auto compute_store = [&](int b, int h, int t0, const float2 (&xc)[KX][8])
+  // bf16 hi / lo parts of pixel u of an x pair (lo = 0 for bf16 x)
+  auto split_x = [&](const XPair& p, int u) __attribute__((always_inline)) -> bf16x2 {
+    if constexpr (BF)
+      return {__builtin_bit_cast(__bf16, (unsigned short)(u ? (p >> 16) : (p & 0xffffu))),
+              (__bf16)0.f};
+    else
+      return split_bf16(u ? p.y : p.x);
+  };
+  auto compute_store = [&](int b, int h, int t0, const XPair (&xc)[KX][8])
       __attribute__((always_inline)) {
     const int t = t0 + wrow;
     v4f acc[4][2];
@@ -260,15 +287,16 @@ k_row_synth(const float* __restrict__ x, const float2* __restrict__ yhat,
           v8bf bh, bl;
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
-            const bf16x2 p = split_bf16(u ? xc[ks][i].y : xc[ks][i].x);
-            bh[i] = p.hi;
-            bl[i] = p.lo;
+            const bf16x2 q = split_x(xc[ks][i], u);
+            bh[i] = q.hi;
+            bl[i] = q.lo;
           }
 #pragma unroll
           for (int ot = 0; ot < 4; ++ot) {
             const v8bf wh = wf[((ot * KSX + ks) * 2) * 64 + lane];
             const v8bf wl = wf[((ot * KSX + ks) * 2 + 1) * 64 + lane];
-            acc[ot][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wh, bl, acc[ot][u], 0, 0, 0);
+            if constexpr (!BF)
+              acc[ot][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wh, bl, acc[ot][u], 0, 0, 0);
             acc[ot][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wl, bh, acc[ot][u], 0, 0, 0);
             acc[ot][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wh, bh, acc[ot][u], 0, 0, 0);
           }
@@ -346,9 +374,9 @@ k_row_synth(const float* __restrict__ x, const float2* __restrict__ yhat,
           v8bf bh, bl;
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
-            const bf16x2 p = split_bf16(u ? xc[ks][i].y : xc[ks][i].x);
-            bh[i] = p.hi;
-            bl[i] = p.lo;
+            const bf16x2 q = split_x(xc[ks][i], u);
+            bh[i] = q.hi;
+            bl[i] = q.lo;
           }
 #pragma unroll
           for (int t = 0; t < 2; ++t) {
@@ -361,7 +389,8 @@ k_row_synth(const float* __restrict__ x, const float2* __restrict__ yhat,
               gh[i] = (i == (m16 & 7)) ? g.hi : (__bf16)0.f;
               gl[i] = (i == (m16 & 7)) ? g.lo : (__bf16)0.f;
             }
-            acc[ot][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(gh, bl, acc[ot][u], 0, 0, 0);
+            if constexpr (!BF)
+              acc[ot][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(gh, bl, acc[ot][u], 0, 0, 0);
             acc[ot][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(gl, bh, acc[ot][u], 0, 0, 0);
             acc[ot][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(gh, bh, acc[ot][u], 0, 0, 0);
           }
@@ -375,9 +404,9 @@ k_row_synth(const float* __restrict__ x, const float2* __restrict__ yhat,
       }
     }
     const __amdgpu_buffer_rsrc_t ry = make_rsrc(y + (int64_t)b * rg::kCo * HW,
-                                                (uint32_t)rg::kCo * HW * 4u);
+                                                (uint32_t)rg::kCo * HW * ES);
     const uint32_t yvoff =
-        ((uint32_t)(4 * G) * HW + (uint32_t)(wrow * NR * W + col0)) * 4u;
+        ((uint32_t)(4 * G) * HW + (uint32_t)(wrow * NR * W + col0)) * ES;
 #pragma unroll
     for (int ot = 0; ot < 4; ++ot)
 #pragma unroll
@@ -386,10 +415,16 @@ k_row_synth(const float* __restrict__ x, const float2* __restrict__ yhat,
         v0 = act_select(gelu_erf(v0), v0, gmask);
         v1 = act_select(gelu_erf(v1), v1, gmask);
         const int soff = __builtin_amdgcn_readfirstlane(
-            (int)(((uint32_t)(16 * ot + r) * HW + (uint32_t)h * W) * 4u));
-        __builtin_amdgcn_raw_buffer_store_b64(
-            __builtin_bit_cast(__attribute__((ext_vector_type(2))) int, make_float2(v0, v1)), ry,
-            (int)yvoff, soff, 0);
+            (int)(((uint32_t)(16 * ot + r) * HW + (uint32_t)h * W) * ES));
+        if constexpr (BF) {
+          const uint32_t lo = __builtin_bit_cast(unsigned short, (__bf16)v0);
+          const uint32_t hi = __builtin_bit_cast(unsigned short, (__bf16)v1);
+          __builtin_amdgcn_raw_buffer_store_b32(lo | (hi << 16), ry, (int)yvoff, soff, 0);
+        } else {
+          __builtin_amdgcn_raw_buffer_store_b64(
+              __builtin_bit_cast(__attribute__((ext_vector_type(2))) int, make_float2(v0, v1)),
+              ry, (int)yvoff, soff, 0);
+        }
       }
   };
 
@@ -566,13 +601,13 @@ bool rowsynth_covers(int H, int W, int Ci, int Co, int m1, int m2h) {
   return rowsynth_lds_bytes(rowgemm_ksz(m2h), 2) <= 160 * 1024;
 }
 
-template <int W, int CI, int KSZ, bool XSKIP, bool MLP = false>
-static int launch_rowsynth(const float* x, const float2* yhat, const float* skip_w,
-                           const float* bias, float* y, int B, int H, int m1, int m2h,
+template <int W, int CI, int KSZ, bool XSKIP, bool MLP = false, bool BF = false>
+static int launch_rowsynth(const typename RowIO<BF>::T* x, const float2* yhat, const float* skip_w,
+                           const float* bias, typename RowIO<BF>::T* y, int B, int H, int m1, int m2h,
                            int skip_kind, int act, float s, hipStream_t st,
                            const LayerMlp& mlp = LayerMlp{}) {
   const size_t lds = rowsynth_lds_bytes(KSZ, XSKIP ? CI / 32 : 0, MLP);
-  auto kern = k_row_synth<W, CI, KSZ, XSKIP, MLP>;
+  auto kern = k_row_synth<W, CI, KSZ, XSKIP, MLP, BF>;
   if (lds > 64 * 1024) {
     int rc = hip_status(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
@@ -625,15 +660,19 @@ bool rowsynth_mlp_covers(int H, int W, int Ci, int Co, int m1, int m2h, int hidd
   return rowsynth_lds_bytes(rowgemm_ksz(m2h), 2, true) <= 160 * 1024;
 }
 
-int rowsynth_mlp_epilogue(const float* x, const float2* yhat, const float* skip_w,
-                          const float* bias, float* y, int B, int H, int W, int m1, int m2h,
-                          int skip_kind, int act, float s, const LayerMlp& mlp, hipStream_t st) {
+// bf: x and y bfloat16 (else float32).
+int rowsynth_mlp_epilogue(const void* x, const float2* yhat, const float* skip_w,
+                          const float* bias, void* y, int B, int H, int W, int m1, int m2h,
+                          int skip_kind, int act, float s, const LayerMlp& mlp, bool bf,
+                          hipStream_t st) {
   const int ksz = rowgemm_ksz(m2h);
-#define FNO_RSM(w, k)                                                                              \
-  if (W == w && ksz == k)                                                                          \
-    return launch_rowsynth<w, 64, k, true, true>(x, yhat, skip_w, bias, y, B, H, m1, m2h,         \
-                                                 skip_kind, act, s, st, mlp);
-  FNO_RSM(128, 1) FNO_RSM(128, 2) FNO_RSM(256, 1) FNO_RSM(256, 2)
+#define FNO_RSM(w, k, b)                                                                           \
+  if (W == w && ksz == k && bf == b)                                                               \
+    return launch_rowsynth<w, 64, k, true, true, b>(                                               \
+        static_cast<const typename RowIO<b>::T*>(x), yhat, skip_w, bias,                           \
+        static_cast<typename RowIO<b>::T*>(y), B, H, m1, m2h, skip_kind, act, s, st, mlp);
+  FNO_RSM(128, 1, false) FNO_RSM(128, 2, false) FNO_RSM(256, 1, false) FNO_RSM(256, 2, false)
+  FNO_RSM(128, 1, true) FNO_RSM(128, 2, true) FNO_RSM(256, 1, true) FNO_RSM(256, 2, true)
 #undef FNO_RSM
   set_error("row epilogue with channel MLP: unsupported W=%d m2h=%d", W, m2h);
   return FNO_ERR_UNSUPPORTED;

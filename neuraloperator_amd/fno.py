@@ -6,9 +6,12 @@ from __future__ import annotations
 import warnings
 from typing import List, Literal, Tuple, Union
 
+import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from . import _native as nat
+from . import functional as Fh
 from .channel_mlp import ChannelMLP
 from .embeddings import GridEmbeddingND
 from .complex import ComplexValued
@@ -142,8 +145,9 @@ class FNO(nn.Module):
         if self.positional_embedding is not None:
             with maybe_profile(profiler, "fno/positional_embedding", x.device):
                 x = self.positional_embedding(x)
+        bf16_io = self._bf16_storage(x, output_shape)
         with maybe_profile(profiler, "fno/lifting", x.device):
-            x = self.lifting(x)
+            x = self._mlp_bf16(self.lifting, x, y_bf16=True) if bf16_io else self.lifting(x)
         if self.domain_padding is not None:
             with maybe_profile(profiler, "fno/domain_padding/pad", x.device):
                 x = self.domain_padding.pad(x)
@@ -153,8 +157,49 @@ class FNO(nn.Module):
             with maybe_profile(profiler, "fno/domain_padding/unpad", x.device):
                 x = self.domain_padding.unpad(x)
         with maybe_profile(profiler, "fno/projection", x.device):
-            x = self.projection(x)
+            if x.dtype == torch.bfloat16 and self._mlp_io_ok(self.projection, x, x_bf16=True):
+                x = self._mlp_bf16(self.projection, x, y_bf16=False)
+            else:
+                x = self.projection(x.float() if bf16_io else x)
         return x
+
+    # ---- bf16 activation storage: under torch.autocast(dtype=bfloat16),
+    # without gradients, when the layers run as one-pass bf16 layers
+    # (fno_layer_bf16), the activations from the lifting to the projection
+    # are kept in bfloat16: every layer reads and writes half the bytes.  The
+    # arithmetic is that of the fp32 autocast forward, on values rounded to
+    # bf16 at each layer boundary (the lifting's output is bf16 in the
+    # reference's autocast forward too: a Conv1d output).
+    def _mlp_io_ok(self, mlp, x, x_bf16=False, y_bf16=False) -> bool:
+        if not isinstance(mlp, ChannelMLP) or mlp.n_layers != 2 or mlp.dropout is not None:
+            return False
+        if mlp.non_linearity is not F.gelu:
+            return False
+        P = 1
+        for s in x.shape[2:]:
+            P *= s
+        return Fh.channel_mlp_io_is_supported(mlp.in_channels, mlp.hidden_channels,
+                                              mlp.out_channels, P, x_bf16, y_bf16)
+
+    def _bf16_storage(self, x, output_shape) -> bool:
+        if not x.is_cuda or x.is_complex() or not Fh.autocast_bf16(x.device.type):
+            return False
+        if torch.is_grad_enabled() and (x.requires_grad or
+                                        any(p.requires_grad for p in self.parameters())):
+            return False
+        if self.domain_padding is not None or any(o is not None for o in output_shape):
+            return False
+        if not self._mlp_io_ok(self.lifting, x, y_bf16=True):
+            return False
+        return self.fno_blocks.bf16_layer_ok(x.shape[0], x.shape[2:], 0)
+
+    @staticmethod
+    def _mlp_bf16(mlp, x, y_bf16):
+        fc0, fc1 = mlp.fcs
+        d = lambda t: None if t is None else t.detach()
+        return Fh.channel_mlp_io(x.detach(), d(fc0.weight).reshape(fc0.out_channels, -1),
+                                 d(fc0.bias), d(fc1.weight).reshape(fc1.out_channels, -1),
+                                 d(fc1.bias), nat.ACT_NONE, y_bf16)
 
     @property
     def n_modes(self):

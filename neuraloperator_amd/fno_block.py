@@ -270,7 +270,8 @@ class FNOBlocks(nn.Module):
         """(skip_kind, gate) when the channel MLP, its skip and the second
         activation of this layer can run as one fno_channel_mlp_f32 call, else
         None."""
-        if not self.use_channel_mlp or not x.is_cuda or x.dtype != torch.float32:
+        if not self.use_channel_mlp or not x.is_cuda or x.dtype not in (torch.float32,
+                                                                        torch.bfloat16):
             return None
         if _needs_grad(self, x):
             return None
@@ -291,6 +292,11 @@ class FNOBlocks(nn.Module):
         if not Fh.channel_mlp_is_supported(mlp.in_channels, mlp.hidden_channels, mlp.out_channels, P,
                                            x):
             return None
+        return self._mlp_skip(index)
+
+    def _mlp_skip(self, index):
+        """(skip_kind, gate) of the channel-MLP skip if a kernel can apply it."""
+        conv = self.convs[index]
         if self.channel_mlp_skips is None:
             return nat.SKIP_NONE, None
         sk = self.channel_mlp_skips[index]
@@ -300,16 +306,44 @@ class FNOBlocks(nn.Module):
             return nat.SKIP_IDENTITY, None
         return None
 
+    def bf16_layer_ok(self, batch, sizes, index=0) -> bool:
+        """True if layer `index` runs as one fno_layer_bf16 call for a
+        bfloat16 input [batch, C, *sizes] (under a bf16 autocast, without
+        gradients): the structure _fused_layer needs, checked without a
+        tensor, so FNO can choose bf16 activation storage up front."""
+        if not self.use_channel_mlp or self.norm is not None or self.non_linearity is not F.gelu:
+            return False
+        if self.stabilizer is not None or self.preactivation:
+            return False
+        conv = self.convs[index]
+        if not isinstance(conv, SpectralConv) or conv.resolution_scaling_factor is not None:
+            return False
+        if (conv.separable or conv.complex_data or conv._contract not in ("dense", "cp", "tt")
+                or conv.in_channels != conv.out_channels):
+            return False
+        mlp = self.channel_mlp[index]
+        if (mlp.n_layers != 2 or mlp.non_linearity is not F.gelu or mlp.dropout is not None
+                or mlp.in_channels != conv.out_channels):
+            return False
+        kind, _ = self._fused_skip(index)
+        mskip = self._mlp_skip(index)
+        if kind is None or mskip is None:
+            return False
+        kept, _ = conv.window(list(sizes))
+        return Fh.layer_is_fused(batch, conv.out_channels, mlp.hidden_channels, list(sizes), kept,
+                                 kind, mskip[0], bf16=True)
+
     def _fused_layer(self, x, index, fused_mlp):
         """The whole layer (spectral block, its skip and activation, the
         channel MLP, its skip and the second activation) as one fno_layer_f32
-        call, for the bf16-autocast forward; None where that kernel does not
-        cover the layer."""
+        call, for the bf16-autocast forward (fno_layer_bf16, with a bfloat16
+        output, for a bfloat16 x); None where that kernel does not cover the
+        layer."""
         conv = self.convs[index]
         if (conv.separable or conv.complex_data or conv._contract not in ("dense", "cp", "tt")
                 or conv.in_channels != conv.out_channels):
             return None
-        if not Fh.autocast_bf16(x.device.type) or x.dtype != torch.float32:
+        if not Fh.autocast_bf16(x.device.type) or x.dtype not in (torch.float32, torch.bfloat16):
             return None
         kind, sw = self._fused_skip(index)
         mkind, gate = fused_mlp
@@ -317,7 +351,8 @@ class FNOBlocks(nn.Module):
         sizes = list(x.shape[2:])
         kept, sl = conv.window(sizes)
         C, Ch = conv.out_channels, mlp.hidden_channels
-        if not Fh.layer_is_fused(x.shape[0], C, Ch, sizes, kept, kind, mkind):
+        if not Fh.layer_is_fused(x.shape[0], C, Ch, sizes, kept, kind, mkind,
+                                 bf16=x.dtype == torch.bfloat16):
             return None
         fc0, fc1 = mlp.fcs
         d = lambda t: None if t is None else t.detach()
@@ -345,6 +380,11 @@ class FNOBlocks(nn.Module):
                 y = self._fused_layer(x, index, fused_mlp)
             if y is not None:
                 return y
+        if x.dtype == torch.bfloat16:
+            # bf16 activation storage of the FNO forward, for a layer the
+            # one-pass kernel does not cover: continue in fp32
+            x = x.float()
+            fused_mlp = self._fused_mlp(x, index, output_shape)
         x_in = x
         if self.use_channel_mlp and self.channel_mlp_skips is not None and fused_mlp is None:
             with maybe_profile(profiler, f"{prefix}/channel_mlp_skip", x.device):

@@ -293,10 +293,41 @@ def spectral_block(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.T
     return y
 
 
-def layer_is_fused(B, C, hidden, sizes, modes, skip_kind, mlp_skip_kind) -> bool:
+def channel_mlp_io_is_supported(Ci, Ch, Co, P, x_bf16: bool, y_bf16: bool) -> bool:
     lib = nat.load()
-    return bool(lib.fno_layer_is_fused(B, C, hidden, len(sizes), nat.i32_array(sizes),
-                                       nat.i32_array(modes), skip_kind, mlp_skip_kind))
+    return bool(lib.fno_channel_mlp_io_is_supported(Ci, Ch, Co, P, int(x_bf16), int(y_bf16)))
+
+
+def channel_mlp_io(x: torch.Tensor, w1: torch.Tensor, b1: Optional[torch.Tensor], w2: torch.Tensor,
+                   b2: Optional[torch.Tensor], act: int, y_bf16: bool) -> torch.Tensor:
+    """act(W2 gelu(W1 x + b1) + b2) with bf16 products (fno_channel_mlp_io):
+    x is read as stored (bfloat16 or float32), y is bfloat16 when y_bf16 —
+    the lifting and projection of the bf16 FNO forward."""
+    _require_gpu(x, w1, w2)
+    lib = nat.load()
+    x_bf16 = x.dtype == torch.bfloat16
+    x = x.contiguous() if x_bf16 else _f32(x)
+    B, Ci, *S = x.shape
+    P = 1
+    for s_ in S:
+        P *= s_
+    Ch, Co = w1.shape[0], w2.shape[0]
+    y = torch.empty((B, Co, *S), dtype=torch.bfloat16 if y_bf16 else torch.float32,
+                    device=x.device)
+    w1f, b1f, w2f, b2f = (_f32(t.reshape(-1)) if t is not None else None for t in (w1, b1, w2, b2))
+    nat.check(lib.fno_channel_mlp_io(_ptr(x), _ptr(w1f), _ptr(b1f), _ptr(w2f), _ptr(b2f), _ptr(y), B,
+                                     Ci, Ch, Co, P, act, int(x_bf16), int(bool(y_bf16)),
+                                     _stream(x.device)),
+              "fno_channel_mlp_io")
+    return y
+
+
+def layer_is_fused(B, C, hidden, sizes, modes, skip_kind, mlp_skip_kind, bf16=False) -> bool:
+    """Shapes fno_layer_f32 (bf16: fno_layer_bf16) covers."""
+    lib = nat.load()
+    fn = lib.fno_layer_bf16_is_fused if bf16 else lib.fno_layer_is_fused
+    return bool(fn(B, C, hidden, len(sizes), nat.i32_array(sizes), nat.i32_array(modes), skip_kind,
+                   mlp_skip_kind))
 
 
 def fno_layer(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor],
@@ -306,24 +337,28 @@ def fno_layer(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor
               gate_bias: Optional[torch.Tensor], act: int, fft_norm: str = "forward") -> torch.Tensor:
     """One FNO layer in one pass (fno_layer_f32): act(W2 gelu(W1 y1 + b1) +
     b2 + mlp_skip(x)) with y1 = act(SpectralConv(x) + skip(x)); the MLP
-    products on bf16-rounded operands (the autocast forward)."""
+    products on bf16-rounded operands (the autocast forward).  A bfloat16 x
+    runs fno_layer_bf16 and gives a bfloat16 y (activation storage of the
+    bf16 FNO forward)."""
     _require_gpu(x, weight, bias, skip_weight, w1, w2, gate_weight)
     lib = nat.load()
-    x = _f32(x)
+    bf = x.dtype == torch.bfloat16
+    x = x.contiguous() if bf else _f32(x)
     weight = _c64(weight)
     B, C, *S = x.shape
     nd = len(S)
     hidden = w1.shape[0]
-    y = torch.empty((B, C, *S), dtype=torch.float32, device=x.device)
+    y = torch.empty((B, C, *S), dtype=x.dtype, device=x.device)
     flat = [(_f32(t.reshape(-1)) if t is not None else None)
             for t in (bias, skip_weight, w1, b1, w2, b2, gate_weight, gate_bias)]
     b, sw, w1f, b1f, w2f, b2f, gw, gb = flat
     sz, md = nat.i32_array(S), nat.i32_array(modes)
     wsb = lib.fno_spectral_block_workspace_bytes(B, C, C, nd, sz, md)
     ws = _workspace(wsb, x.device)
-    nat.check(lib.fno_layer_f32(_ptr(x), _ptr(weight), _ptr(b), _ptr(sw), _ptr(w1f), _ptr(b1f),
-                                _ptr(w2f), _ptr(b2f), _ptr(gw), _ptr(gb), _ptr(y), B, C, hidden, nd,
-                                sz, md, nat.NORMS[fft_norm], skip_kind, mlp_skip_kind, act,
-                                _ptr(ws), wsb, _stream(x.device)),
-              "fno_layer_f32")
+    fn = lib.fno_layer_bf16 if bf else lib.fno_layer_f32
+    nat.check(fn(_ptr(x), _ptr(weight), _ptr(b), _ptr(sw), _ptr(w1f), _ptr(b1f), _ptr(w2f),
+                 _ptr(b2f), _ptr(gw), _ptr(gb), _ptr(y), B, C, hidden, nd, sz, md,
+                 nat.NORMS[fft_norm], skip_kind, mlp_skip_kind, act, _ptr(ws), wsb,
+                 _stream(x.device)),
+              "fno_layer_bf16" if bf else "fno_layer_f32")
     return y

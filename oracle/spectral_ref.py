@@ -539,7 +539,7 @@ def domain_unpad(x, pads):
     return x[(Ellipsis,) + tuple(slice(p, -p) if p else slice(None) for p in pads)]
 
 
-def fno_forward(x, params: dict, bf16_products=False):
+def fno_forward(x, params: dict, bf16_products=False, bf16_storage=False):
     """FNO.forward (fno.py:342-408): grid embedding, lifting, domain padding,
     blocks, unpadding, projection.
 
@@ -550,6 +550,10 @@ def fno_forward(x, params: dict, bf16_products=False):
     operands (``channel_mlp``), as their Conv1d layers do under
     torch.autocast(dtype=bfloat16) (training/trainer.py:669-672); the spectral
     path and the block skips stay at full precision.
+    bf16_storage: the activations between the lifting, the layers and the
+    projection are held in bfloat16 (``bf16_round`` of the lifting's and each
+    layer's output), the storage of the bf16 FNO forward; the lifting output
+    is a Conv1d output, bf16 under the reference's autocast as well.
     """
     complex_data = params.get("complex_data", False)
 
@@ -562,6 +566,8 @@ def fno_forward(x, params: dict, bf16_products=False):
     if params.get("positional_embedding", True):
         x = grid_embedding_nd(x)
     x = mlp(params["lifting"], x)
+    if bf16_storage:
+        x = bf16_round(x)
     pads = None
     if params.get("domain_padding") is not None:
         x, pads = domain_pad(x, params["domain_padding"])
@@ -571,6 +577,8 @@ def fno_forward(x, params: dict, bf16_products=False):
                               layer.get("mlp"), layer.get("mlp_skip"),
                               non_linearity=cgelu if complex_data else gelu,
                               bf16_products=bf16_products)
+        if bf16_storage:
+            x = bf16_round(x)
     if pads is not None:
         x = domain_unpad(x, pads)
     return mlp(params["projection"], x)

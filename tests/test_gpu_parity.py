@@ -392,18 +392,25 @@ def test_fno_c3_shape_bf16_input(cuda_device):
     # fp32 accumulation; against the oracle with the same rounding, and
     # against the full-precision oracle at the configuration's 2e-2
     print("fno c3 shape B2 under autocast(bf16)", flush=True)
+    assert model._bf16_storage(x.to(cuda_device).float(), [None] * 4) is False  # gradients on
     with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        xin = model.positional_embedding(x.to(cuda_device).float())
+        assert model._bf16_storage(xin, [None] * 4)     # bf16 activation storage
         ybf = model(x.to(cuda_device).float())
     torch.cuda.synchronize()
     assert ybf.dtype == torch.float32
-    ref_bf = R.fno_forward(x.double(), params, bf16_products=True)
+    # against the oracle that rounds the operands the kernels round and stores
+    # the activations between layers in bf16, and against the fp32 oracle
+    ref_bf = R.fno_forward(x.double(), params, bf16_products=True, bf16_storage=True)
+    ref_p = R.fno_forward(x.double(), params, bf16_products=True)
     err_bf = rel_err(ybf, ref_bf)
-    print(f"autocast: vs rounded oracle {err_bf:.2e}, vs fp32 oracle {rel_err(ybf, ref):.2e}",
-          flush=True)
+    print(f"autocast: vs rounded oracle {err_bf:.2e}, vs products-only oracle "
+          f"{rel_err(ybf, ref_p):.2e}, vs fp32 oracle {rel_err(ybf, ref):.2e}", flush=True)
     assert err_bf <= 2e-2
     assert rel_err(ybf, ref) <= 2e-2
-    # the rounded oracle is the closer one: the kernels round the operands it rounds
-    assert (ybf.double().cpu() - ref_bf).abs().mean() < (ybf.double().cpu() - ref).abs().mean()
+    # the rounded oracle is the closest: the kernels round what it rounds
+    dev_of = lambda r: (ybf.double().cpu() - r).abs().mean()
+    assert dev_of(ref_bf) < dev_of(ref_p) and dev_of(ref_bf) < dev_of(ref)
 
 
 def test_c0_workload_full_size(cuda_device):
@@ -1356,6 +1363,58 @@ def test_fused_fno_layer(B, H, W, nm, skip, gate, act, cuda_device):
     print(f"  vs composed {err_c:.2e}, vs rounded oracle {err:.2e}", flush=True)
     assert err_c <= 2e-3
     assert err <= 2e-2
+    # bfloat16 storage (fno_layer_bf16): a bf16 x is exact in one bf16 term,
+    # so the layer on it is the fp32 layer on the widened x, rounded to bf16
+    # (nearest even) at the store -- bit for bit
+    xb = dev(x).to(torch.bfloat16)
+    if not Fh.layer_is_fused(B, C, Ch, [H, W], kept, kinds[skip], gkind, bf16=True):
+        assert H not in (64, 128, 256)    # planes without the streamed forward
+        with pytest.raises(RuntimeError, match="no one-pass bfloat16 kernel"):
+            Fh.fno_layer(xb, wwin, bias, kept, kinds[skip], dev(ws), dev(w1), dev(b1), dev(w2),
+                         dev(b2), gkind, dev(gwt), dev(gbt), a)
+        return
+    with torch.no_grad():
+        yb = Fh.fno_layer(xb, wwin, bias, kept, kinds[skip], dev(ws), dev(w1), dev(b1), dev(w2),
+                          dev(b2), gkind, dev(gwt), dev(gbt), a)
+        yw = Fh.fno_layer(xb.float(), wwin, bias, kept, kinds[skip], dev(ws), dev(w1), dev(b1),
+                          dev(w2), dev(b2), gkind, dev(gwt), dev(gbt), a)
+    torch.cuda.synchronize()
+    assert yb.dtype == torch.bfloat16
+    assert torch.equal(yb, yw.to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("B,ci,ch,co,P", [(2, 3, 128, 64, 4096), (3, 4, 64, 32, 1024),
+                                         (2, 64, 128, 1, 4096), (2, 32, 64, 16, 512)])
+def test_channel_mlp_bf16_storage(B, ci, ch, co, P, cuda_device):
+    """fno_channel_mlp_io: the lifting with a bfloat16 output and the
+    projection with a bfloat16 input are the bf16-product channel MLP on the
+    same values, the output rounded to bf16 at the store: bit for bit against
+    fno_channel_mlp_f32 (rounded / on the widened input), and within the
+    rounding of the output against the oracle."""
+    print(f"channel mlp bf16 storage B{B} {ci}->{ch}->{co} P{P}", flush=True)
+    g = torch.Generator().manual_seed(61)
+    w1, b1 = torch.randn(ch, ci, generator=g) / 2, torch.randn(ch, generator=g) / 4
+    w2, b2 = torch.randn(co, ch, generator=g) / 8, torch.randn(co, generator=g) / 4
+    x = torch.randn(B, ci, P, generator=g)
+    d = lambda t: t.to(cuda_device)
+    lifting = ci <= 4
+    assert Fh.channel_mlp_io_is_supported(ci, ch, co, P, not lifting, lifting)
+    assert not Fh.channel_mlp_io_is_supported(ci, ch, co, P, lifting, not lifting)
+    xin = d(x) if lifting else d(x).to(torch.bfloat16)
+    with torch.no_grad():
+        y = Fh.channel_mlp_io(xin, d(w1), d(b1), d(w2), d(b2), nat.ACT_NONE, y_bf16=lifting)
+        yf = Fh.channel_mlp(xin.float(), d(w1), d(b1), d(w2), d(b2), bf16_products=True)
+    torch.cuda.synchronize()
+    assert y.dtype == (torch.bfloat16 if lifting else torch.float32)
+    if lifting:
+        assert torch.equal(y, yf.to(torch.bfloat16))
+    else:
+        assert torch.equal(y, yf)
+    ref = R.channel_mlp(xin.float().cpu().double(), [w1.double(), w2.double()],
+                        [b1.double(), b2.double()], bf16_products=True)
+    # bf16 products: the hidden activation's rounding (fp32 here, float64 in
+    # the oracle) can differ by one bf16 step near ties, ~1e-4 of the output
+    assert rel_err(y.float(), ref) <= (2.0 ** -8 if lifting else 0) + 1e-3
 
 
 _EPI_CASES = [

@@ -157,6 +157,39 @@ def test_channel_mlp_bf16_products_rounding():
     assert (R.channel_mlp(xs, ws, bs, bf16_products=True) - ref).abs().max() > 0
 
 
+def test_fno_forward_bf16_storage_rounds_at_layer_boundaries():
+    """bf16_storage rounds the lifting's output and each layer's output to the
+    nearest bfloat16, ties to even, and nothing else: closed forms on a model
+    whose stored activations are constants.  Lifting: zero weights, output bias
+    1 + 2^-8, halfway between the bf16 neighbours 1 and 1 + 2^-7 (so 1.0 under
+    ties-to-even).  Layer: zero spectral weight and bias, zero skips, output
+    bias 1 + 3 * 2^-8, halfway between 1 + 2^-7 and 1 + 2^-6 (even: 1 + 2^-6).
+    Projection: GELU of its input (unit weights, no rounding of products)."""
+    z = lambda *s: torch.zeros(*s, dtype=torch.float64)
+    one = torch.ones(1, 1, dtype=torch.float64)
+    x = z(1, 1, 8, 8)
+    lift = {"weights": [z(1, 1), z(1, 1)], "biases": [z(1), torch.tensor([1 + 2.0 ** -8], dtype=torch.float64)]}
+    proj = {"weights": [one, one], "biases": [z(1), z(1)]}
+    g = lambda v: 0.5 * v * (1 + math.erf(v / math.sqrt(2)))
+    params = {"lifting": lift, "projection": proj, "layers": [], "positional_embedding": False}
+    close = lambda y, v: torch.allclose(y, torch.full_like(y, v), rtol=0, atol=1e-12)
+    y = R.fno_forward(x, params, bf16_storage=True)
+    assert close(y, g(1.0))
+    y = R.fno_forward(x, params)
+    assert close(y, g(1 + 2.0 ** -8))
+    layer = {"conv": dict(weight=torch.zeros(1, 1, 4, 3, dtype=torch.complex128), bias=z(1, 1, 1),
+                          n_modes=(4, 3), max_n_modes=(4, 3)),
+             "fno_skip": {"type": "linear", "w": z(1, 1)},
+             "mlp": {"weights": [z(1, 1), z(1, 1)],
+                     "biases": [z(1), torch.tensor([1 + 3 * 2.0 ** -8], dtype=torch.float64)]},
+             "mlp_skip": {"type": "soft-gating", "w": z(1)}}
+    params["layers"] = [layer]
+    y = R.fno_forward(x, params, bf16_storage=True)
+    assert close(y, g(1 + 2.0 ** -6))
+    y = R.fno_forward(x, params)
+    assert close(y, g(1 + 3 * 2.0 ** -8))
+
+
 def _wave(shape, freqs):
     """cos(2 pi sum_d f_d n_d / N_d) on a grid of the given shape."""
     grids = torch.meshgrid(*[torch.arange(n, dtype=torch.float64) for n in shape], indexing="ij")
