@@ -200,6 +200,83 @@ int main() {
     EXPECT(fno_spectral_block_f32_noalloc(x, w, nullptr, nullptr, y, 1, 64, 64, 3, s3, m3, 0,
                                           FNO_SKIP_NONE, FNO_ACT_NONE, st), FNO_ERR_UNSUPPORTED);
   }
+  // ------------------------------------------- one-pass FNO layer (fp32 / bf16)
+  {
+    float* const x = reinterpret_cast<float*>((uintptr_t)1 << 44);
+    float* const y = reinterpret_cast<float*>((uintptr_t)2 << 44);
+    const int32_t s2[2] = {256, 256}, m2[2] = {64, 33}, s48[2] = {48, 256}, m48[2] = {20, 12};
+    CHECK(fno_layer_is_fused(2, 64, 32, 2, s2, m2, FNO_SKIP_LINEAR, FNO_SKIP_SOFT_GATING) == 1);
+    CHECK(fno_layer_bf16_is_fused(2, 64, 32, 2, s2, m2, FNO_SKIP_LINEAR, FNO_SKIP_SOFT_GATING) == 1);
+    CHECK(fno_layer_is_fused(2, 64, 32, 2, s48, m48, FNO_SKIP_LINEAR, FNO_SKIP_IDENTITY) == 1);
+    CHECK(fno_layer_bf16_is_fused(2, 64, 32, 2, s48, m48, FNO_SKIP_LINEAR, FNO_SKIP_IDENTITY) == 0);
+    CHECK(fno_layer_is_fused(2, 64, 48, 2, s2, m2, FNO_SKIP_LINEAR, FNO_SKIP_SOFT_GATING) == 0);
+    CHECK(fno_layer_is_fused(2, 64, 32, 2, s2, m2, FNO_SKIP_NONE, FNO_SKIP_SOFT_GATING) == 0);
+    CHECK(fno_layer_is_fused(2, 64, 32, 2, s2, m2, FNO_SKIP_LINEAR, 7) == 0);
+    const size_t need = fno_spectral_block_workspace_bytes(2, 64, 64, 2, s2, m2);
+    EXPECT(fno_layer_f32(x, w, nullptr, w, w, nullptr, w, nullptr, w, nullptr, y, 2, 64, 32, 2, s2,
+                         m2, 0, FNO_SKIP_LINEAR, FNO_SKIP_SOFT_GATING, FNO_ACT_GELU, ws, need - 1, st),
+           FNO_ERR_WORKSPACE);
+    EXPECT(fno_layer_bf16(x, w, nullptr, w, w, nullptr, w, nullptr, w, nullptr, y, 2, 64, 32, 2, s2,
+                          m2, 0, FNO_SKIP_LINEAR, FNO_SKIP_SOFT_GATING, FNO_ACT_GELU, ws, need - 1,
+                          st), FNO_ERR_WORKSPACE);
+    EXPECT(fno_layer_f32(x, w, nullptr, w, nullptr, nullptr, w, nullptr, w, nullptr, y, 2, 64, 32, 2,
+                         s2, m2, 0, FNO_SKIP_LINEAR, FNO_SKIP_SOFT_GATING, FNO_ACT_GELU, ws, need,
+                         st), FNO_ERR_INVALID);                                  // no W1
+    EXPECT(fno_layer_f32(x, w, nullptr, w, w, nullptr, w, nullptr, nullptr, nullptr, y, 2, 64, 32, 2,
+                         s2, m2, 0, FNO_SKIP_LINEAR, FNO_SKIP_SOFT_GATING, FNO_ACT_GELU, ws, need,
+                         st), FNO_ERR_INVALID);                                  // no gate weight
+    EXPECT(fno_layer_f32(x, w, nullptr, w, w, nullptr, w, nullptr, w, nullptr, y, 2, 64, 48, 2, s2,
+                         m2, 0, FNO_SKIP_LINEAR, FNO_SKIP_SOFT_GATING, FNO_ACT_GELU, ws, need, st),
+           FNO_ERR_UNSUPPORTED);                                                 // 48 hidden
+    EXPECT(fno_layer_bf16(x, w, nullptr, w, w, nullptr, w, nullptr, w, nullptr, y, 2, 64, 32, 2, s48,
+                          m48, 0, FNO_SKIP_LINEAR, FNO_SKIP_IDENTITY, FNO_ACT_GELU, ws, big_ws, st),
+           FNO_ERR_UNSUPPORTED);                                                 // 48-row planes
+    // bf16 x and y: 2 bytes per element, so y one fp32 plane-half past x overlaps
+    EXPECT(fno_layer_bf16(x, w, nullptr, w, w, nullptr, w, nullptr, w, nullptr,
+                          reinterpret_cast<char*>(x) + 2 * 64 * 256 * 256, 2, 64, 32, 2, s2, m2, 0,
+                          FNO_SKIP_LINEAR, FNO_SKIP_SOFT_GATING, FNO_ACT_GELU, ws, need, st),
+           FNO_ERR_INVALID);
+  }
+  // ----------------------------- lifting / projection with bf16 storage
+  {
+    CHECK(fno_channel_mlp_io_is_supported(3, 128, 64, 1024, 0, 1) == 1);
+    CHECK(fno_channel_mlp_io_is_supported(64, 128, 1, 1024, 1, 0) == 1);
+    CHECK(fno_channel_mlp_io_is_supported(3, 128, 64, 1024, 1, 0) == 0);
+    CHECK(fno_channel_mlp_io_is_supported(64, 128, 1, 1024, 0, 1) == 0);
+    CHECK(fno_channel_mlp_io_is_supported(64, 32, 64, 1024, 1, 1) == 0);
+    CHECK(fno_channel_mlp_io_is_supported(64, 32, 64, 1022, 0, 0) == 0);
+    EXPECT(fno_channel_mlp_io(x, w, nullptr, w, nullptr, y, 1, 64, 128, 1, 1024, 0, 0, 1, st),
+           FNO_ERR_UNSUPPORTED);
+    EXPECT(fno_channel_mlp_io(x, w, nullptr, w, nullptr, y, 1, 3, 128, 64, 1024, 0, 2, 0, st),
+           FNO_ERR_INVALID);
+    EXPECT(fno_channel_mlp_io(x, w, nullptr, w, nullptr, y, 1, 3, 128, 64, 1024, 5, 0, 1, st),
+           FNO_ERR_INVALID);
+    EXPECT(fno_channel_mlp_io(x + 1, w, nullptr, w, nullptr, y, 1, 3, 128, 64, 8, 0, 0, 1, st),
+           FNO_ERR_UNSUPPORTED);                                                 // misaligned
+    EXPECT(fno_channel_mlp_io(x, w, nullptr, w, nullptr, x + 4, 1, 3, 128, 64, 8, 0, 0, 1, st),
+           FNO_ERR_INVALID);                                                     // overlap
+    EXPECT(fno_channel_mlp_io(nullptr, w, nullptr, w, nullptr, y, 1, 3, 128, 64, 8, 0, 0, 1, st),
+           FNO_ERR_INVALID);
+  }
+  // ------------------------------------------------ inverse + epilogue
+  {
+    float* const x = reinterpret_cast<float*>((uintptr_t)1 << 44);
+    float* const y = reinterpret_cast<float*>((uintptr_t)2 << 44);
+    const int32_t s3[3] = {16, 16, 64}, m3[3] = {8, 8, 9}, m3bad[3] = {8, 8, 40};
+    const size_t need = fno_irfft_window_workspace_bytes(2 * 32, 3, s3, m3);
+    EXPECT(fno_irfft_window_epilogue_f32(x, nullptr, x, w, y, 2, 32, 32, 3, s3, m3bad, 0,
+                                         FNO_SKIP_LINEAR, FNO_ACT_GELU, ws, big_ws, st),
+           FNO_ERR_INVALID);
+    EXPECT(fno_irfft_window_epilogue_f32(x, nullptr, x, nullptr, y, 2, 32, 32, 3, s3, m3, 0,
+                                         FNO_SKIP_LINEAR, FNO_ACT_GELU, ws, big_ws, st),
+           FNO_ERR_INVALID);                                                     // no skip weight
+    EXPECT(fno_irfft_window_epilogue_f32(x, nullptr, x, w, y, 2, 32, 32, 3, s3, m3, 0, 9,
+                                         FNO_ACT_GELU, ws, big_ws, st), FNO_ERR_INVALID);
+    if (need > 0)
+      EXPECT(fno_irfft_window_epilogue_f32(x, nullptr, x, w, y, 2, 32, 32, 3, s3, m3, 0,
+                                           FNO_SKIP_LINEAR, FNO_ACT_GELU, ws, need - 1, st),
+             FNO_ERR_WORKSPACE);
+  }
   // ------------------------------------ the error message is per host thread
   {
     EXPECT(fno_contract_dense_c64(x, w, y, 0, 3, 4, 10, 0, st), FNO_ERR_INVALID);
