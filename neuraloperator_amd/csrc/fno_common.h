@@ -79,6 +79,18 @@ __device__ __forceinline__ float act_select(float g, float v, uint32_t m) {
                                        (__builtin_bit_cast(uint32_t, v) & ~m));
 }
 
+// 16-byte loads / stores with the non-temporal (streaming) cache policy, for
+// activations a kernel touches once (16-byte aligned addresses).
+typedef float nt_v4f __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 load_nt(const float* p) {
+  const nt_v4f v = __builtin_nontemporal_load(reinterpret_cast<const nt_v4f*>(p));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void store_nt(float* p, float4 v) {
+  const nt_v4f w = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(w, reinterpret_cast<nt_v4f*>(p));
+}
+
 // Raw buffer resource over [base, base + bytes): loads past the end return
 // zero, and offsets are 32-bit, so address arithmetic stays in 32-bit VGPRs.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {

@@ -143,8 +143,7 @@ k_line_epilogue(const float2* __restrict__ z, const float* __restrict__ x,
       for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-          xv[ks][i] = *reinterpret_cast<const float4*>(
-              x + (((int64_t)b * CI + 32 * ks + 8 * G + i) * L + line) * kW + 4 * n);
+          xv[ks][i] = load_nt(x + (((int64_t)b * CI + 32 * ks + 8 * G + i) * L + line) * kW + 4 * n);
     }
 #pragma unroll
     for (int ot = 0; ot < OT; ++ot) {
@@ -198,8 +197,7 @@ k_line_epilogue(const float2* __restrict__ z, const float* __restrict__ x,
         v.y = act_select(gelu_erf(acc[ot][1][r]), acc[ot][1][r], gmask);
         v.z = act_select(gelu_erf(acc[ot][2][r]), acc[ot][2][r], gmask);
         v.w = act_select(gelu_erf(acc[ot][3][r]), acc[ot][3][r], gmask);
-        *reinterpret_cast<float4*>(
-            y + (((int64_t)b * CO + 16 * ot + 4 * G + r) * L + line) * kW + 4 * n) = v;
+        store_nt(y + (((int64_t)b * CO + 16 * ot + 4 * G + r) * L + line) * kW + 4 * n, v);
       }
   }
 }

@@ -49,6 +49,12 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 
 namespace rg {
 constexpr int kWaves = 8, kThreads = 64 * kWaves;
+// cache policy of the x loads and y stores: non-temporal (streaming).  Each
+// x and y byte is touched once here, and streaming them keeps the caches for
+// the spectrum every block re-reads; measured 482 -> 465 us per block call at
+// B32 C64 256^2 (calls back to back: less of y left to write back in the
+// next call).
+constexpr int kNT = 2;
 constexpr int kCo = 64;                 // output channels (4 tiles of 16)
 constexpr int kStepPx = 256;            // pixels per step
 }  // namespace rg
@@ -251,10 +257,10 @@ k_row_synth(const typename RowIO<BF>::T* __restrict__ x, const float2* __restric
           const int soff = __builtin_amdgcn_readfirstlane(
               (int)(((uint32_t)(32 * ks + i) * HW + (uint32_t)h * W) * ES));
           if constexpr (BF)
-            dst[ks][i] = __builtin_amdgcn_raw_buffer_load_b32(rx, (int)xvoff, soff, 0);
+            dst[ks][i] = __builtin_amdgcn_raw_buffer_load_b32(rx, (int)xvoff, soff, rg::kNT);
           else
             dst[ks][i] = __builtin_bit_cast(
-                float2, __builtin_amdgcn_raw_buffer_load_b64(rx, (int)xvoff, soff, 0));
+                float2, __builtin_amdgcn_raw_buffer_load_b64(rx, (int)xvoff, soff, rg::kNT));
         }
     }
   };
@@ -419,11 +425,11 @@ k_row_synth(const typename RowIO<BF>::T* __restrict__ x, const float2* __restric
         if constexpr (BF) {
           const uint32_t lo = __builtin_bit_cast(unsigned short, (__bf16)v0);
           const uint32_t hi = __builtin_bit_cast(unsigned short, (__bf16)v1);
-          __builtin_amdgcn_raw_buffer_store_b32(lo | (hi << 16), ry, (int)yvoff, soff, 0);
+          __builtin_amdgcn_raw_buffer_store_b32(lo | (hi << 16), ry, (int)yvoff, soff, rg::kNT);
         } else {
           __builtin_amdgcn_raw_buffer_store_b64(
               __builtin_bit_cast(__attribute__((ext_vector_type(2))) int, make_float2(v0, v1)),
-              ry, (int)yvoff, soff, 0);
+              ry, (int)yvoff, soff, rg::kNT);
         }
       }
   };

@@ -103,8 +103,8 @@ k_slab_fwd64(const float* __restrict__ x, float2* __restrict__ out, int64_t slab
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         const float* p = xs + (16 * mt + n) * kN + 32 * ks + 8 * G;
-        xv[mt][ks][0] = *reinterpret_cast<const float4*>(p);
-        xv[mt][ks][1] = *reinterpret_cast<const float4*>(p + 4);
+        xv[mt][ks][0] = load_nt(p);
+        xv[mt][ks][1] = load_nt(p + 4);
       }
     v4f a1[4][2];
 #pragma unroll
