@@ -18,6 +18,7 @@
 //      window's twiddles (cos / sin) in that slot order, scaled by s.
 // The twiddle fragments of both products are built once per workgroup in LDS.
 #include "fno_common.h"
+#include "fno_fft_lds.h"
 #include "fno_twiddle.h"
 
 namespace fno {
@@ -174,8 +175,13 @@ k_axis_inv64(const float2* __restrict__ src, float2* __restrict__ dst, int64_t s
   // A fragments [row tile 8][hi|lo][64]: row tile rt = 2 t + part, rows
   // d = 16 t + lane % 16; K slot (G, i) = window row 4 G + i / 2, Re / Im of U
   __shared__ v8bf af[8 * 2 * 64];
+  // per wave: the slab's [64][inner] output, staged so it leaves as whole
+  // 16-byte words of one contiguous run (64 inner 8 bytes per slab)
+  extern __shared__ float4 stage[];   // [kWaves][32 inner]
   const int tid = threadIdx.x, lane = tid & 63;
   const int G = lane >> 4, n = lane & 15;
+  float4* st4 = stage + (tid >> 6) * 32 * inner;
+  float2* stw = reinterpret_cast<float2*>(st4);
   for (int f = tid; f < 8 * 64; f += kThreads) {
     const int ln = f & 63, rt = f >> 6;
     const int d = 16 * (rt >> 1) + (ln & 15), part = rt & 1, g = ln >> 4;
@@ -222,9 +228,14 @@ k_axis_inv64(const float2* __restrict__ src, float2* __restrict__ dst, int64_t s
       im = mma3(af[((2 * t + 1) * 2) * 64 + lane], af[((2 * t + 1) * 2 + 1) * 64 + lane], bh, bl, im);
       if (n < inner) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) zs[(16 * t + 4 * G + r) * inner + n] = make_float2(re[r], im[r]);
+        for (int r = 0; r < 4; ++r) stw[(16 * t + 4 * G + r) * inner + n] = make_float2(re[r], im[r]);
       }
     }
+    wave_sync();
+    // 32 inner float4 words: the slab's output run (16-byte aligned: 512 inner bytes per slab)
+    float4* z4 = reinterpret_cast<float4*>(zs);
+    for (int q = lane; q < 32 * inner; q += 64) z4[q] = st4[q];
+    wave_sync();
   }
 }
 
@@ -268,7 +279,8 @@ int axis_inv64(const float2* src, float2* dst, int64_t slabs, int m, int inner, 
                hipStream_t st) {
   int64_t grid = (slabs + sl::kWaves - 1) / sl::kWaves;
   if (grid > 4 * slab_cus()) grid = 4 * slab_cus();
-  hipLaunchKernelGGL(k_axis_inv64, dim3((unsigned)grid), dim3(sl::kThreads), 0, st, src, dst, slabs,
+  hipLaunchKernelGGL(k_axis_inv64, dim3((unsigned)grid), dim3(sl::kThreads),
+                     (size_t)sl::kWaves * 32 * inner * sizeof(float4), st, src, dst, slabs,
                      m, inner, scale);
   return launch_status("k_axis_inv64");
 }
