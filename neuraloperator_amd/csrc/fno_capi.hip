@@ -53,6 +53,10 @@ bool fast2d_bf16_supported(const int32_t* sizes, const int32_t* modes);
 size_t fast2d_workspace(int B, int Ci, int Co, const int32_t* sizes, const int32_t* modes);
 bool rowsynth_covers(int H, int W, int Ci, int Co, int m1, int m2h);
 bool fast1d_supported(int Ci, int Co, int N, int m);
+bool line1d_supported(int Ci, int Co, int N, int m, int skip_kind);
+int line1d_block(const float* x, const float2* w, const float* bias, const float* skip_w, float* y,
+                 int B, int Ci, int Co, int N, int m, int norm, int skip_kind, int act, void* ws,
+                 size_t ws_bytes, hipStream_t st);
 int fast1d_block(const float* x, const float2* w, const float* bias, const float* skip_w, float* y,
                  int B, int Ci, int Co, int N, int m, int norm, int skip_kind, int act,
                  hipStream_t st);
@@ -547,6 +551,10 @@ int spectral_block_run(const float* x, const void* w, const float* bias, const f
                        int32_t skip_kind, int32_t act, void* workspace, size_t workspace_bytes,
                        hipStream_t st) {
   int rc;
+  if (ndim == 1 && line1d_supported(in_channels, out_channels, sizes[0], modes[0], skip_kind))
+    return line1d_block(x, reinterpret_cast<const float2*>(w), bias, skip_weight, y, batch,
+                        in_channels, out_channels, sizes[0], modes[0], norm, skip_kind, act,
+                        workspace, workspace_bytes, st);
   if (ndim == 1 && fast1d_supported(in_channels, out_channels, sizes[0], modes[0]))
     return fast1d_block(x, reinterpret_cast<const float2*>(w), bias, skip_weight, y, batch,
                         in_channels, out_channels, sizes[0], modes[0], norm, skip_kind, act, st);

@@ -1,5 +1,6 @@
-// Fused 1D spectral block in one launch, for lines of N = 256 .. 1024 points
-// (N dividing 1024) and at most 16 kept rfft bins:
+// 1D spectral block for lines of N = 256 .. 1024 points (N dividing 1024) and
+// at most 16 kept rfft bins, as one launch (linear skip, below) or as two
+// (no / identity / soft-gating skip, the line path further down):
 //
 //   y[b, o, n] = act( sum_k c_k s_i Re( Y[b, o, k] e^{2 pi i k n / N} )
 //                     + bias[o] + (Ws x)[b, o, n] ),
@@ -23,7 +24,7 @@
 //      folded in, the imaginary part of the DC bin meeting sin 0 = 0) plus
 //      the skip Ws[16 x Ci] . x[Ci x N] (the 1x1 conv; diag(g) for
 //      soft-gating, the identity), seeded with the bias; activation; store.
-// The spectrum never leaves the chip and the library needs no workspace.
+// The spectrum never leaves the chip.
 // Products as three-term bf16 splits with fp32 accumulation, as in the 2D
 // row epilogue (each within 3 * 2^-16 of |a b|).
 #include "fno_twiddle.h"
@@ -300,6 +301,232 @@ k_conv1d_fused(const float* __restrict__ x, const float2* __restrict__ w,
 // most 16 kept bins (never the Nyquist bin then), 32 or 64 input channels
 // (the forward product and the skip tile them by 16 and 32), output channels
 // a multiple of 16.
+// ---------------------------------------------------------------------------
+// Two-kernel 1D path for blocks without a linear skip (the plain SpectralConv
+// of a 1D FNO): the one-launch kernel above runs one workgroup per (sample, 16
+// output channels), each loading its sample's whole x and computing its full
+// truncated DFT, so a batch of 16 samples keeps 64 CUs busy, bound by their
+// loads.  Here the DFT is spread over one wave per line and the synthesis over
+// one workgroup per (sample, 4 output channels), and only the m-bin spectra
+// pass between the two through the workspace.
+namespace l1 {
+constexpr int kThreads = 256, kLines = 4;   // lines (waves) per DFT workgroup
+constexpr int kOut = 4;                      // output channels per synthesis workgroup
+constexpr int kSynThreads = 512;             // two waves (point halves) per output channel
+constexpr int kMaxM = 16;
+constexpr int kChunk = 8;                    // contraction loads in flight per thread
+}  // namespace l1
+
+// X[line][k] = s sum_n x[line][n] e^{-2 pi i k n / N}, k < m.  Lane l of the
+// line's wave holds n = l + 64 j (j < J = N / 64):
+//   X[k] = sum_l e^{-2 pi i k l / N} S_{k mod J}(l),
+//   S_r(l) = sum_j x[l + 64 j] e^{-2 pi i r j / J}
+// (a J-point DFT per lane with constant twiddles, S_{J - r} = conj(S_r) for
+// real x, one twiddle per bin, then the sum over the wave's lanes as a
+// butterfly reduce-scatter of the 32 floats: 32 lane exchanges instead of
+// 6 x 32).
+template <int N>
+__global__ void __launch_bounds__(l1::kThreads)
+k_line_dft(const float* __restrict__ x, float2* __restrict__ xhat, int64_t lines, int m,
+           float scale) {
+  constexpr int J = N / 64;
+  const int lane = threadIdx.x & 63;
+  const int64_t line = (int64_t)blockIdx.x * l1::kLines + (threadIdx.x >> 6);
+  if (line >= lines) return;   // whole waves; the kernel has no barrier
+  const float* xl = x + line * N;
+  float xv[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) xv[j] = xl[lane + 64 * j];
+  float2 S[J / 2 + 1];
+#pragma unroll
+  for (int r = 0; r <= J / 2; ++r) {
+    float2 sr = make_float2(0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const float2 t = twiddle_any((r * j) % J, J);
+      sr.x = fmaf(xv[j], t.x, sr.x);
+      sr.y = fmaf(-xv[j], t.y, sr.y);
+    }
+    S[r] = sr;
+  }
+  const float2 wl = twiddle_any(lane, N);         // e^{+2 pi i l / N}
+  const float2 step = make_float2(wl.x, -wl.y);   // e^{-2 pi i l / N}
+  float2 p = make_float2(1.f, 0.f);               // e^{-2 pi i k l / N}
+  float v[2 * l1::kMaxM];
+#pragma unroll
+  for (int k = 0; k < l1::kMaxM; ++k) {
+    const int r = k % J;
+    const float2 sk = r <= J / 2 ? S[r] : make_float2(S[J - r].x, -S[J - r].y);
+    const float2 a = cmul(p, sk);
+    v[2 * k] = a.x;
+    v[2 * k + 1] = a.y;
+    p = cmul(p, step);
+  }
+  // reduce-scatter: after the exchange over lane bit b the lane keeps the half
+  // of its values selected by that bit; the last exchange (bit 0) completes
+  // the sum of value 16 b5 + 8 b4 + 4 b3 + 2 b2 + b1
+#pragma unroll
+  for (int h = 16, bit = 32; h >= 1; h >>= 1, bit >>= 1) {
+    const bool up = (lane & bit) != 0;
+#pragma unroll
+    for (int i = 0; i < h; ++i) {
+      // the empty asm keeps the two selects on values: folded into one select
+      // of the array index they become a lane-varying index into v[], which
+      // lowers to compare-and-select chains over the whole array
+      float lo = v[i], hi = v[h + i];
+      asm volatile("" : "+v"(lo), "+v"(hi));
+      const float send = up ? lo : hi;
+      const float keep = up ? hi : lo;
+      v[i] = keep + __shfl_xor(send, bit, 64);
+    }
+  }
+  float t = v[0] + __shfl_xor(v[0], 1, 64);
+  const int idx = lane >> 1;   // 2 k + (0 re | 1 im)
+  if (!(lane & 1) && idx < 2 * m)
+    reinterpret_cast<float*>(xhat)[line * 2 * m + idx] = t * scale;
+}
+
+// v[jj] = bo + sum_k Re(q_k e^{2 pi i k j / J}), j = H J / 2 + jj: the table
+// index k j mod J is a compile-time constant
+template <int J, int H>
+__device__ __forceinline__ void line_synth_half(const float2 (&q)[l1::kMaxM], float bo,
+                                                float (&v)[J / 2]) {
+#pragma unroll
+  for (int jj = 0; jj < J / 2; ++jj) {
+    float a = bo;
+#pragma unroll
+    for (int k = 0; k < l1::kMaxM; ++k) {
+      const float2 t = twiddle_any((k * (jj + H * J / 2)) % J, J);
+      a = fmaf(q[k].x, t.x, a);
+      a = fmaf(-q[k].y, t.y, a);
+    }
+    v[jj] = a;
+  }
+}
+
+// y[b, o, n] for kOut output channels o of sample b:
+//   Y[o][k] = sum_c X[b][c][k] W[c][o][k]
+//   y = act( bias[o] + s sum_k c_k Re(Y[o][k] e^{2 pi i k n / N}) + skip(x)[b, o, n] )
+// (c_0 = 1, c_k = 2: m <= N / 2 - 1 keeps the Nyquist bin out; the imaginary
+// part of the DC bin meets sin 0).  Skip: none, identity or soft-gating.
+// Wave w: output channel o0 + w % 4, points n = l + 64 j with j in the
+// half w / 4 of 0 .. J - 1.
+template <int N>
+__global__ void __launch_bounds__(l1::kSynThreads)
+k_line_synth(const float2* __restrict__ xhat, const float2* __restrict__ w,
+             const float* __restrict__ bias, const float* __restrict__ x,
+             const float* __restrict__ skip_w, float* __restrict__ y, int Ci, int Co, int m,
+             int skip_kind, int act, float s) {
+  constexpr int J = N / 64, JH = J / 2;
+  __shared__ float2 yp[2][l1::kOut][l1::kMaxM];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ow = wave & 3, half = wave >> 2;
+  const int groups = Co / l1::kOut;
+  const int b = blockIdx.x / groups, o0 = l1::kOut * (blockIdx.x % groups);
+  const int o = o0 + ow;
+  // contraction: thread (o, k = lane % 16, part = 4 half + lane / 16) sums
+  // the channels c = part + 8 i in chunks whose loads are all issued first;
+  // then the sum over lane / 16 by exchanges and over the halves in LDS
+  {
+    const int k = lane & 15, part = 4 * half + (lane >> 4);
+    float2 acc = make_float2(0.f, 0.f);
+    if (k < m) {
+      const float2* xb = xhat + (int64_t)b * Ci * m + k;
+      const float2* wo = w + (int64_t)o * m + k;
+      const int64_t ws = (int64_t)Co * m;
+      for (int c0 = part; c0 < Ci; c0 += 8 * l1::kChunk) {
+        float2 xv[l1::kChunk], wv[l1::kChunk];
+#pragma unroll
+        for (int u = 0; u < l1::kChunk; ++u) {
+          const int c = c0 + 8 * u;
+          xv[u] = c < Ci ? xb[(int64_t)c * m] : make_float2(0.f, 0.f);
+          wv[u] = c < Ci ? wo[(int64_t)c * ws] : make_float2(0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < l1::kChunk; ++u) cfma(acc, xv[u], wv[u]);
+      }
+    }
+    acc.x += __shfl_xor(acc.x, 16, 64);
+    acc.y += __shfl_xor(acc.y, 16, 64);
+    acc.x += __shfl_xor(acc.x, 32, 64);
+    acc.y += __shfl_xor(acc.y, 32, 64);
+    if (lane < 16) yp[half][ow][k] = acc;   // k >= m: zero
+  }
+  __syncthreads();
+  // synthesis: q_k = c_k s Y_k e^{2 pi i k l / N}
+  const float2 wl = twiddle_any(lane, N);
+  float2 p = make_float2(1.f, 0.f);
+  float2 q[l1::kMaxM];
+#pragma unroll
+  for (int k = 0; k < l1::kMaxM; ++k) {
+    const float ck = (k == 0 ? 1.f : 2.f) * s;
+    const float2 a = yp[0][ow][k], c = yp[1][ow][k];
+    q[k] = cmul(make_float2(ck * (a.x + c.x), ck * (a.y + c.y)), p);
+    p = cmul(p, wl);
+  }
+  const float bo = bias ? bias[o] : 0.f;
+  const float g = skip_kind == FNO_SKIP_SOFT_GATING ? skip_w[o] : 1.f;
+  const bool skip = skip_kind != FNO_SKIP_NONE;
+  const uint32_t gmask = act_mask(act == FNO_ACT_GELU);
+  const float* xo = x + ((int64_t)b * Ci + o) * N + 64 * JH * half + lane;
+  float* yo = y + ((int64_t)b * Co + o) * N + 64 * JH * half + lane;
+  float xs[JH];
+  if (skip) {
+#pragma unroll
+    for (int j = 0; j < JH; ++j) xs[j] = xo[64 * j];
+  }
+  float vo[JH];
+  if (half == 0)
+    line_synth_half<J, 0>(q, bo, vo);
+  else
+    line_synth_half<J, 1>(q, bo, vo);
+#pragma unroll
+  for (int j = 0; j < JH; ++j) {
+    float v = vo[j];
+    if (skip) v = fmaf(g, xs[j], v);
+    yo[64 * j] = act_select(gelu_erf(v), v, gmask);
+  }
+}
+
+bool line1d_supported(int Ci, int Co, int N, int m, int skip_kind) {
+  if (!(N == 256 || N == 512 || N == 1024)) return false;
+  if (m < 1 || m > l1::kMaxM || m > N / 2 - 1) return false;
+  if (Ci < 1 || Co < l1::kOut || Co % l1::kOut != 0) return false;
+  if (skip_kind == FNO_SKIP_LINEAR) return false;
+  return skip_kind == FNO_SKIP_NONE || Ci == Co;
+}
+
+size_t line1d_workspace(int B, int Ci, int m) { return (size_t)B * Ci * m * sizeof(float2); }
+
+int line1d_block(const float* x, const float2* w, const float* bias, const float* skip_w, float* y,
+                 int B, int Ci, int Co, int N, int m, int norm, int skip_kind, int act, void* ws,
+                 size_t ws_bytes, hipStream_t st) {
+  if (ws_bytes < line1d_workspace(B, Ci, m)) {
+    set_error("1D block: workspace %zu < %zu bytes", ws_bytes, line1d_workspace(B, Ci, m));
+    return FNO_ERR_WORKSPACE;
+  }
+  const int32_t sz[1] = {N};
+  const float fs = (float)forward_scale(norm, sz, 1);
+  const float is = (float)inverse_scale(norm, sz, 1);
+  float2* xhat = reinterpret_cast<float2*>(ws);
+  const int64_t lines = (int64_t)B * Ci;
+  const unsigned g1 = (unsigned)((lines + l1::kLines - 1) / l1::kLines);
+  const unsigned g2 = (unsigned)((int64_t)B * (Co / l1::kOut));
+#define FNO_L1(n)                                                                                  \
+  if (N == n) {                                                                                    \
+    hipLaunchKernelGGL(k_line_dft<n>, dim3(g1), dim3(l1::kThreads), 0, st, x, xhat, lines, m, fs); \
+    int rc = launch_status("k_line_dft");                                                          \
+    if (rc) return rc;                                                                             \
+    hipLaunchKernelGGL(k_line_synth<n>, dim3(g2), dim3(l1::kSynThreads), 0, st, xhat, w, bias, x,  \
+                       skip_w, y, Ci, Co, m, skip_kind, act, is);                                  \
+    return launch_status("k_line_synth");                                                          \
+  }
+  FNO_L1(256) FNO_L1(512) FNO_L1(1024)
+#undef FNO_L1
+  set_error("1D block: unsupported N=%d", N);
+  return FNO_ERR_UNSUPPORTED;
+}
+
 bool fast1d_supported(int Ci, int Co, int N, int m) {
   if (!(N == 256 || N == 512 || N == 1024)) return false;
   if (m < 1 || m > f1::kMaxM || 2 * m > N) return false;

@@ -8,6 +8,7 @@ a CPU tensor or a missing library raises.
 from __future__ import annotations
 
 import ctypes
+import functools
 from typing import Optional, Sequence
 
 import torch
@@ -267,6 +268,14 @@ def spectral_block_is_fused(B, Ci, Co, sizes, modes, skip_kind) -> bool:
                                                 nat.i32_array(modes), skip_kind))
 
 
+@functools.lru_cache(maxsize=256)
+def _block_shape(B, Ci, Co, sizes, modes):
+    """The C-ABI size / mode arrays and the workspace size of a block shape
+    (read-only arrays, so one copy serves every call of that shape)."""
+    sz, md = nat.i32_array(sizes), nat.i32_array(modes)
+    return sz, md, nat.load().fno_spectral_block_workspace_bytes(B, Ci, Co, len(sizes), sz, md)
+
+
 def spectral_block(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor],
                    modes: Sequence[int], skip_kind: int = nat.SKIP_NONE,
                    skip_weight: Optional[torch.Tensor] = None, act: int = nat.ACT_NONE,
@@ -283,8 +292,7 @@ def spectral_block(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.T
     y = out if out is not None else torch.empty((B, Co, *S), dtype=torch.float32, device=x.device)
     b = _f32(bias.reshape(-1)) if bias is not None else None
     w = _f32(skip_weight.reshape(-1)) if skip_weight is not None else None
-    sz, md = nat.i32_array(S), nat.i32_array(modes)
-    wsb = lib.fno_spectral_block_workspace_bytes(B, Ci, Co, nd, sz, md)
+    sz, md, wsb = _block_shape(B, Ci, Co, tuple(S), tuple(int(m) for m in modes))
     ws = _workspace(wsb, x.device)
     nat.check(lib.fno_spectral_block_f32(_ptr(x), _ptr(weight), _ptr(b), _ptr(w), _ptr(y), B, Ci, Co,
                                          nd, sz, md, nat.NORMS[fft_norm], skip_kind, act, _ptr(ws),

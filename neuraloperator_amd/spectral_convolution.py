@@ -33,7 +33,7 @@ from torch import nn
 
 from . import _native as nat
 from . import functional as Fh
-from .factorized_tensors import FactorizedTensor, TuckerTensor, _TuckerView
+from .factorized_tensors import DenseTensor, FactorizedTensor, TuckerTensor, _TuckerView
 from .resample import resample
 from .utils import get_active_profiler, maybe_profile, validate_scaling_factor
 
@@ -480,9 +480,10 @@ class SpectralConv(BaseSpectralConv):
     def dense_window_weight(self, sl) -> torch.Tensor:
         """The weight window as a dense complex tensor (reconstructing a
         factorized weight when needed)."""
-        w = self.weight[sl] if isinstance(self.weight, FactorizedTensor) else self.weight[sl]
-        w = w.to_tensor() if isinstance(w, FactorizedTensor) else w
-        return w
+        if type(self.weight) is DenseTensor:   # a view of the parameter, no window module
+            return self.weight.tensor[sl]
+        w = self.weight[sl]
+        return w.to_tensor() if isinstance(w, FactorizedTensor) else w
 
     # ---------------------------------------------------------------- forward
     def forward(self, x: torch.Tensor, output_shape: Optional[Tuple[int]] = None):
@@ -549,7 +550,9 @@ class SpectralConv(BaseSpectralConv):
         bias = self.bias.reshape(-1) if self.bias is not None else None
         same_size = out_sizes == sizes
         kind = self._contract
-        params = [self.bias] + list(self.weight.parameters()) + [skip_weight]
+        # the parameters only matter to _attach with gradients enabled
+        params = ([self.bias] + list(self.weight.parameters()) + [skip_weight]
+                  if torch.is_grad_enabled() else [])
         if kind in ("dense", "cp", "tt") and same_size and not self.separable:
             w = self.dense_window_weight(sl).detach()
             y = Fh.spectral_block(x.detach(), w, None if bias is None else bias.detach(), kept,

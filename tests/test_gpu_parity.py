@@ -413,6 +413,37 @@ def test_fno_c3_shape_bf16_input(cuda_device):
     assert dev_of(ref_bf) < dev_of(ref_p) and dev_of(ref_bf) < dev_of(ref)
 
 
+@pytest.mark.parametrize("N,m,Ci,Co,B", [(1024, 16, 3, 20, 2), (512, 7, 5, 4, 5), (256, 1, 1, 8, 1),
+                                         (256, 16, 12, 12, 3), (1024, 13, 96, 96, 2)])
+@pytest.mark.parametrize("skip", ["identity", "none"])
+def test_line_1d_block_channel_counts(N, m, Ci, Co, B, skip, cuda_device):
+    """The two-launch 1D line path on channel counts the one-launch kernel
+    does not take (Ci not 32 / 64, Co a multiple of 4 but not of 16, batch 1,
+    a single bin): the float64 oracle's SpectralConv forward plus skip and
+    GELU, and without GELU for the identity skip."""
+    if skip == "identity" and Ci != Co:
+        pytest.skip("identity skip needs Ci == Co")
+    print(f"line 1d N{N} m{m} Ci{Ci} Co{Co} B{B} {skip}", flush=True)
+    g = torch.Generator().manual_seed(70 + N + m + Ci)
+    x = torch.randn(B, Ci, N, generator=g)
+    w = torch.complex(torch.randn(Ci, Co, m, generator=g), torch.randn(Ci, Co, m, generator=g)) / Ci
+    bias = torch.randn(Co, generator=g) / 4
+    kind = nat.SKIP_IDENTITY if skip == "identity" else nat.SKIP_NONE
+    act = nat.ACT_NONE if skip == "identity" else nat.ACT_GELU
+    d = lambda t: t.to(cuda_device)
+    with torch.no_grad():
+        y = Fh.spectral_block(d(x), d(w), d(bias), [m], kind, None, act)
+    torch.cuda.synchronize()
+    ref = R.spectral_conv_forward(x.double(), w.to(torch.complex128), bias.double().view(-1, 1),
+                                  [m], [m])
+    if skip == "identity":
+        ref = ref + x.double()
+    else:
+        ref = R.gelu(ref)
+    err = rel_err(y, ref)
+    assert err <= TOL, err
+
+
 def test_c0_workload_full_size(cuda_device):
     """The 1D workload at its full size through the call the benchmark times
     (SpectralConv.forward): x[16, 64, 1024] ~ N(0, 1), n_modes 30 -> 16 rfft
@@ -1581,10 +1612,12 @@ def test_kernel_gelu_matches_exact_erf(cuda_device):
 @pytest.mark.parametrize("skip", ["linear", "soft-gating", "identity", "none"])
 @pytest.mark.parametrize("norm", ["forward", "backward", "ortho"])
 def test_fused_1d_block(N, m, Ci, Co, skip, norm, cuda_device):
-    """The one-launch 1D block (forward DFT product, contraction and the
-    synthesis product with skip, bias and GELU in one kernel) against the
-    float64 oracle: the SpectralConv forward (first m rfft bins) plus the
-    skip and erf GELU."""
+    """The 1D block against the float64 oracle: the SpectralConv forward
+    (first m rfft bins) plus the skip and erf GELU.  A linear skip takes the
+    one-launch kernel (forward DFT product, contraction and the synthesis
+    product with skip, bias and GELU in one kernel), the other skips the
+    two-launch line path (one wave's DFT per line, then contraction and
+    synthesis per 4 output channels)."""
     if skip in ("soft-gating", "identity") and Ci != Co:
         pytest.skip("gating/identity skips need Ci == Co")
     print(f"fused 1d N{N} m{m} Ci{Ci} Co{Co} {skip} {norm}", flush=True)
