@@ -153,10 +153,14 @@ k_channel_mlp(const void* xv, const float* __restrict__ w1, const float* __restr
       const int q = tid + kMlpThreads * j;
       const int c = q / (kMlpTP / 4);
       const int64_t p = p0 + 4 * (q % (kMlpTP / 4));
-      XQ zero;
-      if constexpr (XBF) zero = make_uint2(0u, 0u);
-      else zero = make_float4(0.f, 0.f, 0.f, 0.f);
-      pre[j] = q < NQ && p < P && c < ci ? *reinterpret_cast<const XQ*>(xb + c * P + p) : zero;
+      // a branch, not `cond ? *ptr : zero`: with two lvalue operands that
+      // selects between the addresses, putting zero in scratch memory and
+      // turning the load into a flat one
+      XQ v;
+      if constexpr (XBF) v = make_uint2(0u, 0u);
+      else v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (q < NQ && p < P && c < ci) v = *reinterpret_cast<const XQ*>(xb + c * P + p);
+      pre[j] = v;
     }
   };
   auto widen = [](const XQ& v) __attribute__((always_inline)) -> float4 {

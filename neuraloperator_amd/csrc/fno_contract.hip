@@ -1,4 +1,4 @@
-// Mode-wise complex contraction on fp32 MFMA (v_mfma_f32_32x32x2f32):
+// Mode-wise complex contraction on the matrix cores:
 //
 //   Y[b, o, k] = sum_i X[b, i, k] W[i, o, k]      X [B][Ci][M], W [Ci][Co][M], Y [B][Co][M]
 //
@@ -10,60 +10,87 @@
 //   A[Co+o][2i] =  Wi[i][o]     A[Co+o][2i+1] =  Wr[i][o]
 //   Bm[2i][b]   =  Xr[b][i]     Bm[2i+1][b]   =  Xi[b][i]
 //
+// Arithmetic: v_mfma_f32_16x16x16_bf16 with three-term bf16 splits, a =
+// a_hi + a_lo with a_hi = bf16(a), a_lo = bf16(a - a_hi) (round to nearest
+// even each), a b ~ a_hi b_lo + a_lo b_hi + a_hi b_hi with fp32 accumulation:
+// each product within 3 * 2^-16 of |a b| (the row epilogue's arithmetic).
+// Against fp32 products this takes a fifth of the matrix-core cycles
+// (v_mfma_f32_32x32x2f32: 64 cycles per 4,096 flop); the kernel is then
+// bound by its loads (fp32 products: 50 us at B32 C64 64x33 modes, bf16
+// splits 40 us).
+//
 // A workgroup owns KB = 16 consecutive modes (a 128-byte run of every X and W
 // row in their reference layouts), 32 batch entries and one half of the
-// output channels; wave w owns modes k0 + 2w and k0 + 2w + 1, i.e. four 32x32
-// tiles (the Yr and Yi rows of its 32 channels for both modes).  Eight waves
-// and <= 128 VGPRs per workgroup let two workgroups share a CU, so the 2 x 132
-// workgroups of a 64x33-mode layer run in one wave of the grid.  Input channels stream through LDS in chunks
-// of IC, transposed on the way in so each MFMA operand read is a run of
-// consecutive words, with the next chunk loaded into registers meanwhile.
-// The two channel halves of a mode block are placed on one XCD, next to each
-// other, so the second read of the block's X rows hits that XCD's L2.
+// output channels; wave w owns modes k0 + 2w and k0 + 2w + 1, i.e. 8 16x16
+// tiles per mode (Yr and Yi rows of its 32 channels x 32 batch entries).
+// Input channels stream through LDS in chunks of IC, split and transposed on
+// the way in, double-buffered, with the next chunk loaded into registers
+// meanwhile.  The two channel halves of a mode block are placed on one XCD,
+// next to each other, so the second read of the block's X rows hits that
+// XCD's L2.
 #include "fno_common.h"
 
 namespace fno {
-
-typedef float v16f_c __attribute__((ext_vector_type(16)));
 
 namespace {
 constexpr int MPW = 2;            // modes per wave
 constexpr int IC = 8;             // input channels per LDS chunk
 constexpr int OH = 32;            // output channels per workgroup
-constexpr int PS = OH;            // plane stride of a W tile row (re, im planes)
-constexpr int MS = 2 * PS + 4;    // (i, mode) block stride of the W tile
-constexpr int XM = 64 + 4;        // (i, mode) block stride of the X tile: [c][b]
 constexpr int WF4 = 4;            // W float4 per thread per chunk (IC*OH*KB/2/THREADS)
 constexpr int XF4 = 4;            // X float4 per thread per chunk (IC*32*KB/2/THREADS)
 __host__ __device__ constexpr int contract_threads(int kb) { return 64 * kb / MPW; }
-__host__ __device__ constexpr size_t contract_lds(int kb) {
-  return 2 * (size_t)IC * kb * (MS + XM) * sizeof(float);   // two chunk buffers
-}
 }  // namespace
 
-// KB modes per workgroup (KB/2 waves): 16 normally (one workgroup per CU), 18
-// when that keeps the grid within one round, 8 when even 16 leaves most CUs
-// idle.
+// KB modes per workgroup (KB/2 waves): 16 normally (one workgroup per CU),
+// 18 when that keeps the grid within one round, 8 when even 16 leaves most
+// CUs idle.  The chunk's operands are split once as they go into LDS, as
+// (hi, lo) pairs of bf16x2 words:
+//   Wl[i][mode][o] = (Wr, -Wi)    Xl[i][mode][b] = (Xr, Xi)
+// (33 pairs per row, one of padding).  One k-step of 16 is the chunk's 8
+// input channels: lane (r = l % 16, g = l / 16) holds k = 4 g .. 4 g + 3,
+// i.e. channels 2 g and 2 g + 1, so A[o][k] of the Yr rows is one pair from
+// each of those channels' rows, and A of the Yi rows (Wi, Wr) is the same
+// word with its halves swapped and the low half negated.
+namespace cb3 {
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+constexpr int RS = 33;            // uint2 per (channel, mode) row: 32 + 1 padding
+__host__ __device__ constexpr size_t lds_bytes(int kb) {
+  return 2 * (size_t)2 * IC * kb * RS * sizeof(uint2);   // two buffers of W and X
+}
+// (hi, lo) bf16x2 words of the pair (a, b)
+__device__ __forceinline__ uint2 split2(float a, float b) {
+  const v2bf h = {(__bf16)a, (__bf16)b};
+  const v2bf l = {(__bf16)(a - (float)h[0]), (__bf16)(b - (float)h[1])};
+  return make_uint2(__builtin_bit_cast(uint32_t, h), __builtin_bit_cast(uint32_t, l));
+}
+// (re, -im) -> (im, re): swap the halves, negate the new low half
+__device__ __forceinline__ uint32_t rot_conj(uint32_t w) {
+  return __builtin_amdgcn_alignbit(w, w, 16) ^ 0x8000u;
+}
+__device__ __forceinline__ v4s frag(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(v4s, make_uint2(a, b));
+}
+}  // namespace cb3
+
 template <int KB>
 __global__ void __launch_bounds__(contract_threads(KB))
 __attribute__((amdgpu_waves_per_eu(2, 4)))
 k_contract_mfma(const float2* __restrict__ X, const float2* __restrict__ W, float2* __restrict__ Y,
-                int B, int Ci, int Co, int64_t M, int nblocks, int ymap_w) {
+               int B, int Ci, int Co, int64_t M, int nblocks, int ymap_w) {
+  using namespace cb3;
   constexpr int THREADS = contract_threads(KB);
-  constexpr int NP = KB / 2;          // float4 (mode pairs) per operand row
+  constexpr int NP = KB / 2;
   static_assert(KB % 2 == 0 && IC * OH * KB / 2 == WF4 * THREADS && IC * 32 * KB / 2 == XF4 * THREADS,
                 "tile split");
+  static_assert(IC == 8, "one k-step of 16 per chunk");
   extern __shared__ float4 smem4[];
+  uint2* lds2 = reinterpret_cast<uint2*>(smem4);
   float* smem = reinterpret_cast<float*>(smem4);
-  // two chunk buffers, each W chunk [i][mode][re/im plane][o] then
-  // X chunk [i][mode][re/im][b]
-  constexpr int BUF = IC * KB * (MS + XM);
-  auto Wbuf = [&](int d) __attribute__((always_inline)) { return smem + d * BUF; };
-  auto Xbuf = [&](int d) __attribute__((always_inline)) { return smem + d * BUF + IC * KB * MS; };
-  // pair (mode block, channel half) placement: the halves of block p run on
-  // one XCD (workgroup id mod 8), 8 ids apart, and each XCD takes a
-  // contiguous range of mode blocks, so the 128-byte lines that two adjacent
-  // blocks' mode runs share are fetched into one L2
+  constexpr int BUF = 2 * IC * KB * RS;   // uint2 per buffer: W rows, then X rows
+  auto Wl = [&](int d) __attribute__((always_inline)) { return lds2 + d * BUF; };
+  auto Xl = [&](int d) __attribute__((always_inline)) { return lds2 + d * BUF + IC * KB * RS; };
   const int bid = blockIdx.x;
   const int p = (bid % 8) * ((nblocks + 7) / 8) + bid / 16;
   const int half = (bid / 8) % 2;
@@ -76,13 +103,7 @@ k_contract_mfma(const float2* __restrict__ X, const float2* __restrict__ W, floa
   const uint32_t wbytes = (uint32_t)((int64_t)Ci * Co * M * 8);
   const int Mi = (int)M;
 
-  // float4 q of a chunk: part = q % NP (modes 2*part, 2*part+1), row = q / NP.
-  // W rows: o = row % OH fastest, then the chunk's input channel.
-  // X rows: b = row % 32 fastest, then the chunk's input channel.
   float4 wr[WF4], xr[XF4];
-  // Entries outside the operands (mode >= M, channel >= Co, batch >= B) get
-  // an offset past the buffer end, which the buffer load returns as zero: no
-  // select on the loaded value, so every load of a chunk stays in flight.
   constexpr uint32_t kOut = 0x80000000u;
   auto load = [&](int i0) __attribute__((always_inline)) {
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(W, wbytes), rx = make_rsrc(X, xbytes);
@@ -108,43 +129,36 @@ k_contract_mfma(const float2* __restrict__ X, const float2* __restrict__ W, floa
     }
   };
   auto stash = [&](int buf) __attribute__((always_inline)) {
-    float* Ws = Wbuf(buf);
-    float* Xs = Xbuf(buf);
+    uint2* Ws = Wl(buf);
+    uint2* Xs = Xl(buf);
 #pragma unroll
     for (int j = 0; j < WF4; ++j) {
       const int q = tid + THREADS * j, part = q % NP, row = q / NP;
       const int o = row % OH, ii = row / OH, m = 2 * part;
-      float* d = Ws + (ii * KB + m) * MS + o;
-      d[0] = wr[j].x;
-      d[PS] = wr[j].y;
-      d[MS] = wr[j].z;
-      d[MS + PS] = wr[j].w;
+      uint2* d = Ws + (ii * KB + m) * RS + o;
+      d[0] = split2(wr[j].x, -wr[j].y);
+      d[RS] = split2(wr[j].z, -wr[j].w);
     }
 #pragma unroll
     for (int j = 0; j < XF4; ++j) {
       const int q = tid + THREADS * j, part = q % NP, row = q / NP;
       const int b = row & 31, ii = row >> 5, m = 2 * part;
-      float* d = Xs + (ii * KB + m) * XM + b;
-      d[0] = xr[j].x;
-      d[32] = xr[j].y;
-      d[XM] = xr[j].z;
-      d[XM + 32] = xr[j].w;
+      uint2* d = Xs + (ii * KB + m) * RS + b;
+      d[0] = split2(xr[j].x, xr[j].y);
+      d[RS] = split2(xr[j].z, xr[j].w);
     }
   };
 
-  v16f_c acc[MPW][2];
+  // acc[mode][row tile: Yr o 0-15, Yr o 16-31, Yi o 0-15, Yi o 16-31][batch tile]
+  v4f acc[MPW][4][2];
 #pragma unroll
   for (int mm = 0; mm < MPW; ++mm)
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[mm][t][r] = 0.f;
-  const int c = lane >> 5, oo = lane & 31;
-  const float sgn = c ? -1.f : 1.f;   // A[o][2i+1] = -Wi
+      for (int c = 0; c < 2; ++c) acc[mm][t][c] = v4f{0.f, 0.f, 0.f, 0.f};
+  const int r16 = lane & 15, g = lane >> 4;
 
-  // Double-buffered chunks: chunk n+1 is transposed into the other buffer
-  // while the MFMAs of chunk n run, and chunk n+2 is in flight meanwhile, so
-  // one barrier per chunk separates the phases.
   load(0);
   stash(0);
   if (IC < Ci) load(IC);
@@ -155,54 +169,61 @@ k_contract_mfma(const float2* __restrict__ X, const float2* __restrict__ W, floa
       stash(cb ^ 1);
       if (i0 + 2 * IC < Ci) load(i0 + 2 * IC);
     }
-    const float* Ws = Wbuf(cb);
-    const float* Xs = Xbuf(cb);
-    // operands of input channel s + 1 are read while the MFMAs of s run
-    float bv[2][MPW], ar[2][MPW], ai[2][MPW];
-    auto operands = [&](int s, int d) __attribute__((always_inline)) {
+    const uint2* Ws = Wl(cb);
+    const uint2* Xs = Xl(cb);
 #pragma unroll
-      for (int mm = 0; mm < MPW; ++mm) {
-        const int m = MPW * w + mm;
-        bv[d][mm] = Xs[(s * KB + m) * XM + c * 32 + oo];
-        const float* wrow = Ws + (s * KB + m) * MS + oo;
-        ar[d][mm] = wrow[c * PS];         // Yr rows: Wr (c=0), Wi (c=1, negated below)
-        ai[d][mm] = wrow[(1 - c) * PS];   // Yi rows: Wi (c=0), Wr (c=1)
+    for (int mm = 0; mm < MPW; ++mm) {
+      const int m = MPW * w + mm;
+      const uint2* w0 = Ws + ((2 * g) * KB + m) * RS + r16;
+      const uint2* x0 = Xs + ((2 * g) * KB + m) * RS + r16;
+      v4s ah[4], al[4], bh[2], bl[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const uint2 u0 = w0[16 * t], u1 = w0[KB * RS + 16 * t];
+        ah[t] = frag(u0.x, u1.x);
+        al[t] = frag(u0.y, u1.y);
+        ah[2 + t] = frag(rot_conj(u0.x), rot_conj(u1.x));
+        al[2 + t] = frag(rot_conj(u0.y), rot_conj(u1.y));
+        const uint2 v0 = x0[16 * t], v1 = x0[KB * RS + 16 * t];
+        bh[t] = frag(v0.x, v1.x);
+        bl[t] = frag(v0.y, v1.y);
       }
-    };
-    operands(0, 0);
+      // the small terms first, over all tiles, then the main term
 #pragma unroll
-    for (int s = 0; s < IC; ++s) {
-      if (s + 1 < IC) operands(s + 1, (s + 1) & 1);
-      __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead of the MFMAs
+      for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int mm = 0; mm < MPW; ++mm) {
-        acc[mm][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(sgn * ar[s & 1][mm], bv[s & 1][mm],
-                                                          acc[mm][0], 0, 0, 0);
-        acc[mm][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(ai[s & 1][mm], bv[s & 1][mm],
-                                                          acc[mm][1], 0, 0, 0);
-      }
-      __builtin_amdgcn_sched_barrier(0);
+        for (int c = 0; c < 2; ++c)
+          acc[mm][t][c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah[t], bl[c], acc[mm][t][c], 0, 0, 0);
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+          acc[mm][t][c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(al[t], bh[c], acc[mm][t][c], 0, 0, 0);
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+          acc[mm][t][c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah[t], bh[c], acc[mm][t][c], 0, 0, 0);
     }
-    __syncthreads();   // chunk n+1 is in place; chunk n's buffer is free
+    __syncthreads();
   }
-  // D[m][n]: lane l, register r holds row 8(r/4) + 4(l/32) + r%4 (channel),
-  // column l%32 (batch entry).  Y rows [b][o][k0 .. k0+KB) are 8*KB-byte runs:
-  // transpose through LDS, 16 batch entries at a time, and store whole runs.
-  constexpr int YB = 32 * KB * 2 + 8;   // LDS stride of one batch entry: [o][mode][re/im]
-  static_assert(16 * YB <= 2 * IC * KB * (MS + XM), "transpose tile fits the chunk buffers");
-#pragma unroll 1
+  // D[row][col]: lane l, register r holds row 4 (l / 16) + r, column l % 16.
+  // Batch tile hb at a time through LDS into [b][o][mode][re/im], then the
+  // rows [b][o][k0 .. k0+KB) as whole runs.
+  constexpr int YB = 32 * KB * 2 + 8;
+  static_assert(16 * YB * sizeof(float) <= lds_bytes(KB), "transpose tile fits the chunk buffers");
+  // unrolled: acc[..][hb] with a run-time hb would put acc in scratch memory
+#pragma unroll
   for (int hb = 0; hb < 2; ++hb) {
     __syncthreads();
-    if ((oo >> 4) == hb) {
 #pragma unroll
-      for (int mm = 0; mm < MPW; ++mm) {
-        float* d = smem + (oo & 15) * YB + (MPW * w + mm) * 2;
+    for (int mm = 0; mm < MPW; ++mm) {
+      float* d = smem + r16 * YB + (MPW * w + mm) * 2;
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < 4; ++t)
 #pragma unroll
-          for (int r = 0; r < 16; ++r)
-            d[(8 * (r >> 2) + 4 * c + (r & 3)) * KB * 2 + t] = acc[mm][t][r];
-      }
+        for (int r = 0; r < 4; ++r)
+          d[(16 * (t & 1) + 4 * g + r) * KB * 2 + (t >> 1)] = acc[mm][t][hb][r];
     }
     __syncthreads();
 #pragma unroll
@@ -215,7 +236,6 @@ k_contract_mfma(const float2* __restrict__ X, const float2* __restrict__ W, floa
       if (b < B && o0 + o < Co && k < M) {
         float2* yp = Y + ((int64_t)b * Co + o0 + o) * M;
         if (ymap_w) {
-          // rows of AC bins first, the DC column after them (see contract_mfma)
           const int m1 = Mi / ymap_w;
           auto map = [&](int kk) {
             const int j = kk / ymap_w, kw = kk - j * ymap_w;
@@ -248,19 +268,20 @@ static int launch_contract(const float2* X, const float2* W, float2* Y, int B, i
   const int nblocks = (int)((M + KB - 1) / KB);
   const int pairs16 = (nblocks + 7) / 8;              // groups of 8 blocks
   dim3 grid((unsigned)(pairs16 * 16), (unsigned)((B + 31) / 32));
-  const size_t lds = contract_lds(KB);
+  auto kern = k_contract_mfma<KB>;
+  const size_t lds = cb3::lds_bytes(KB);
   if (lds > 64 * 1024) {
-    int rc = hip_status(hipFuncSetAttribute(reinterpret_cast<const void*>(k_contract_mfma<KB>),
+    int rc = hip_status(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
                         "hipFuncSetAttribute(MaxDynamicSharedMemorySize)");
     if (rc) return rc;
   }
-  hipLaunchKernelGGL(k_contract_mfma<KB>, grid, dim3(contract_threads(KB)), lds, st, X, W, Y, B,
-                     Ci, Co, M, nblocks, ymap_w);
+  hipLaunchKernelGGL(kern, grid, dim3(contract_threads(KB)), lds, st, X, W, Y, B, Ci, Co, M,
+                     nblocks, ymap_w);
   return launch_status("k_contract_mfma");
 }
 
-// One workgroup per CU (the double-buffered tile takes 136-157 KB of LDS at
+// One workgroup per CU (the double-buffered tile takes 135-152 KB of LDS at
 // 16-18 modes); a grid just over the CU count would leave a few CUs a second
 // round, so such grids take the smallest wider block that fits one round.
 // ymap_w = 0: Y [B][Co][M] in the mode order of X and W.  ymap_w = W' > 0

@@ -15,7 +15,7 @@
 //                      x is read once, 16-byte loads, the next chunk's rows in
 //                      flight; 39 KB of LDS and <= 128 VGPRs let 4 workgroups
 //                      share a CU.
-// K2  contraction      fno_contract.hip (mode-wise complex GEMM on fp32 MFMA).
+// K2  contraction      fno_contract.hip (mode-wise complex GEMM on bf16-split MFMA).
 // K3  k_inv_cols       one workgroup per (b, o) plane: inverse FFT along H of
 //                      the m2h kept columns (zero-padded window rows), written
 //                      as one contiguous block Z[b][o][h][kw].
