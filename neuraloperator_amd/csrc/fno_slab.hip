@@ -94,19 +94,28 @@ k_slab_fwd64(const float* __restrict__ x, float2* __restrict__ out, int64_t slab
   __syncthreads();
 
   const int64_t nwaves = (int64_t)gridDim.x * kWaves;
+  // rows 16 mt + m of a slab, columns 32 ks + 8 G .. + 7.  Rolling
+  // prefetch: as soon as step 1 has issued the products of row tile mt, that
+  // tile's registers are loaded with the next slab's rows, so those loads are
+  // in flight during the rest of step 1, step 2 and the store
+  float4 xv[4][2][2];
+  auto load = [&](int64_t sl, int mt) __attribute__((always_inline)) {
+    const float* xs = x + sl * (kN * kN);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const float* p = xs + (16 * mt + n) * kN + 32 * ks + 8 * G;
+      xv[mt][ks][0] = load_nt(p);
+      xv[mt][ks][1] = load_nt(p + 4);
+    }
+  };
+  int64_t s = (int64_t)blockIdx.x * kWaves + (tid >> 6);
+  if (s < slabs) {
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) load(s, mt);
+  }
 #pragma unroll 1
-  for (int64_t s = (int64_t)blockIdx.x * kWaves + (tid >> 6); s < slabs; s += nwaves) {
-    // rows 16 mt + m of the slab, columns 32 ks + 8 G .. + 7
-    const float* xs = x + s * (kN * kN);
-    float4 xv[4][2][2];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const float* p = xs + (16 * mt + n) * kN + 32 * ks + 8 * G;
-        xv[mt][ks][0] = load_nt(p);
-        xv[mt][ks][1] = load_nt(p + 4);
-      }
+  for (; s < slabs; s += nwaves) {
+    const bool more = s + nwaves < slabs;
     v4f a1[4][2];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
@@ -128,6 +137,7 @@ k_slab_fwd64(const float* __restrict__ x, float2* __restrict__ out, int64_t slab
           a1[mt][nt] = mma3(ah, al, ff[((ks * 2 + nt) * 2) * 64 + lane],
                             ff[((ks * 2 + nt) * 2 + 1) * 64 + lane], a1[mt][nt]);
       }
+      if (more) load(s + nwaves, mt);
     }
     // step 2: k-step ks of the window product is row tile ks of step 1
     v4f a2[2] = {(v4f)0.f, (v4f)0.f};
