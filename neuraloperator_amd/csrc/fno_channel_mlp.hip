@@ -58,7 +58,10 @@ struct MlpLds {
   static constexpr int MT1 = CH / 16, MT2 = CO / 16, KB1 = (CI + 31) / 32, KB2 = (MT1 + 1) / 2;
   static constexpr size_t w1 = BF ? (size_t)MT1 * KB1 * 1024 : (size_t)CH * CI * 4;
   static constexpr size_t w2 = !TWO ? 0 : BF ? (size_t)MT2 * KB2 * 1024 : (size_t)CO * CH * 4;
-  static constexpr size_t total = w1 + w2 + (size_t)(CI * kMlpXS + 2 * CO) * 4;
+  // output tile [CO][TP] for 16-byte stores: the input slab when it is at
+  // least as tall, else a region of its own
+  static constexpr size_t ot = CO <= CI ? 0 : (size_t)CO * kMlpXS * 4;
+  static constexpr size_t total = w1 + w2 + (size_t)(CI * kMlpXS + 2 * CO) * 4 + ot;
 };
 }  // namespace
 
@@ -82,9 +85,8 @@ k_channel_mlp(const void* xv, const float* __restrict__ w1, const float* __restr
   YT* y = static_cast<YT*>(yv);
   static_assert(CI % 4 == 0 && CH % 16 == 0 && CO % 16 == 0, "channel multiples");
   static_assert(TWO || CH == CO, "one layer: CH == CO");
-  // outputs go back through the slab (as [CO][TP]) for 16-byte stores when
-  // they fit in it
-  constexpr bool STAGE = CO <= CI;
+  // outputs go back through LDS as a [CO][TP] tile (the slab, or a region of
+  // their own when CO > CI) for 16-byte stores
   constexpr int NQO = CO * kMlpTP / 4;                // float4s per output tile
   constexpr int LPO = (NQO + kMlpThreads - 1) / kMlpThreads;
   constexpr int KS1 = CI / 4, MT1 = CH / 16, MT2 = CO / 16;
@@ -102,6 +104,7 @@ k_channel_mlp(const void* xv, const float* __restrict__ w1, const float* __restr
   float* slab = reinterpret_cast<float*>(lds + LD::w1 + LD::w2);   // [CI][kMlpXS]
   float* bos = slab + CI * kMlpXS;                // [CO] output bias (+ gate bias)
   float* gws = bos + CO;                          // [CO] gate weight
+  float* otile = CO <= CI ? slab : gws + CO;      // [CO][kMlpXS] output tile
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int G = lane >> 4, t = lane & 15;
 
@@ -171,22 +174,6 @@ k_channel_mlp(const void* xv, const float* __restrict__ w1, const float* __restr
       return v;
   };
 
-  // skip input of the outputs this lane stores for tile `tile`
-  auto load_skip = [&](int64_t tile, float (&dst)[2][MT2][4]) __attribute__((always_inline)) {
-    const int64_t b = tile / tiles_per_sample;
-    const int64_t p0 = (tile % tiles_per_sample) * kMlpTP;
-#pragma unroll
-    for (int n = 0; n < 2; ++n) {
-      const int64_t p = p0 + 32 * wave + 16 * n + t;
-#pragma unroll
-      for (int mo = 0; mo < MT2; ++mo)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          dst[n][mo][r] = has_skip && p < P && 16 * mo + 4 * G + r < co
-                              ? xs[(b * co + 16 * mo + 4 * G + r) * P + p] : 0.f;
-    }
-  };
-
   int64_t tile = blockIdx.x;
   if (tile < tiles) load_slab(tile);
   for (; tile < tiles; tile += gridDim.x) {
@@ -203,20 +190,16 @@ k_channel_mlp(const void* xv, const float* __restrict__ w1, const float* __restr
     const int64_t p0 = (tile % tiles_per_sample) * kMlpTP;
     if (tile + gridDim.x < tiles) load_slab(tile + gridDim.x);
     // the skip input of this tile's outputs, in flight during the GEMMs
-    float sv[2][MT2][4];
     float4 svq[LPO];
-    if constexpr (STAGE) {
 #pragma unroll
-      for (int j = 0; j < LPO; ++j) {
-        const int q = tid + kMlpThreads * j;
-        const int c = q / (kMlpTP / 4);
-        const int64_t p = p0 + 4 * (q % (kMlpTP / 4));
-        svq[j] = has_skip && q < NQO && c < co && p < P
-                     ? *reinterpret_cast<const float4*>(xs + (b * co + c) * P + p)
-                     : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-    } else {
-      load_skip(tile, sv);
+    for (int j = 0; j < LPO; ++j) {
+      const int q = tid + kMlpThreads * j;
+      const int c = q / (kMlpTP / 4);
+      const int64_t p = p0 + 4 * (q % (kMlpTP / 4));
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (has_skip && q < NQO && c < co && p < P)
+        v = *reinterpret_cast<const float4*>(xs + (b * co + c) * P + p);
+      svq[j] = v;
     }
 
     // GEMM 1: h[16m + row][point] over the wave's 2 column tiles
@@ -305,69 +288,48 @@ k_channel_mlp(const void* xv, const float* __restrict__ w1, const float* __restr
       }
     }
 
-    if constexpr (STAGE) {
-      // every wave is past GEMM 1: the slab becomes the [CO][TP] output tile
-      __syncthreads();
+    // every wave is past GEMM 1 (the slab may be the output tile)
+    __syncthreads();
 #pragma unroll
-      for (int n = 0; n < 2; ++n)
-#pragma unroll
-        for (int mo = 0; mo < MT2; ++mo)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int row = 16 * mo + 4 * G + r;
-            slab[row * kMlpXS + out_col(row, 32 * wave + 16 * n + t)] = o[mo][n][r];
-          }
-      __syncthreads();
-#pragma unroll
-      for (int j = 0; j < LPO; ++j) {
-        const int q = tid + kMlpThreads * j;
-        const int c = q / (kMlpTP / 4);
-        const int64_t p = p0 + 4 * (q % (kMlpTP / 4));
-        if (q >= NQO || c >= co || p >= P) continue;
-        float4 v = *reinterpret_cast<const float4*>(slab + c * kMlpXS + out_col(c, 4 * (q % (kMlpTP / 4))));
-        const float bb = bos[c], gg = gws[c];
-        v.x += bb; v.y += bb; v.z += bb; v.w += bb;
-        if (has_skip) {
-          v.x = fmaf(gg, svq[j].x, v.x);
-          v.y = fmaf(gg, svq[j].y, v.y);
-          v.z = fmaf(gg, svq[j].z, v.z);
-          v.w = fmaf(gg, svq[j].w, v.w);
-        }
-        if (gelu_out) {
-          v.x = gelu_erf(v.x);
-          v.y = gelu_erf(v.y);
-          v.z = gelu_erf(v.z);
-          v.w = gelu_erf(v.w);
-        }
-        if constexpr (YBF) {
-          auto pk = [](float a, float b) __attribute__((always_inline)) {
-            return (uint32_t)__builtin_bit_cast(unsigned short, (__bf16)a) |
-                   ((uint32_t)__builtin_bit_cast(unsigned short, (__bf16)b) << 16);
-          };
-          *reinterpret_cast<uint2*>(y + (b * co + c) * P + p) = make_uint2(pk(v.x, v.y), pk(v.z, v.w));
-        } else {
-          *reinterpret_cast<float4*>(y + (b * co + c) * P + p) = v;
-        }
-      }
-      continue;
-    }
-    // epilogue: output channel 16 mo + 4G + r, point p0 + 32 wave + 16 n + t
-#pragma unroll
-    for (int n = 0; n < 2; ++n) {
-      const int64_t p = p0 + 32 * wave + 16 * n + t;
-      if (p >= P) continue;
+    for (int n = 0; n < 2; ++n)
 #pragma unroll
       for (int mo = 0; mo < MT2; ++mo)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int oc = 16 * mo + 4 * G + r;
-          if (oc >= co) continue;
-          const int64_t idx = (b * co + oc) * P + p;
-          float v = o[mo][n][r] + bos[oc];
-          if (has_skip) v = fmaf(gws[oc], sv[n][mo][r], v);
-          if (gelu_out) v = gelu_erf(v);
-          y[idx] = (YT)v;
+          const int row = 16 * mo + 4 * G + r;
+          otile[row * kMlpXS + out_col(row, 32 * wave + 16 * n + t)] = o[mo][n][r];
         }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < LPO; ++j) {
+      const int q = tid + kMlpThreads * j;
+      const int c = q / (kMlpTP / 4);
+      const int64_t p = p0 + 4 * (q % (kMlpTP / 4));
+      if (q >= NQO || c >= co || p >= P) continue;
+      float4 v = *reinterpret_cast<const float4*>(otile + c * kMlpXS + out_col(c, 4 * (q % (kMlpTP / 4))));
+      const float bb = bos[c], gg = gws[c];
+      v.x += bb; v.y += bb; v.z += bb; v.w += bb;
+      if (has_skip) {
+        v.x = fmaf(gg, svq[j].x, v.x);
+        v.y = fmaf(gg, svq[j].y, v.y);
+        v.z = fmaf(gg, svq[j].z, v.z);
+        v.w = fmaf(gg, svq[j].w, v.w);
+      }
+      if (gelu_out) {
+        v.x = gelu_erf(v.x);
+        v.y = gelu_erf(v.y);
+        v.z = gelu_erf(v.z);
+        v.w = gelu_erf(v.w);
+      }
+      if constexpr (YBF) {
+        auto pk = [](float a, float b) __attribute__((always_inline)) {
+          return (uint32_t)__builtin_bit_cast(unsigned short, (__bf16)a) |
+                 ((uint32_t)__builtin_bit_cast(unsigned short, (__bf16)b) << 16);
+        };
+        *reinterpret_cast<uint2*>(y + (b * co + c) * P + p) = make_uint2(pk(v.x, v.y), pk(v.z, v.w));
+      } else {
+        *reinterpret_cast<float4*>(y + (b * co + c) * P + p) = v;
+      }
     }
   }
 }
