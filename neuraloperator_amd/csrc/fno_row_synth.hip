@@ -96,10 +96,12 @@ __device__ __forceinline__ float synth_entry(int j, int col, int W, int m2h, flo
 // block boundaries too.  Two barriers per block.
 //
 // Workgroup -> blocks: when the batch is a multiple of the 8 XCDs and the
-// grid is 8 x (H / R) workgroups, workgroup g (placed on XCD g mod 8) takes
-// residue r = g / 8 of samples g mod 8, g mod 8 + 8, ...: the workgroups of
-// one XCD work on one sample at a time, so that sample's 1 MB spectrum stays
-// in the XCD's L2.  Otherwise blocks are dealt out in a stride.
+// CU count is a multiple of 8 x (H / R), the grid is one workgroup per CU and
+// workgroup g (placed on XCD g mod 8) takes residue i mod (H / R), i = g / 8,
+// of samples g mod 8 + 8 (i / (H / R)) + 8 S k, k = 0, 1, ... (S = CUs /
+// (8 H / R) samples per XCD at a time): the workgroups of one XCD work on S
+// samples at a time, so their spectra stay in the XCD's L2.  Otherwise blocks
+// are dealt out in a stride.
 namespace rs {
 constexpr int R = 8;                     // rows per block
 constexpr int kHidden = 32;              // hidden units of a folded channel MLP
@@ -165,8 +167,11 @@ k_row_synth(const typename RowIO<BF>::T* __restrict__ x, const float2* __restric
   // block index k of this workgroup -> (sample, residue), or -1 past the end
   auto block_of = [&](int k, int& b, int& r) __attribute__((always_inline)) -> bool {
     if (xcd_map) {
-      b = (int)(blockIdx.x & 7) + 8 * k;
-      r = (int)(blockIdx.x >> 3);
+      // xcd_map = S samples per XCD at a time: workgroup g takes residue
+      // (g / 8) % NR of the XCD's sample slot (g / 8) / NR
+      const int i = (int)(blockIdx.x >> 3), sl = i / NR;
+      b = (int)(blockIdx.x & 7) + 8 * (sl + xcd_map * k);
+      r = i - sl * NR;
       return b < B;
     }
     const int64_t e = (int64_t)blockIdx.x + (int64_t)gridDim.x * k;
@@ -623,12 +628,13 @@ static int launch_rowsynth(const typename RowIO<BF>::T* x, const float2* yhat, c
   const int NR = H / rs::R;
   const int64_t nblocks = (int64_t)B * NR;
   const int cus = device_cus();
-  // XCD-grouped blocks when every XCD gets whole samples and the grid is one
-  // workgroup per CU; otherwise a stride over all blocks
-  const bool xcd = (B % 8 == 0) && (8 * NR == cus);
-  const int64_t grid = xcd ? 8 * NR : (nblocks < cus ? nblocks : cus);
+  // XCD-grouped blocks when every XCD gets whole samples and one workgroup
+  // per CU covers S whole samples' residues per XCD (S = 1 at 256 rows, 2 at
+  // 128); otherwise a stride over all blocks
+  const int S = (B % 8 == 0 && cus % (8 * NR) == 0) ? cus / (8 * NR) : 0;
+  const int64_t grid = S ? cus : (nblocks < cus ? nblocks : cus);
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(rg::kThreads), lds, st, x, yhat, skip_w,
-                     bias, y, B, H, m1, m2h, skip_kind, act, s, xcd ? 1 : 0, mlp);
+                     bias, y, B, H, m1, m2h, skip_kind, act, s, S, mlp);
   return launch_status("k_row_synth");
 }
 
