@@ -107,8 +107,11 @@ constexpr int R = 8;                     // rows per block
 constexpr int kHidden = 32;              // hidden units of a folded channel MLP
 }  // namespace rs
 static constexpr int kSynthMaxM1 = 128;   // window rows of the LDS twiddle table
+// window rows whose loads are issued together: 4 keeps the 256-pixel row
+// kernels free of spills (8: 15 VGPRs spilled) and measured 1-3% faster at
+// B32 C64 128^2 and 256^2 than 8 or 16, on a par with 2
 #ifndef SYN_BATCH
-#define SYN_BATCH 8                      // window rows whose loads are issued together
+#define SYN_BATCH 4
 #endif
 
 // BF: x and y are bfloat16 (activation storage of the bf16 FNO forward); x
