@@ -242,6 +242,8 @@ class FNOBlocks(nn.Module):
             return False   # the composed path carries the gradients
         if self.norm is not None or self.stabilizer is not None or self.preactivation:
             return False
+        if conv.fno_block_precision in ("half", "mixed"):
+            return False   # the conv's own forward restates the half arithmetic
         if self.non_linearity is not F.gelu:
             return False
         if output_shape is not None or conv.resolution_scaling_factor is not None:

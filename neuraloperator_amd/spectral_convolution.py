@@ -341,6 +341,13 @@ class _SpectralConvComplexFn(torch.autograd.Function):
         return gx, gw, gb, None, None, None, None
 
 
+def _fp16_round(t: torch.Tensor) -> torch.Tensor:
+    """Round to float16 (nearest even) and widen back; complex part by part."""
+    if t.is_complex():
+        return torch.complex(_fp16_round(t.real), _fp16_round(t.imag))
+    return t.half().float()
+
+
 def _attach(y, *params):
     if torch.is_grad_enabled() and any(p is not None and p.requires_grad for p in params):
         return _NoGradThroughHip.apply(y, *[p for p in params if p is not None])
@@ -499,14 +506,61 @@ class SpectralConv(BaseSpectralConv):
             if torch.is_grad_enabled() and (x.requires_grad or
                                             any(p.requires_grad for p in self.parameters())):
                 y = self._forward_autograd(x, output_shape)
+            elif self._half_arithmetic():
+                return self._forward_half(x, output_shape)
             else:
                 y = self._forward_hip(x, output_shape)
             # fno_block_precision 'half' / 'mixed' (:436-459): the reference's
             # inverse returns float16, promoted to float32 by the float32 bias
-            # when there is one; the kernels compute in fp32 either way
+            # when there is one (with gradients and for factorized contractions
+            # the values are the fp32 ones)
             if self.fno_block_precision in ("half", "mixed") and self.bias is None:
                 y = y.half()
             return y
+
+    def _half_arithmetic(self) -> bool:
+        """fno_block_precision 'half' / 'mixed' with a contraction whose
+        complex-half arithmetic _forward_half restates: a dense window weight
+        (dense, or factorized and reconstructed), real data."""
+        return (self.fno_block_precision in ("half", "mixed") and not self.complex_data and
+                self._contract in ("dense", "dense_separable"))
+
+    def _forward_half(self, x, output_shape=None):
+        """fno_block_precision 'half' / 'mixed' (spectral_convolution.py
+        :436-462, :520-568 with _contract_dense on complex32, einsum_utils.py
+        :10-34), rounded where the reference holds half precision: x ('half'
+        only), the kept spectrum (complex32), the weight and each of the four
+        real partial contractions of the complex-half einsum, their
+        combination Re = t00 - t11, Im = t10 + t01, and the inverse's output.
+        The library's transforms and contraction run in fp32 between those
+        roundings; the complex32 intermediate between the reference's split
+        inverse transforms (ifftn over the leading axes, then irfft) is not
+        rounded here (its effect on y is below one float16 step of the output).
+        Returns float16, or float32 after the float32 bias."""
+        sizes = list(x.shape[2:])
+        kept, sl = self.window(sizes)
+        out_sizes = self.output_sizes(sizes, output_shape)
+        xin = x.detach()
+        if self.fno_block_precision == "half":
+            xin = _fp16_round(xin)
+        X = _fp16_round(Fh.rfft_window(xin, kept, self.fft_norm))
+        W = self.dense_window_weight(sl).detach()
+        if self.separable:
+            # complex32 x times the complex64 weight, rounded by the store
+            Y = _fp16_round(X * W)
+        else:
+            z = torch.zeros_like(W.real)
+            A = Fh.contract_dense(X, torch.complex(_fp16_round(W.real), z))    # t00 + i t10
+            Bq = Fh.contract_dense(X, torch.complex(_fp16_round(W.imag), z))   # t01 + i t11
+            t00, t10 = _fp16_round(A.real), _fp16_round(A.imag)
+            t01, t11 = _fp16_round(Bq.real), _fp16_round(Bq.imag)
+            Y = torch.complex(_fp16_round(t00 - t11), _fp16_round(t10 + t01))
+        y = Fh.irfft_window(Y.contiguous(), sizes, out_sizes, None, self.fft_norm,
+                            self.enforce_hermitian_symmetry)
+        y = y.half()
+        if self.bias is not None:
+            y = y + self.bias.detach()
+        return y
 
     def _forward_complex(self, x, output_shape=None):
         """complex_data=True: fftn / window / contraction / ifftn on complex

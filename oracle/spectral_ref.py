@@ -113,6 +113,28 @@ def contract_dense_separable(x, weight, separable=True):
     return x * weight
 
 
+def fp16_round(t):
+    """Round to the nearest float16 (ties to even) and widen back; complex
+    tensors part by part (the values a complex32 tensor holds)."""
+    if t.is_complex():
+        return torch.complex(fp16_round(t.real), fp16_round(t.imag))
+    return t.to(torch.float16).to(t.dtype)
+
+
+def contract_dense_complexhalf(x, weight, separable=False):
+    """_contract_dense on complex32 operands (spectral_convolution.py:41-43 ->
+    einsum_utils.py:10-34): both operands viewed as real pairs and rounded to
+    float16, one real contraction per (x part, weight part) pair, each result
+    rounded to float16 (half GEMM, fp32 accumulation: float64 here), then
+    Re = tmp[0, 0] - tmp[1, 1] and Im = tmp[1, 0] + tmp[0, 1] in float16."""
+    xr, xi = fp16_round(x.real), fp16_round(x.imag)
+    wr, wi = fp16_round(weight.real), fp16_round(weight.imag)
+    c = lambda a, b: fp16_round(contract_dense(a, b, separable))
+    t00, t11 = c(xr, wr), c(xi, wi)
+    t10, t01 = c(xi, wr), c(xr, wi)
+    return torch.complex(fp16_round(t00 - t11), fp16_round(t10 + t01))
+
+
 def contract_tucker(x, core, factors, separable=False):
     """spectral_convolution.py:76-103 (einsum with core and all factors)."""
     order = x.ndim
@@ -210,6 +232,7 @@ def spectral_conv_forward(
     resolution_scaling_factor=None,
     factorization: Optional[str] = None,
     implementation: str = "reconstructed",
+    precision: str = "full",
 ):
     """Forward of a SpectralConv, op for op.
 
@@ -217,7 +240,21 @@ def spectral_conv_forward(
     n//2+1 for real data).  ``weight`` is either a dense complex tensor of the
     max_n_modes window, or a dict describing a factorized weight:
     {"tucker": (core, factors)}, {"cp": (weights, factors)}, {"tt": factors}.
+
+    ``precision`` is fno_block_precision (spectral_convolution.py:436-462):
+    'half' rounds x to float16 before the transform, 'half' and 'mixed' hold
+    the spectrum in complex32 (``fp16_round`` after the forward transform),
+    contract through the complex-half einsum and hold out_fft, the
+    intermediate of the split inverse and the inverse's output in half
+    precision.  The float16 transforms themselves are restated as exact
+    transforms rounded once, and only dense (or reconstructed) real-data
+    weights are covered.
     """
+    half = precision in ("half", "mixed")
+    if half and (complex_data or (isinstance(weight, dict) and implementation == "factorized")):
+        raise NotImplementedError("half precision: dense / reconstructed real-data weights only")
+    if precision == "half":                            # :436-437
+        x = fp16_round(x)
     if max_n_modes is None:
         max_n_modes = list(n_modes)
     order = len(n_modes)
@@ -235,6 +272,8 @@ def spectral_conv_forward(
         dims_to_fft_shift = fft_dims[:-1]
     if order > 1:                                      # :448-449
         xf = torch.fft.fftshift(xf, dim=dims_to_fft_shift)
+    if half:                                           # :451-454 (and the half rfftn)
+        xf = fp16_round(xf)
 
     cdtype = xf.dtype
     if isinstance(weight, dict):
@@ -253,7 +292,15 @@ def spectral_conv_forward(
     sl_x = x_slices(fft_size, kept)                    # :500-519
     xs = xf[sl_x]
 
-    if isinstance(weight, dict):
+    if half and isinstance(weight, dict):              # reconstructed, then dense
+        w = _reconstruct_window(weight, sl_w).to(cdtype)
+    if half and separable:
+        # complex32 x times the complex64 weight promotes to complex64; the
+        # store into the complex32 out_fft rounds
+        y = fp16_round(contract_dense_separable(xs, w.to(cdtype)))
+    elif half:
+        y = contract_dense_complexhalf(xs, w.to(cdtype))
+    elif isinstance(weight, dict):
         y = _contract_factorized(xs, weight, sl_w, w_start, separable, implementation, cdtype)
     elif separable:
         y = contract_dense_separable(xs, w.to(cdtype))
@@ -275,6 +322,8 @@ def spectral_conv_forward(
     elif enforce_hermitian_symmetry:                   # :547-559
         if order > 1:
             out_fft = torch.fft.ifftn(out_fft, s=mode_sizes[:-1], dim=fft_dims[:-1], norm=fft_norm)
+            if half:
+                out_fft = fp16_round(out_fft)
         else:
             # ifftn over zero dims is the identity, but torch still returns a copy
             out_fft = out_fft.clone()
@@ -284,6 +333,8 @@ def spectral_conv_forward(
         out = torch.fft.irfft(out_fft, n=mode_sizes[-1], dim=fft_dims[-1], norm=fft_norm)
     else:                                              # :564
         out = torch.fft.irfftn(out_fft, s=mode_sizes, dim=fft_dims, norm=fft_norm)
+    if half:
+        out = fp16_round(out)
 
     if bias is not None:                               # :567-568
         out = out + bias
@@ -343,6 +394,18 @@ def _contract_factorized(xs, weight, sl_w, w_start, separable, implementation, c
     if separable:
         return contract_dense_separable(xs, full)
     return contract_dense(xs, full)
+
+
+def _reconstruct_window(weight, sl_w):
+    """The dense window of a sliced factorized weight (tltorch to_tensor of
+    FactorizedTensor.__getitem__, as _contract_factorized's 'reconstructed')."""
+    if "tucker" in weight:
+        core, factors = weight["tucker"]
+        return tucker_to_tensor(core, [U[s] for U, s in zip(factors, sl_w)])
+    if "cp" in weight:
+        w, factors = weight["cp"]
+        return cp_to_tensor(w, [U[s] for U, s in zip(factors, sl_w)])
+    return tt_to_tensor([G[:, s, :] for G, s in zip(weight["tt"], sl_w)])
 
 
 # ---------------------------------------------------------------------------

@@ -887,20 +887,37 @@ def test_complex_data_tucker(cuda_device):
 
 @pytest.mark.parametrize("precision", ["half", "mixed"])
 @pytest.mark.parametrize("bias", [True, False])
-def test_block_precision_output_dtype(precision, bias, cuda_device):
+@pytest.mark.parametrize("shape,modes,separable", [((2, 3, 12, 12), (6, 6), False),
+                                                   ((2, 3, 64), (10,), False),
+                                                   ((2, 4, 16, 12), (8, 6), True)])
+def test_block_precision_half_arithmetic(precision, bias, shape, modes, separable, cuda_device):
     """fno_block_precision 'half' / 'mixed': output dtype as the reference's
-    (float16 from the inverse, float32 once the float32 bias is added); the
-    values are the fp32 computation."""
+    (float16 from the inverse, float32 once the float32 bias is added) and the
+    values of the oracle restating the complex-half arithmetic
+    (spectral_convolution.py:436-462, einsum_utils.py:10-34).  Bound: 3e-3 of
+    max |y| (a few float16 steps: the kernels round the same intermediates,
+    but fp32 and float64 can land on different sides of a float16 rounding
+    boundary, and the complex32 intermediate of the split inverse is not
+    rounded on the GPU); 1D has no such intermediate: 2e-3.  The half result
+    sits closer to the half oracle than to the full-precision one."""
+    print(f"half arithmetic {precision} bias={bias} {shape} {modes} sep={separable}", flush=True)
     torch.manual_seed(24)
-    conv = na.SpectralConv(3, 4, (6, 6), bias=bias, fno_block_precision=precision).to(cuda_device)
-    x = torch.randn(2, 3, 12, 12)
+    C = shape[1]
+    conv = na.SpectralConv(C, C if separable else 4, modes, bias=bias, separable=separable,
+                           fno_block_precision=precision).to(cuda_device)
+    x = torch.randn(*shape)
     with torch.no_grad():
         y = conv(x.to(cuda_device))
     assert y.dtype == (torch.float32 if bias else torch.float16)
-    ref = R.spectral_conv_forward(x.double(), conv.weight.to_tensor().detach().cpu().to(torch.complex128),
-                                  conv.bias.detach().cpu().double() if bias else None, conv.n_modes,
-                                  conv.max_n_modes)
-    assert rel_err(y, ref) <= (TOL if bias else 2e-3)
+    w = conv.weight.to_tensor().detach().cpu().to(torch.complex128)
+    b = conv.bias.detach().cpu().double() if bias else None
+    kw = dict(separable=separable)
+    ref_h = R.spectral_conv_forward(x.double(), w, b, conv.n_modes, conv.max_n_modes,
+                                    precision=precision, **kw)
+    ref_f = R.spectral_conv_forward(x.double(), w, b, conv.n_modes, conv.max_n_modes, **kw)
+    assert rel_err(y, ref_h) <= (2e-3 if len(shape) == 3 else 3e-3)
+    dev = lambda r: (y.double().cpu() - r).abs().mean().item()
+    assert dev(ref_h) < dev(ref_f)
 
 
 def test_fno_staged_matches_oracle(cuda_device):

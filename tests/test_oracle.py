@@ -366,3 +366,64 @@ def test_oracle_reproduces_golden(path):
         y = R.gelu(y + R.linear_skip(x, torch.from_numpy(d["skip_w"]).double()))
     exp = d["expected"]
     assert np.abs(y.numpy() - exp).max() <= 1e-6 * np.abs(exp).max()
+
+
+# ------------------------------------------------- fno_block_precision half
+def test_fp16_round_ties_to_even():
+    """float16 has 10 fraction bits: 1 + 2^-11 is half way between 1 and
+    1 + 2^-10 (goes to the even 1), 1 + 3 2^-11 half way between 1 + 2^-10
+    and 1 + 2^-9 (goes to the even 1 + 2^-9); 2049 lies between 2048 and
+    2050 (spacing 2) and goes to 2048; complex parts round separately."""
+    t = torch.tensor([1 + 2 ** -11, 1 + 3 * 2 ** -11, 2049.0, -2049.0, 1 + 2 ** -10],
+                     dtype=torch.float64)
+    want = torch.tensor([1.0, 1 + 2 ** -9, 2048.0, -2048.0, 1 + 2 ** -10], dtype=torch.float64)
+    assert torch.equal(R.fp16_round(t), want)
+    c = torch.complex(t, t.flip(0))
+    assert torch.equal(R.fp16_round(c), torch.complex(want, want.flip(0)))
+
+
+def test_complexhalf_contraction_rounds_partial_sums():
+    """einsum_utils.py:10-34 rounds each real partial contraction to float16
+    before Re = t00 - t11: with Xr = (2048, 1), Wr = (1, 1) the exact
+    t00 = 2049 becomes 2048, and t11 = Xi . Wi = 1, so Re = 2047 where the
+    exact complex product gives 2048; Im = fp16(t10 + t01) = fp16(1 + 2048) =
+    2048.  Swapping the pairing (Re = t00 - t10, say) or dropping a rounding
+    changes the answer."""
+    f64 = lambda v: torch.tensor(v, dtype=torch.float64)
+    x = torch.complex(f64([2048.0, 1.0]), f64([1.0, 0.0]))
+    w = torch.complex(f64([1.0, 1.0]), f64([1.0, 0.0]))
+    xs = x.reshape(1, 2, 1)          # [B, Ci, mode]
+    ws = w.reshape(2, 1, 1)          # [Ci, Co, mode]
+    y = R.contract_dense_complexhalf(xs, ws)
+    assert y.shape == (1, 1, 1)
+    assert y.real.item() == 2047.0 and y.imag.item() == 2048.0
+    exact = R.contract_dense(xs, ws)
+    assert exact.real.item() == 2048.0 and exact.imag.item() == 2049.0
+
+
+def test_complexhalf_contraction_exact_on_small_integers():
+    """With operands and every partial sum exactly representable in float16
+    (small integers), the complex-half contraction equals the exact one."""
+    g = torch.Generator().manual_seed(5)
+    xs = torch.complex(torch.randint(-4, 5, (2, 3, 4, 3), generator=g).double(),
+                       torch.randint(-4, 5, (2, 3, 4, 3), generator=g).double())
+    ws = torch.complex(torch.randint(-4, 5, (3, 5, 4, 3), generator=g).double(),
+                       torch.randint(-4, 5, (3, 5, 4, 3), generator=g).double())
+    assert torch.equal(R.contract_dense_complexhalf(xs, ws), R.contract_dense(xs, ws))
+
+
+@pytest.mark.parametrize("precision", ["half", "mixed"])
+def test_half_precision_forward_output_is_float16(precision):
+    """The half forward's output (before the bias) is float16-valued, and
+    with x exactly representable in float16 'half' and 'mixed' agree (they
+    differ only in rounding x before the transform)."""
+    g = torch.Generator().manual_seed(6)
+    x = (torch.randint(-64, 65, (2, 3, 16, 12), generator=g) / 32).double()
+    w = torch.complex(torch.randn(3, 4, 8, 7, generator=g, dtype=torch.float64),
+                      torch.randn(3, 4, 8, 7, generator=g, dtype=torch.float64))
+    y = R.spectral_conv_forward(x, w, None, [8, 7], [8, 7], precision=precision)
+    assert torch.equal(R.fp16_round(y), y)
+    other = "mixed" if precision == "half" else "half"
+    assert torch.equal(y, R.spectral_conv_forward(x, w, None, [8, 7], [8, 7], precision=other))
+    full = R.spectral_conv_forward(x, w, None, [8, 7], [8, 7])
+    assert 0 < (y - full).abs().max().item() <= 4e-3 * full.abs().max().item()
