@@ -28,7 +28,7 @@ def _inputs(B, C, sizes, modes, seed, dev):
     return [t.to(dev) for t in (x, w, ws, bias)]
 
 
-def _run_both(B, C, sizes, modes, seed, dev):
+def _run_both(B, C, sizes, modes, seed, dev, skip=nat.SKIP_LINEAR):
     lib = nat.load()
     x, w, ws, bias = _inputs(B, C, sizes, modes, seed, dev)
     nd = len(sizes)
@@ -39,10 +39,10 @@ def _run_both(B, C, sizes, modes, seed, dev):
     y_ref = torch.empty_like(x)
     y = torch.full_like(x, float("nan"))
     nat.check(lib.fno_spectral_block_f32(_ptr(x), _ptr(w), _ptr(bias), _ptr(ws), _ptr(y_ref), B, C,
-                                         C, nd, sz, md, 1, nat.SKIP_LINEAR, nat.ACT_GELU,
+                                         C, nd, sz, md, 1, skip, nat.ACT_GELU,
                                          _ptr(work), wsb, st), "fno_spectral_block_f32")
     nat.check(lib.fno_spectral_block_f32_noalloc(_ptr(x), _ptr(w), _ptr(bias), _ptr(ws), _ptr(y), B,
-                                                 C, C, nd, sz, md, 1, nat.SKIP_LINEAR,
+                                                 C, C, nd, sz, md, 1, skip,
                                                  nat.ACT_GELU, st),
               "fno_spectral_block_f32_noalloc")
     torch.cuda.synchronize()
@@ -62,6 +62,20 @@ def test_noalloc_matches_workspace_entry_point(first, second, cuda_device):
         y, y_ref, wsb = _run_both(B, C, sizes, modes, 100 + i, cuda_device)
         if i == 0:
             assert wsb > SCRATCH, "the first call should span several chunks"
+        assert torch.isfinite(y).all()
+        err = ((y - y_ref).abs().max() / y_ref.abs().max()).item()
+        assert err <= 1e-6, err
+
+
+@pytest.mark.parametrize("skip", [nat.SKIP_IDENTITY, nat.SKIP_NONE, nat.SKIP_SOFT_GATING])
+def test_noalloc_1d_line_path(skip, cuda_device):
+    """The 1D block without a linear skip (one DFT wave per line, then the
+    contraction and synthesis per 4 output channels, the spectra passing
+    through the scratch array): 16 x 64 lines of 1024 points with 16 bins,
+    then 3 x 32 lines of 256 points with 9 bins."""
+    for i, (B, C, sizes, modes) in enumerate(((16, 64, (1024,), (16,)), (3, 32, (256,), (9,)))):
+        print(f"noalloc 1d call {i}: B{B} C{C} {sizes} modes {modes} skip {skip}", flush=True)
+        y, y_ref, _ = _run_both(B, C, sizes, modes, 200 + i, cuda_device, skip)
         assert torch.isfinite(y).all()
         err = ((y - y_ref).abs().max() / y_ref.abs().max()).item()
         assert err <= 1e-6, err
