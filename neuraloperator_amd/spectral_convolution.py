@@ -221,9 +221,19 @@ class _SpectralConvFn(torch.autograd.Function):
         kept, norm, sizes = ctx.kept, ctx.fft_norm, ctx.sizes
         gy = gy.contiguous().float()
         dual = _DUAL_NORM[norm]
-        gY = _inverse_adjoint(gy, kept, sizes, ctx.out_sizes, dual, ctx.enforce)
+        same_dense = ctx.out_sizes == sizes and not ctx.separable
+        gY = None
+        if ctx.needs_input_grad[1] or (ctx.needs_input_grad[0] and not same_dense):
+            gY = _inverse_adjoint(gy, kept, sizes, ctx.out_sizes, dual, ctx.enforce)
         gx = gw = gb = None
-        if ctx.needs_input_grad[0]:
+        if ctx.needs_input_grad[0] and same_dense:
+            # on the input grid the Hermitian weights cancel (gX / c with gY =
+            # c . F_dual gy), so gx = I_dual(conj(W)^T . F_dual gy) is the
+            # spectral block itself with the transposed conjugate weight and the
+            # dual norm: one call of the fused forward kernels
+            wt = w.conj().transpose(0, 1).contiguous()              # [Co, Ci, *m]
+            gx = Fh.spectral_block(gy, wt, None, kept, nat.SKIP_NONE, None, nat.ACT_NONE, dual)
+        elif ctx.needs_input_grad[0]:
             if ctx.separable:
                 gX = Fh.contract_dense(gY.contiguous(), w.conj().contiguous(), separable=True)
             else:

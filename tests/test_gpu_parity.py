@@ -559,6 +559,37 @@ def test_spectral_conv_gradients(dim, sizes, nm, norm, cuda_device):
     assert rel_err(conv.bias.grad, bd.grad) <= TOL
 
 
+@pytest.mark.parametrize("B,Ci,Co,sizes,nm,norm", [
+    (2, 64, 64, (64, 128), (16, 16), "forward"),    # adjoint block: fused 2D path
+    (2, 32, 32, (128, 256), (32, 32), "backward"),
+    (3, 12, 8, (256,), (12,), "forward"),           # adjoint block: 1D line path (8 -> 12)
+    (2, 64, 64, (1024,), (30,), "ortho"),
+])
+def test_spectral_conv_gradients_fused_adjoint(B, Ci, Co, sizes, nm, norm, cuda_device):
+    """On the input grid the x gradient is the spectral block of the output
+    cotangent with the transposed conjugate weight and the dual norm
+    (the Hermitian weights cancel): shapes whose adjoint block takes the fused
+    2D kernels or the 1D line path, against torch autograd through the
+    float64 oracle."""
+    print(f"fused adjoint grad B{B} {Ci}->{Co} {sizes} {nm} {norm}", flush=True)
+    torch.manual_seed(19)
+    conv = na.SpectralConv(Ci, Co, nm, fft_norm=norm).to(cuda_device)
+    with torch.no_grad():
+        conv.bias.normal_()
+    x = torch.randn(B, Ci, *sizes)
+    g = torch.randn(B, Co, *sizes)
+    xg = x.to(cuda_device).requires_grad_(True)
+    (conv(xg) * g.to(cuda_device)).sum().backward()
+    xd = x.double().requires_grad_(True)
+    wd = conv.weight.to_tensor().detach().cpu().to(torch.complex128).requires_grad_(True)
+    bd = conv.bias.detach().cpu().double().requires_grad_(True)
+    yd = R.spectral_conv_forward(xd, wd, bd, conv.n_modes, conv.max_n_modes, fft_norm=norm)
+    (yd * g.double()).sum().backward()
+    assert rel_err(xg.grad, xd.grad) <= TOL
+    assert rel_err(torch.view_as_real(conv.weight.to_tensor().grad), torch.view_as_real(wd.grad)) <= TOL
+    assert rel_err(conv.bias.grad, bd.grad) <= TOL
+
+
 @pytest.mark.parametrize("sizes,nm,kw", [
     ((32,), (9,), dict(output_shape=(64,))),                 # every bin incl. N//2, upsampled
     ((30,), (8,), dict(resolution_scaling_factor=0.5)),
