@@ -468,7 +468,8 @@ k_line_synth(const float2* __restrict__ xhat, const float2* __restrict__ w,
   const float g = skip_kind == FNO_SKIP_SOFT_GATING ? skip_w[o] : 1.f;
   const bool skip = skip_kind != FNO_SKIP_NONE;
   const uint32_t gmask = act_mask(act == FNO_ACT_GELU);
-  const float* xo = x + ((int64_t)b * Ci + o) * N + 64 * JH * half + lane;
+  // x rows exist for o < Ci only: the skips that read them have Ci == Co
+  const float* xo = skip ? x + ((int64_t)b * Ci + o) * N + 64 * JH * half + lane : x;
   float* yo = y + ((int64_t)b * Co + o) * N + 64 * JH * half + lane;
   float xs[JH];
   if (skip) {
