@@ -25,18 +25,27 @@ def _require_gpu(*tensors):
 
 
 def _ptr(t: Optional[torch.Tensor]):
-    """Device address of a tensor's data for the C-ABI.  The kernels read the
-    storage as it is, so a lazily conjugated or negated view (torch's conj /
-    neg bits, which leave the storage untouched) must have been resolved."""
+    """Device address of a tensor's data for the C-ABI (an int, which the
+    c_void_p arguments take as it is).  The kernels read the storage as it is,
+    so a lazily conjugated or negated view (torch's conj / neg bits, which
+    leave the storage untouched) must have been resolved."""
     if t is None:
-        return ctypes.c_void_p(0)
+        return None
     if t.is_conj() or t.is_neg():
         raise RuntimeError("internal: a conjugate / negative view reached the C-ABI unresolved")
-    return ctypes.c_void_p(t.data_ptr())
+    return t.data_ptr()
+
+
+# torch's current stream of a device as the raw hipStream_t, without building
+# a torch.cuda.Stream object per call (the public route below otherwise)
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
 def _stream(device):
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+    if _raw_stream is not None:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        return _raw_stream(idx)
+    return torch.cuda.current_stream(device).cuda_stream
 
 
 def _workspace(nbytes: int, device):
