@@ -946,6 +946,9 @@ static int c2c_axis_fwd(const float2* src, float2* dst, int64_t outer, int N, in
 bool axis_inv64_supported(int N, int Np, int m, int64_t inner);
 int axis_inv64(const float2* src, float2* dst, int64_t slabs, int m, int inner, float scale,
                hipStream_t st);
+bool axis_inv64x2_supported(int N0, int Np0, int m0, int N1, int Np1, int m1, int64_t inner);
+int axis_inv64x2(const float2* src, float2* dst, int64_t planes, int m0, int m1, int inner,
+                 float scale, hipStream_t st);
 
 static int c2c_axis_inv(const float2* src, float2* dst, int64_t outer, int N, int Np, int64_t inner,
                         int m, int off, float sc, hipStream_t st) {
@@ -1066,6 +1069,14 @@ static int inverse_nonlast(const float2* yhat, int64_t planes, int32_t ndim,
                            hipStream_t st) {
   float2* bufs[2] = {reinterpret_cast<float2*>(ws), reinterpret_cast<float2*>(ws) + eb};
   const float2* src = yhat;
+  // 3D, 64 x 64 leading axes: both in one pass, written where stage 1 writes
+  if (ndim == 3 && axis_inv64x2_supported(in_sizes[0], out_sizes[0], modes[0], in_sizes[1],
+                                          out_sizes[1], modes[1], modes[2])) {
+    const int rc = axis_inv64x2(yhat, bufs[1], planes, modes[0], modes[1], modes[2], 1.f, st);
+    if (rc) return rc;
+    *out = bufs[1];
+    return FNO_OK;
+  }
   for (int d = 0; d < ndim - 1; ++d) {
     int64_t outer = planes;
     for (int a = 0; a < d; ++a) outer *= out_sizes[a];

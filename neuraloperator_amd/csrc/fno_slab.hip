@@ -249,6 +249,144 @@ k_axis_inv64(const float2* __restrict__ src, float2* __restrict__ dst, int64_t s
   }
 }
 
+// ----------------------------------------------------------------------------
+// Inverse along the first two 64-point axes of a plane's window of m0 x m1
+// centred rows (m0, m1 <= 16) and inner <= 16 columns:
+//
+//   U[d0, j1, c] = sum_{j0 < m0} Y[j0, j1, c] e^{2 pi i (j0 - m0/2) d0 / 64}
+//   Z[d0, d1, c] = t sum_{j1 < m1} U[d0, j1, c] e^{2 pi i (j1 - m1/2) d1 / 64}
+//
+// (the first two ifftn axes of a 3D SpectralConv.forward inverse,
+// spectral_convolution.py:547-548).  A workgroup takes 16 values of d0 of one
+// plane: it loads the plane's window into LDS, forms U for its 16 d0 there as
+// a product on the matrix cores (the window expanded along the first axis
+// never goes through memory), and each wave runs k_axis_inv64's product on 4
+// of the 16 slabs.  Both products: three-term bf16 splits, fp32 accumulation.  The four
+// workgroups of a plane run on one XCD, so the window is fetched into one L2.
+constexpr int kInv2D0 = 16;   // values of d0 per workgroup
+
+__global__ void __launch_bounds__(sl::kThreads)
+k_axis_inv64x2(const float2* __restrict__ src, float2* __restrict__ dst, int64_t planes, int m0,
+               int m1, int inner, float scale) {
+  using namespace sl;
+  __shared__ float2 tw[kN];
+  // [ybig] the plane's window [m0][m1][inner], later the waves' output
+  // stages [kWaves][64 inner]; then U [kInv2D0][m1][inner]
+  extern __shared__ float4 dyn[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int G = lane >> 4, n = lane & 15;
+  // workgroup i -> plane 8 (i / 32) + i % 8, quarter (i / 8) % 4: consecutive
+  // workgroups go to consecutive XCDs, so the quarters of a plane share one
+  const int i = (int)blockIdx.x, k = i >> 3;
+  const int64_t p = (int64_t)(k >> 2) * 8 + (i & 7);
+  const int d0b = kInv2D0 * (k & 3);
+  if (p >= planes) return;
+  const int ul = m1 * inner, yl = m0 * ul;
+  const int ybig = yl > kWaves * 64 * inner ? yl : kWaves * 64 * inner;
+  float2* yb = reinterpret_cast<float2*>(dyn);
+  float2* ub = yb + ybig;
+  const float2* ys = src + p * yl;
+  for (int f = tid; f < yl; f += kThreads) yb[f] = ys[f];
+  if (tid < kN) tw[tid] = twiddle_any(tid, kN);
+  __syncthreads();
+  // U for d0 = d0b + dl as a product on the matrix cores: rows (dl, Re | Im)
+  // in two row tiles, K slot (G, e) = window row j0 = 4 G + e / 2 and Re / Im
+  // of Y (as in the second product), columns (j1, c) in tiles of 16
+  {
+    v8bf ah[2], al[2];
+#pragma unroll
+    for (int part = 0; part < 2; ++part) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int j = 4 * G + (e >> 1), cu = e & 1;
+        float v = 0.f;
+        if (j < m0) {
+          const float2 t = tw[((j - m0 / 2) * (d0b + n)) & (kN - 1)];
+          v = part == 0 ? (cu == 0 ? t.x : -t.y) : (cu == 0 ? t.y : t.x);
+        }
+        const bf2 q = split(v);
+        ah[part][e] = q.hi;
+        al[part][e] = q.lo;
+      }
+    }
+    const int ctiles = (ul + 15) / 16;
+#pragma unroll 1
+    for (int ct = wave; ct < ctiles; ct += kWaves) {
+      const int col = 16 * ct + n;
+      v8bf bh, bl;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int j = 4 * G + q;
+        const float2 yv = (j < m0 && col < ul) ? yb[j * ul + col] : make_float2(0.f, 0.f);
+        const bf2 a = split(yv.x), c = split(yv.y);
+        bh[2 * q] = a.hi;
+        bl[2 * q] = a.lo;
+        bh[2 * q + 1] = c.hi;
+        bl[2 * q + 1] = c.lo;
+      }
+      const v4f re = mma3(ah[0], al[0], bh, bl, (v4f)0.f);
+      const v4f im = mma3(ah[1], al[1], bh, bl, (v4f)0.f);
+      if (col < ul) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ub[(4 * G + r) * ul + col] = make_float2(re[r], im[r]);
+      }
+    }
+  }
+  __syncthreads();
+  // the second product's A fragments (as in k_axis_inv64, window rows j1) in
+  // registers: row tile rt = 2 t + part, rows d1 = 16 t + lane % 16
+  v8bf fh[8], fl[8];
+#pragma unroll
+  for (int rt = 0; rt < 8; ++rt) {
+    const int d = 16 * (rt >> 1) + n, part = rt & 1;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int j = 4 * G + (e >> 1), cu = e & 1;
+      float v = 0.f;
+      if (j < m1) {
+        const float2 t = tw[((j - m1 / 2) * d) & (kN - 1)];
+        v = part == 0 ? (cu == 0 ? t.x : -t.y) : (cu == 0 ? t.y : t.x);
+        v *= scale;
+      }
+      const bf2 q = split(v);
+      fh[rt][e] = q.hi;
+      fl[rt][e] = q.lo;
+    }
+  }
+  // the window is no longer read: its space holds the waves' output stages
+  float4* st4 = dyn + wave * 32 * inner;
+  float2* stw = reinterpret_cast<float2*>(st4);
+#pragma unroll 1
+  for (int dl = wave; dl < kInv2D0; dl += kWaves) {
+    const float2* us = ub + dl * ul;
+    v8bf bh, bl;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int j = 4 * G + q;
+      const float2 uv = (j < m1 && n < inner) ? us[j * inner + n] : make_float2(0.f, 0.f);
+      const bf2 a = split(uv.x), c = split(uv.y);
+      bh[2 * q] = a.hi;
+      bl[2 * q] = a.lo;
+      bh[2 * q + 1] = c.hi;
+      bl[2 * q + 1] = c.lo;
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      v4f re = (v4f)0.f, im = (v4f)0.f;
+      re = mma3(fh[2 * t], fl[2 * t], bh, bl, re);
+      im = mma3(fh[2 * t + 1], fl[2 * t + 1], bh, bl, im);
+      if (n < inner) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) stw[(16 * t + 4 * G + r) * inner + n] = make_float2(re[r], im[r]);
+      }
+    }
+    wave_sync();
+    float4* z4 = reinterpret_cast<float4*>(dst + ((p * kN) + d0b + dl) * kN * inner);
+    for (int q = lane; q < 32 * inner; q += 64) z4[q] = st4[q];
+    wave_sync();
+  }
+}
+
 // ============================================================== host side
 bool slab_fwd64_supported(int N1, int N2, int m1, int m2h) {
   return N1 == sl::kN && N2 == sl::kN && m1 >= 1 && m1 <= 16 && m2h >= 1 && m2h <= 16;
@@ -293,6 +431,29 @@ int axis_inv64(const float2* src, float2* dst, int64_t slabs, int m, int inner, 
                      (size_t)sl::kWaves * 32 * inner * sizeof(float4), st, src, dst, slabs,
                      m, inner, scale);
   return launch_status("k_axis_inv64");
+}
+
+bool axis_inv64x2_supported(int N0, int Np0, int m0, int N1, int Np1, int m1, int64_t inner) {
+  return N0 == sl::kN && Np0 == sl::kN && m0 >= 1 && m0 <= 16 &&
+         axis_inv64_supported(N1, Np1, m1, inner);
+}
+
+// [planes][m0][m1][inner] window -> [planes][64][64][inner], scaled by scale
+int axis_inv64x2(const float2* src, float2* dst, int64_t planes, int m0, int m1, int inner,
+                 float scale, hipStream_t st) {
+  const int64_t yl = (int64_t)m0 * m1 * inner, stg = (int64_t)sl::kWaves * 64 * inner;
+  const size_t lds = (size_t)((yl > stg ? yl : stg) + (int64_t)kInv2D0 * m1 * inner) * 8;
+  if (lds > 64 * 1024) {
+    int rc = hip_status(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_axis_inv64x2),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+                        "hipFuncSetAttribute(MaxDynamicSharedMemorySize)");
+    if (rc) return rc;
+  }
+  // planes rounded up to groups of 8 (one per XCD), four workgroups each
+  const int64_t grid = (planes + 7) / 8 * 8 * (sl::kN / kInv2D0);
+  hipLaunchKernelGGL(k_axis_inv64x2, dim3((unsigned)grid), dim3(sl::kThreads), lds, st, src, dst,
+                     planes, m0, m1, inner, scale);
+  return launch_status("k_axis_inv64x2");
 }
 
 }  // namespace fno

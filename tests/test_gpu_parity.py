@@ -1696,3 +1696,27 @@ def test_fused_1d_block(N, m, Ci, Co, skip, norm, cuda_device):
     ref = R.gelu(ref)
     err = rel_err(y, ref)
     assert err <= TOL, err
+
+
+@pytest.mark.parametrize("B,C,S,nm", [(1, 3, (64, 64, 8), (7, 16, 4)),
+                                      (2, 5, (64, 64, 64), (16, 11, 16)),
+                                      (1, 8, (64, 64, 12), (1, 1, 2))])
+def test_3d_leading_64x64_inverse_matches_oracle(B, C, S, nm, cuda_device):
+    """3D blocks whose first two axes are 64 points: their inverse runs as one
+    pass per plane (both axes expanded in LDS).  Plane counts that are not a
+    multiple of 8 leave some workgroups of the XCD-grouped grid idle; odd and
+    single-row windows.  Against the float64 oracle."""
+    print(f"3d leading 64x64 inverse B{B} C{C} {S} {nm}", flush=True)
+    torch.manual_seed(54)
+    conv = na.SpectralConv(C, C, nm).to(cuda_device)
+    with torch.no_grad():
+        conv.bias.normal_(0, 0.1)
+    g = torch.Generator().manual_seed(55)
+    x = torch.randn(B, C, *S, generator=g)
+    with torch.no_grad():
+        y = conv(x.to(cuda_device))
+    torch.cuda.synchronize()
+    w = conv.weight.to_tensor().detach().cpu().to(torch.complex128)
+    ref = R.spectral_conv_forward(x.double(), w, conv.bias.detach().cpu().double(), conv.n_modes,
+                                  conv.max_n_modes)
+    assert rel_err(y, ref) <= TOL
