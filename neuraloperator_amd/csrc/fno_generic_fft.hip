@@ -145,8 +145,10 @@ k_c2r_fft(const float2* __restrict__ in, float* __restrict__ out, const float* _
 
 // Non-last axis, complex <-> complex, one line per (outer o, inner q) at a
 // stride of `inner` entries.  A workgroup takes QB consecutive q of one o:
-// the [L][QB] tile moves through LDS with coalesced row accesses (stride TS >
-// QB against bank conflicts) and each line FFTs in its own tile column.
+// the [L][QB] tile moves through LDS with coalesced row accesses and each line
+// FFTs in its own tile column.  Row stride TS: with 8 lanes per line, 2 TS = 8
+// mod 64 dwords puts a line's 8 lanes on 8 distinct bank groups in every pass
+// of the strided FFT (TS = 40 put lanes t and t + 4 on the same banks).
 //   forward (SIGN -1): L = N input points; out[o][j][q] = s X[(j + off) mod N]
 //   inverse (SIGN +1): L = Np; window entry j goes to index (j + off) mod N
 //                      when that is < Np (zero-padding / truncation of the
@@ -159,7 +161,7 @@ k_c2c_fft_axis(const float2* __restrict__ in, float2* __restrict__ out, int64_t 
   using PL = LinePlan<L>;
   constexpr int T = PL::T, R = PL::R, Q = PL::Q;
   constexpr int QB = kFftThreads / T;
-  constexpr int TS = (QB == 32) ? 40 : QB + 1;
+  constexpr int TS = (QB == 32) ? 36 : QB + 1;
   extern __shared__ float4 smem4[];
   float2* tw = reinterpret_cast<float2*>(smem4);
   float2* tile = tw + L;   // [L][TS]
@@ -274,7 +276,7 @@ template <int L, int SIGN>
 static int launch_c2c(const float2* in, float2* out, int64_t outer, int64_t inner, int N, int m,
                       int off, float scale, hipStream_t st) {
   constexpr int QB = kFftThreads / LinePlan<L>::T;
-  constexpr int TS = (QB == 32) ? 40 : QB + 1;
+  constexpr int TS = (QB == 32) ? 36 : QB + 1;
   const size_t lds = (size_t)(L + L * TS) * sizeof(float2);
   const int64_t blocks = outer * ((inner + QB - 1) / QB);
   hipLaunchKernelGGL((k_c2c_fft_axis<L, SIGN>), dim3((unsigned)blocks), dim3(kFftThreads), lds,
